@@ -1,0 +1,160 @@
+"""Dual-stream masking (drop-in for alodlm/batch.py).
+
+``build_batch`` keeps the reference's random-number consumption exactly
+(alodlm/batch.py:50-60: per segment one ``uniform_`` of ceil(L/B) floats, then
+one ``randperm`` per block whose masked count round(n*p) is nonzero, all from
+the default generator of the ids' device) and hands the draws to the HIP
+kernel ``alodlm_batch_build``, which writes every dual-stream row.  Masks and
+orders are therefore bit-identical to the reference's for the same generator
+state.  The attention mask is never materialised on the GPU: the attention
+kernels enumerate the closed-form mask from the segment boundaries.
+"""
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import plan_to_device, sparse_plan
+
+
+@dataclass
+class Batch:
+    """Dual-stream rows of one pack (fields of alodlm/batch.py:12-20).
+
+    ``attention_mask`` is the string ``"dual-stream"`` (the kernels derive the
+    mask from ``boundaries``) unless a dense mask or a range plan was requested.
+    ``row_segment`` and ``ar_target`` are the per-row segment index and
+    next-token target the step kernels use.
+    """
+    ids: torch.Tensor
+    original: torch.Tensor
+    positions: torch.Tensor
+    masked: torch.Tensor
+    mask_probability: torch.Tensor
+    boundaries: torch.Tensor
+    attention_mask: object
+    row_segment: torch.Tensor = None
+    ar_target: torch.Tensor = None
+    ar_count: int = 0
+    pairs: int = 0
+
+
+def allowed_pairs(length, block_size):
+    """Number of (query, key) pairs the dual-stream mask allows in one segment:
+    the causal clean stream plus, per noisy block, its causal self-block and
+    the clean rows of all earlier blocks."""
+    total = length * (length + 1) // 2
+    for left in range(0, length, block_size):
+        width = min(block_size, length - left)
+        total += width * (width + 1) // 2 + width * left
+    return total
+
+
+def attention_mask(length, block_size, device):
+    """Dense dual-stream mask of one segment (closed form of alodlm/batch.py:23-31)."""
+    q = torch.arange(2 * length, device=device)[:, None]
+    k = torch.arange(2 * length, device=device)[None, :]
+    q_noisy, k_noisy = q >= length, k >= length
+    q_block = torch.where(q_noisy, q - length, q) // block_size
+    k_block = torch.where(k_noisy, k - length, k) // block_size
+    return ((q_block == k_block) & (q_noisy == k_noisy) & (k <= q)) | ((k_block < q_block) & ~k_noisy)
+
+
+def draw_masking(labels_host, offsets, block_size, device, generator=None):
+    """Draw the masking randomness in the reference's order.
+
+    Returns per-block arrays (p, count) on the host and the list of per-block
+    permutations (device tensors, or None where count is zero).
+    """
+    probs, counts, perms = [], [], []
+    for a, b in zip(offsets, offsets[1:]):
+        length = b - a
+        nblocks = (length + block_size - 1) // block_size
+        u = torch.empty(nblocks, device=device).uniform_(0, 1, generator=generator).clamp_min(1e-8)
+        u_host = u.tolist()
+        seg_labels = labels_host[a:b]
+        for blk in range(nblocks):
+            left = blk * block_size
+            n = int((seg_labels[left:left + block_size] != -100).sum())
+            count = round(n * u_host[blk])
+            probs.append(u_host[blk])
+            counts.append(count)
+            perms.append(torch.randperm(n, device=device, generator=generator) if count else None)
+    return np.asarray(probs, dtype=np.float32), np.asarray(counts, dtype=np.int32), perms
+
+
+@torch.no_grad()
+def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdpa",
+                generator=None, draws=None):
+    """Dual-stream batch of one pack (alodlm/batch.py:34-85) on the GPU.
+
+    ``backend`` is accepted for API compatibility; the attention kernels read the
+    mask from the boundaries whatever its value.  ``draws`` (p, counts, perms)
+    may be supplied to replay known randomness.
+    """
+    if ids.ndim != 1 or ids.shape != labels.shape or ids.numel() == 0:
+        raise ValueError("Expected nonempty flat input and label tensors")
+    offsets = [int(v) for v in boundaries.tolist()]
+    if offsets[0] != 0 or offsets[-1] != len(ids):
+        raise ValueError("Boundaries must cover the packed tokens")
+    if any(a >= b for a, b in zip(offsets, offsets[1:])):
+        raise ValueError("Packed segments must be nonempty")
+    if block_size < 1 or block_size > 1024:
+        raise ValueError("block_size must be in [1, 1024]")
+    device = ids.device
+    if device.type != "cuda":
+        raise ValueError("build_batch runs on the GPU; move ids/labels to a CUDA device")
+    labels_host = labels.detach().cpu().numpy()
+    if draws is None:
+        draws = draw_masking(labels_host, offsets, block_size, device, generator)
+    probs, counts, perms = draws
+    nseg = len(offsets) - 1
+    seg_block = [0]
+    for a, b in zip(offsets, offsets[1:]):
+        seg_block.append(seg_block[-1] + (b - a + block_size - 1) // block_size)
+    nblocks = seg_block[-1]
+    perm_offset = np.zeros(nblocks, dtype=np.int64)
+    chunks, total = [], 0
+    for i, perm in enumerate(perms):
+        perm_offset[i] = total
+        if perm is not None:
+            chunks.append(perm.to(device=device, dtype=torch.int64))
+            total += perm.numel()
+    perm_buf = torch.cat(chunks) if chunks else torch.zeros(1, dtype=torch.int64, device=device)
+    ids = ids.to(torch.int64).contiguous()
+    labels = labels.to(torch.int64).contiguous()
+    n = 2 * len(ids)
+    to_dev = lambda a: torch.from_numpy(a).to(device, non_blocking=False)
+    seg_t = torch.tensor(offsets, dtype=torch.int64, device=device)
+    seg_block_t = torch.tensor(seg_block, dtype=torch.int32, device=device)
+    p_t, c_t, po_t = to_dev(probs), to_dev(counts), to_dev(perm_offset)
+    out = {
+        "ids": torch.empty(n, dtype=torch.int64, device=device),
+        "original": torch.empty(n, dtype=torch.int64, device=device),
+        "positions": torch.empty(n, dtype=torch.int64, device=device),
+        "masked": torch.empty(n, dtype=torch.bool, device=device),
+        "prob": torch.empty(n, dtype=torch.float32, device=device),
+        "row_segment": torch.empty(n, dtype=torch.int32, device=device),
+        "ar_target": torch.empty(n, dtype=torch.int32, device=device),
+        "bounds": torch.empty(nseg + 1, dtype=torch.int64, device=device),
+    }
+    _lib.call("alodlm_batch_build", _lib.ptr(ids), _lib.ptr(labels), _lib.ptr(seg_t),
+              _lib.ptr(seg_block_t), nseg, nblocks, block_size, mask_token_id, _lib.ptr(p_t),
+              _lib.ptr(c_t), _lib.ptr(po_t), _lib.ptr(perm_buf), _lib.ptr(out["ids"]),
+              _lib.ptr(out["original"]), _lib.ptr(out["positions"]), _lib.ptr(out["masked"]),
+              _lib.ptr(out["prob"]), _lib.ptr(out["row_segment"]), _lib.ptr(out["ar_target"]),
+              _lib.ptr(out["bounds"]), _lib.stream_handle(device))
+    # number of autoregressive targets (alodlm/loss.py:21-29), from the host labels
+    ar_count = 0
+    for a, b in zip(offsets, offsets[1:]):
+        if b - a >= 2:
+            ar_count += int((labels_host[a + 1:b] != -100).sum())
+    if backend == "sdpa":
+        mask = "dual-stream"
+    else:
+        mask = plan_to_device(sparse_plan([2 * v for v in offsets], block_size, backend), device)
+    pairs = sum(allowed_pairs(b - a, block_size) for a, b in zip(offsets, offsets[1:]))
+    return Batch(out["ids"], out["original"], out["positions"], out["masked"], out["prob"],
+                 out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count, pairs)

@@ -1,0 +1,168 @@
+// Shared device helpers for the ALoDLM gfx950 kernels.
+//
+// Storage types: float (dtype code 0) and bfloat16 held as uint16_t (dtype
+// code 1).  All arithmetic is float32; bf16 results are rounded to nearest
+// even exactly once per reference rounding point, so that bf16 runs follow
+// the reference's bf16 eager rounding sequence.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/alodlm_hip.h"
+
+typedef uint16_t bf16_t;
+
+#define ALODLM_WAVE 64
+
+// ----------------------------------------------------------------------------
+// bf16 <-> float
+// ----------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float bf16_to_float(bf16_t h) {
+  union { uint32_t u; float f; } v;
+  v.u = (uint32_t)h << 16;
+  return v.f;
+}
+
+__host__ __device__ __forceinline__ bf16_t float_to_bf16(float f) {
+  union { uint32_t u; float f; } v;
+  v.f = f;
+  if ((v.u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((v.u >> 16) | 0x40);  // quiet NaN
+  uint32_t rounding = 0x7fffu + ((v.u >> 16) & 1u);
+  return (bf16_t)((v.u + rounding) >> 16);
+}
+
+// Round a float to the nearest bf16 value and return it as float.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_float(float_to_bf16(f)); }
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+  // Rounding to the storage precision (identity for float).
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+template <> struct Elem<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) { return bf16_to_float(p[i]); }
+  static __device__ __forceinline__ void store(bf16_t* p, int64_t i, float v) { p[i] = float_to_bf16(v); }
+  static __device__ __forceinline__ float round(float v) { return round_bf16(v); }
+};
+
+// ----------------------------------------------------------------------------
+// Wavefront / block reductions (64-wide wavefronts)
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over the whole block; every thread gets the result.  `scratch` must
+// hold blockDim.x/64 floats.  Deterministic (fixed tree order).
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.f;
+  for (int w = 0; w < nwaves; ++w) total += scratch[w];
+  return total;
+}
+
+__device__ __forceinline__ float block_max(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = -INFINITY;
+  for (int w = 0; w < nwaves; ++w) total = fmaxf(total, scratch[w]);
+  return total;
+}
+
+__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// softplus(x) = log(1 + exp(x)) with torch's threshold of 20.
+__device__ __forceinline__ float softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// ----------------------------------------------------------------------------
+// Host-side error plumbing (defined in abi.hip)
+// ----------------------------------------------------------------------------
+int alodlm_set_error(int code, const char* fmt, ...);
+
+#define ALODLM_CHECK_ARG(cond, ...)                                  \
+  do {                                                               \
+    if (!(cond)) return alodlm_set_error(ALODLM_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define ALODLM_CHECK_LAUNCH(name)                                                   \
+  do {                                                                              \
+    hipError_t _e = hipGetLastError();                                              \
+    if (_e != hipSuccess)                                                           \
+      return alodlm_set_error(ALODLM_EHIP, "%s: %s", name, hipGetErrorString(_e));  \
+  } while (0)
+
+static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+// ----------------------------------------------------------------------------
+// 8-element vector access (16 bytes of bf16 or 32 bytes of float).  The
+// pointer must be aligned to 8 elements.
+// ----------------------------------------------------------------------------
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16_t> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float* v) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_to_float((bf16_t)(w[i] & 0xffffu));
+      v[2 * i + 1] = bf16_to_float((bf16_t)(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)float_to_bf16(v[2 * i]) | ((uint32_t)float_to_bf16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float* v) {
+    float4 a = reinterpret_cast<const float4*>(p)[0];
+    float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float* v) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+static inline bool aligned8(const void* p, int dtype) {
+  return (reinterpret_cast<uintptr_t>(p) % (dtype == ALODLM_BF16 ? 16 : 32)) == 0;
+}
+
+// Dispatch a templated launcher over the storage type.
+#define ALODLM_DISPATCH(dtype, T, ...)                                        \
+  do {                                                                        \
+    if ((dtype) == ALODLM_F32) { typedef float T; __VA_ARGS__; }              \
+    else if ((dtype) == ALODLM_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
+    else return alodlm_set_error(ALODLM_EINVAL, "unknown dtype %d", (int)(dtype)); \
+  } while (0)

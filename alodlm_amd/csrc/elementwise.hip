@@ -1,0 +1,134 @@
+// Embedding gather / scatter-add, SwiGLU, and small elementwise helpers.
+#include "common.h"
+
+// out[r] = table[ids[r]]   ([tf] modeling_qwen3.py:352; alodlm/model.py:133,149)
+// An id outside [0, vocab) yields a NaN row instead of an out-of-bounds read.
+template <typename T>
+__global__ void embed_gather_kernel(const T* __restrict__ table, const int64_t* __restrict__ ids,
+                                    T* __restrict__ out, int64_t rows, int64_t H, int64_t vocab) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * H) return;
+  const int64_t r = i / H, c = i % H;
+  const int64_t id = ids[r];
+  if (id < 0 || id >= vocab) Elem<T>::store(out, i, NAN);
+  else out[i] = table[id * H + c];
+}
+
+// dtable[ids[r]] += dout[r] (float accumulate) for rows with
+// row_exits == NULL or row_exits[r] <= max_exit.  One wavefront per row.
+template <typename T>
+__global__ void embed_scatter_kernel(const T* __restrict__ dout, const int64_t* __restrict__ ids,
+                                     const int32_t* __restrict__ row_exits, int64_t max_exit,
+                                     float* __restrict__ dtable, int64_t rows, int64_t H,
+                                     int64_t vocab) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  if (row_exits && row_exits[r] > max_exit) return;
+  if (ids[r] < 0 || ids[r] >= vocab) return;
+  float* dst = dtable + ids[r] * H;
+  const T* src = dout + r * H;
+  for (int64_t c = lane; c < H; c += 64) atomicAdd(dst + c, Elem<T>::load(src, c));
+}
+
+// act = cast(cast(silu(gate)) * up)   ([tf] modeling_qwen3.py:81-83)
+template <typename T>
+__global__ void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ act, int64_t rows,
+                                  int64_t I) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * I) return;
+  const int64_t r = i / I, c = i % I;
+  const float g = Elem<T>::load(gu, r * 2 * I + c);
+  const float u = Elem<T>::load(gu, r * 2 * I + I + c);
+  const float s = Elem<T>::round(g / (1.0f + expf(-g)));
+  Elem<T>::store(act, i, s * u);
+}
+
+// dgate = dact * up * silu'(gate), dup = dact * silu(gate)
+template <typename T>
+__global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restrict__ gu,
+                                  T* __restrict__ dgu, int64_t rows, int64_t I) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * I) return;
+  const int64_t r = i / I, c = i % I;
+  const float g = Elem<T>::load(gu, r * 2 * I + c);
+  const float u = Elem<T>::load(gu, r * 2 * I + I + c);
+  const float da = Elem<T>::load(dact, i);
+  const float sg = 1.0f / (1.0f + expf(-g));
+  const float silu = Elem<T>::round(g * sg);
+  Elem<T>::store(dgu, r * 2 * I + c, da * u * (sg * (1.0f + g * (1.0f - sg))));
+  Elem<T>::store(dgu, r * 2 * I + I + c, da * silu);
+}
+
+template <typename T>
+__global__ void cast_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) Elem<T>::store(dst, i, src[i]);
+}
+
+__global__ void scale_kernel(float* __restrict__ x, const float* __restrict__ s, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] *= s[0];
+}
+
+extern "C" int alodlm_embed_gather(const void* table, const int64_t* ids, void* out, int64_t rows,
+                                   int64_t hidden, int64_t vocab, int dtype, void* stream) {
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    embed_gather_kernel<T><<<ceil_div_u(rows * hidden, 256), 256, 0, as_stream(stream)>>>(
+        (const T*)table, ids, (T*)out, rows, hidden, vocab);
+  });
+  ALODLM_CHECK_LAUNCH("embed_gather");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_embed_scatter_add(const void* dout, const int64_t* ids,
+                                        const int32_t* row_exits, int64_t max_exit, float* dtable,
+                                        int64_t rows, int64_t hidden, int64_t vocab, int dtype,
+                                        void* stream) {
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    embed_scatter_kernel<T><<<ceil_div_u(rows, 4), 256, 0, as_stream(stream)>>>(
+        (const T*)dout, ids, row_exits, max_exit, dtable, rows, hidden, vocab);
+  });
+  ALODLM_CHECK_LAUNCH("embed_scatter_add");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_t inter, int dtype,
+                                 void* stream) {
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    swiglu_fwd_kernel<T><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
+        (const T*)gu, (T*)act, rows, inter);
+  });
+  ALODLM_CHECK_LAUNCH("swiglu_fwd");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, int64_t rows,
+                                 int64_t inter, int dtype, void* stream) {
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    swiglu_bwd_kernel<T><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
+        (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
+  });
+  ALODLM_CHECK_LAUNCH("swiglu_bwd");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_cast_f32(const float* src, void* dst, int64_t n, int dtype, void* stream) {
+  if (n == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    cast_kernel<T><<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(src, (T*)dst, n);
+  });
+  ALODLM_CHECK_LAUNCH("cast_f32");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream) {
+  if (n == 0) return ALODLM_OK;
+  scale_kernel<<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(x, scale, n);
+  ALODLM_CHECK_LAUNCH("scale_f32");
+  return ALODLM_OK;
+}

@@ -1,0 +1,118 @@
+// Gradient clipping and AdamW over a list of tensors
+// (torch.nn.utils.clip_grad_norm_ and torch.optim.AdamW as called at
+// alodlm/train.py:49,140,143).
+//
+// The tensor list is cut into fixed-size chunks on the host once; chunk c
+// covers elements [chunk_start[c], chunk_start[c] + chunk_size) of tensor
+// chunk_tensor[c].  Both kernels walk that table, so a 311M-element embedding
+// and a 128-element norm weight are handled by the same launch.  AdamW keeps a
+// float master copy, first and second moments per tensor (HBM traffic per
+// element: grad + master r/w + m r/w + v r/w + param w).
+#include "common.h"
+
+#define OPT_THREADS 256
+
+template <typename T>
+__global__ void __launch_bounds__(OPT_THREADS)
+grad_sumsq_kernel(const void* const* __restrict__ grads, const int32_t* __restrict__ chunk_tensor,
+                  const int64_t* __restrict__ chunk_start, const int64_t* __restrict__ numels,
+                  int64_t chunk_size, float* __restrict__ partial) {
+  __shared__ float scratch[OPT_THREADS / 64];
+  const int64_t c = blockIdx.x;
+  const int32_t t = chunk_tensor[c];
+  const T* g = reinterpret_cast<const T*>(grads[t]);
+  const int64_t beg = chunk_start[c];
+  const int64_t end = beg + chunk_size < numels[t] ? beg + chunk_size : numels[t];
+  float s = 0.f;
+  for (int64_t i = beg + threadIdx.x; i < end; i += OPT_THREADS) {
+    const float v = Elem<T>::load(g, i);
+    s += v * v;
+  }
+  s = block_sum(s, scratch);
+  if (threadIdx.x == 0) partial[c] = s;
+}
+
+__global__ void __launch_bounds__(1024)
+final_norm_kernel(const float* __restrict__ partial, int64_t n, float* __restrict__ total) {
+  __shared__ float scratch[16];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += partial[i];
+  s = block_sum(s, scratch);
+  if (threadIdx.x == 0) total[0] = sqrtf(s);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(OPT_THREADS)
+adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master,
+             float* const* __restrict__ exp_avg, float* const* __restrict__ exp_avg_sq,
+             const void* const* __restrict__ grads, const int32_t* __restrict__ chunk_tensor,
+             const int64_t* __restrict__ chunk_start, const int64_t* __restrict__ numels,
+             const float* __restrict__ weight_decay, int64_t chunk_size,
+             const float* __restrict__ total_norm, float max_norm, float lr, float beta1,
+             float beta2, float eps, float step_size, float bc2_sqrt) {
+  const int64_t c = blockIdx.x;
+  const int32_t t = chunk_tensor[c];
+  const int64_t beg = chunk_start[c];
+  const int64_t end = beg + chunk_size < numels[t] ? beg + chunk_size : numels[t];
+  float clip = 1.0f;
+  if (total_norm) clip = fminf(1.0f, max_norm / (total_norm[0] + 1e-6f));
+  const float decay = 1.0f - lr * weight_decay[t];
+  T* p = reinterpret_cast<T*>(params[t]);
+  float* w = master[t];
+  float* m = exp_avg[t];
+  float* v = exp_avg_sq[t];
+  const T* g = reinterpret_cast<const T*>(grads[t]);
+  const bool separate = reinterpret_cast<void*>(w) != reinterpret_cast<void*>(p);
+  for (int64_t i = beg + threadIdx.x; i < end; i += OPT_THREADS) {
+    const float gi = Elem<T>::load(g, i) * clip;
+    float wi = w[i] * decay;
+    float mi = m[i];
+    mi = mi + (1.0f - beta1) * (gi - mi);
+    float vi = v[i] * beta2 + (1.0f - beta2) * gi * gi;
+    const float denom = sqrtf(vi) / bc2_sqrt + eps;
+    wi = wi - step_size * (mi / denom);
+    m[i] = mi;
+    v[i] = vi;
+    w[i] = wi;
+    if (separate) Elem<T>::store(p, i, wi);
+  }
+}
+
+extern "C" int alodlm_grad_norm(const void* const* grads, const int32_t* chunk_tensor,
+                                const int64_t* chunk_start, const int64_t* numels,
+                                int64_t n_chunks, int64_t chunk_size, int dtype, float* partial,
+                                float* total_norm, void* stream) {
+  ALODLM_CHECK_ARG(n_chunks > 0 && chunk_size > 0, "grad_norm: empty tensor list");
+  hipStream_t st = as_stream(stream);
+  ALODLM_DISPATCH(dtype, T, {
+    grad_sumsq_kernel<T><<<(unsigned)n_chunks, OPT_THREADS, 0, st>>>(
+        grads, chunk_tensor, chunk_start, numels, chunk_size, partial);
+  });
+  ALODLM_CHECK_LAUNCH("grad_sumsq");
+  final_norm_kernel<<<1, 1024, 0, st>>>(partial, n_chunks, total_norm);
+  ALODLM_CHECK_LAUNCH("grad_norm_final");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_adamw(void* const* params, float* const* master, float* const* exp_avg,
+                            float* const* exp_avg_sq, const void* const* grads,
+                            const int32_t* chunk_tensor, const int64_t* chunk_start,
+                            const int64_t* numels, const float* weight_decay, int64_t n_chunks,
+                            int64_t chunk_size, const float* total_norm, float max_norm, float lr,
+                            float beta1, float beta2, float eps, int64_t step, int dtype,
+                            void* stream) {
+  ALODLM_CHECK_ARG(n_chunks > 0 && chunk_size > 0, "adamw: empty tensor list");
+  ALODLM_CHECK_ARG(step >= 1, "adamw: step must be >= 1");
+  const double bc1 = 1.0 - pow((double)beta1, (double)step);
+  const double bc2 = 1.0 - pow((double)beta2, (double)step);
+  const float step_size = (float)((double)lr / bc1);
+  const float bc2_sqrt = (float)sqrt(bc2);
+  ALODLM_DISPATCH(dtype, T, {
+    adamw_kernel<T><<<(unsigned)n_chunks, OPT_THREADS, 0, as_stream(stream)>>>(
+        params, master, exp_avg, exp_avg_sq, grads, chunk_tensor, chunk_start, numels,
+        weight_decay, chunk_size, total_norm, max_norm, lr, beta1, beta2, eps, step_size,
+        bc2_sqrt);
+  });
+  ALODLM_CHECK_LAUNCH("adamw");
+  return ALODLM_OK;
+}

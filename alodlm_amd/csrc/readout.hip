@@ -1,0 +1,432 @@
+// Readout side of each recurrent depth: the final norm fused with the gate
+// head, the carry norm fused with re-embedding, exit sampling, the selection
+// of loss-bearing rows, and the vocabulary cross-entropy.
+#include "common.h"
+
+#define RO_WAVES 4
+
+// readout = norm(x); gate = cast(cast(readout.w + b) + depth_bias[d])
+// (alodlm/model.py:160-162 and GateHead.forward :37-38).
+template <typename T>
+__global__ void __launch_bounds__(64 * RO_WAVES)
+final_norm_gate_kernel(const T* __restrict__ x, const T* __restrict__ wf, const T* __restrict__ gw,
+                       const T* __restrict__ gb, const T* __restrict__ db, int64_t depth,
+                       T* __restrict__ readout, float* __restrict__ rstd, float* __restrict__ gate,
+                       int64_t rows, int64_t H, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * RO_WAVES + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * H;
+  T* yr = readout + row * H;
+  float ss = 0.f;
+  for (int64_t c = lane; c < H; c += 64) {
+    float v = Elem<T>::load(xr, c);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  float dot = 0.f;
+  for (int64_t c = lane; c < H; c += 64) {
+    float y = Elem<T>::round(Elem<T>::load(wf, c) * Elem<T>::round(Elem<T>::load(xr, c) * r));
+    Elem<T>::store(yr, c, y);
+    dot += y * Elem<T>::load(gw, c);
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) {
+    rstd[row] = r;
+    float g = Elem<T>::round(dot + Elem<T>::load(gb, 0));
+    gate[row] = Elem<T>::round(g + Elem<T>::load(db, depth));
+  }
+}
+
+// out = exits <= d ? table[original] : norm(x)   (model.py:153-154,168)
+template <typename T>
+__global__ void __launch_bounds__(64 * RO_WAVES)
+carry_select_kernel(const T* __restrict__ x, const T* __restrict__ wf, const T* __restrict__ table,
+                    const int64_t* __restrict__ original, const int32_t* __restrict__ exits,
+                    int64_t depth, T* __restrict__ out, float* __restrict__ rstd, int64_t rows,
+                    int64_t H, float eps, int64_t vocab) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * RO_WAVES + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * H;
+  T* yr = out + row * H;
+  float ss = 0.f;
+  for (int64_t c = lane; c < H; c += 64) {
+    float v = Elem<T>::load(xr, c);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  if (lane == 0) rstd[row] = r;
+  if (exits[row] <= depth) {
+    const int64_t id = original[row];
+    if (id < 0 || id >= vocab) {
+      for (int64_t c = lane; c < H; c += 64) Elem<T>::store(yr, c, NAN);
+    } else {
+      const T* er = table + id * H;
+      for (int64_t c = lane; c < H; c += 64) yr[c] = er[c];
+    }
+  } else {
+    for (int64_t c = lane; c < H; c += 64)
+      Elem<T>::store(yr, c, Elem<T>::load(wf, c) * Elem<T>::round(Elem<T>::load(xr, c) * r));
+  }
+}
+
+__global__ void exit_update_kernel(const float* __restrict__ gate, const float* __restrict__ u,
+                                   const uint8_t* __restrict__ masked, int32_t* __restrict__ exits,
+                                   int32_t depth, int32_t K, int64_t rows) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float hazard = sigmoidf_ref(gate[r]);
+  if (u[r] < hazard && masked[r] && exits[r] == K) exits[r] = depth + 1;
+}
+
+__global__ void __launch_bounds__(1024)
+inverse_weight_sum_kernel(const uint8_t* __restrict__ masked, const float* __restrict__ p,
+                          int64_t rows, float* __restrict__ out) {
+  __shared__ float scratch[16];
+  float s = 0.f;
+  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x)
+    if (masked[r]) s += 1.0f / (p[r] + 1e-8f);
+  s = block_sum(s, scratch);
+  if (threadIdx.x == 0) out[0] = s;
+}
+
+// Stable compaction of the loss-bearing rows of depth d with their targets and
+// dL/dce coefficients (loss.py:55-61 for masked rows; loss.py:12-32 and
+// model.py:183-185 for the autoregressive rows).
+__global__ void __launch_bounds__(1024)
+select_rows_kernel(const uint8_t* __restrict__ masked, const int32_t* __restrict__ exits,
+                   const int64_t* __restrict__ original, const int32_t* __restrict__ ar_target,
+                   const float* __restrict__ gates, const float* __restrict__ mask_prob,
+                   const float* __restrict__ wsum, float ar_coef, int32_t depth, int32_t K,
+                   int64_t rows, int32_t* __restrict__ sel_rows, int32_t* __restrict__ sel_target,
+                   float* __restrict__ sel_coef, int32_t* __restrict__ sel_count) {
+  __shared__ int32_t wave_counts[16];
+  __shared__ int32_t base;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  if (threadIdx.x == 0) base = 0;
+  __syncthreads();
+  const float inv_wsum = 1.0f / wsum[0];
+  for (int64_t start = 0; start < rows; start += blockDim.x) {
+    const int64_t r = start + threadIdx.x;
+    int take = 0, target = -1;
+    float coef = 0.f;
+    if (r < rows) {
+      if (masked[r] && exits[r] > depth) {
+        take = 1;
+        target = (int)original[r];
+        float log_surv = 0.f;
+        for (int j = 0; j < depth; ++j) log_surv -= softplusf(gates[(int64_t)j * rows + r]);
+        const bool last = exits[r] == depth + 1 || depth == K - 1;
+        const float log_stick =
+            last ? log_surv : log_surv - softplusf(-gates[(int64_t)depth * rows + r]);
+        const float w = (1.0f / (mask_prob[r] + 1e-8f)) * inv_wsum;
+        coef = 0.5f * w * expf(log_stick);
+      } else if (ar_target[r] >= 0) {
+        take = 1;
+        target = ar_target[r];
+        coef = ar_coef;
+      }
+    }
+    const uint64_t ballot = __ballot(take);
+    const int prefix = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_counts[wave] = __popcll(ballot);
+    __syncthreads();
+    int offset = base;
+    for (int w = 0; w < wave; ++w) offset += wave_counts[w];
+    if (take) {
+      sel_rows[offset + prefix] = (int32_t)r;
+      sel_target[offset + prefix] = target;
+      sel_coef[offset + prefix] = coef;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int total = 0;
+      for (int w = 0; w < nwaves; ++w) total += wave_counts[w];
+      base += total;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sel_count[0] = base;
+}
+
+template <typename T>
+__global__ void gather_rows_kernel(const T* __restrict__ src, const int32_t* __restrict__ sel,
+                                   int64_t n, T* __restrict__ dst, int64_t H) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * H) return;
+  const int64_t j = i / H, c = i % H;
+  dst[i] = src[(int64_t)sel[j] * H + c];
+}
+
+template <typename T>
+__global__ void zero_kernel(T* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = (T)0;
+}
+
+template <typename T>
+__global__ void scatter_rows_kernel(const T* __restrict__ src, const int32_t* __restrict__ sel,
+                                    int64_t n, T* __restrict__ dst, int64_t H) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * H) return;
+  const int64_t j = i / H, c = i % H;
+  dst[(int64_t)sel[j] * H + c] = src[i];
+}
+
+// ce = lse - logit[target] (rounded like the reference's CE output),
+// entropy = lse - sum p*logit, logits <- coef*(softmax - onehot).
+template <typename T, bool V8>
+__global__ void __launch_bounds__(256)
+cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
+                     const float* __restrict__ coef, const int32_t* __restrict__ n_rows,
+                     int64_t V, float* __restrict__ ce, float* __restrict__ entropy) {
+  __shared__ float sm[4], ss[4], st[4];
+  const int64_t row = blockIdx.x;
+  if (row >= n_rows[0]) return;
+  T* lr = logits + row * V;
+  float m = -INFINITY, s = 0.f, t = 0.f;
+  auto add = [&](float x) {
+    if (x > m) {
+      const float scale = expf(m - x);
+      s = s * scale + 1.f;
+      t = t * scale + x;
+      m = x;
+    } else {
+      const float e = expf(x - m);
+      s += e;
+      t += e * x;
+    }
+  };
+  if (V8) {
+    for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
+      float v[8];
+      Vec8<T>::load(lr + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) add(v[i]);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < V; c += 256) add(Elem<T>::load(lr, c));
+  }
+  // combine (m, s, t) across the block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float M = wave_max(m);
+  float scale = (m == -INFINITY) ? 0.f : expf(m - M);
+  float S = wave_sum(s * scale), Tt = wave_sum(t * scale);
+  if (lane == 0) { sm[wave] = M; ss[wave] = S; st[wave] = Tt; }
+  __syncthreads();
+  float gm = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  float gs = 0.f, gt = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = (sm[w] == -INFINITY) ? 0.f : expf(sm[w] - gm);
+    gs += ss[w] * f;
+    gt += st[w] * f;
+  }
+  const float lse = gm + logf(gs);
+  int tg = target[row];
+  const float cf = coef[row];
+  const bool valid = tg >= 0 && tg < V;  // an out-of-range target yields NaN, never a read
+  if (threadIdx.x == 0) {
+    const float xt = valid ? Elem<T>::load(lr, tg) : NAN;
+    ce[row] = Elem<T>::round(lse - xt);
+    if (entropy) entropy[row] = lse - gt / gs;
+  }
+  if (!valid) tg = -1;
+  __syncthreads();  // the target logit is read above before it is overwritten
+  if (V8) {
+    for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
+      float v[8];
+      Vec8<T>::load(lr + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = cf * (expf(v[i] - lse) - (c + i == tg ? 1.f : 0.f));
+      Vec8<T>::store(lr + c, v);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < V; c += 256) {
+      const float v = Elem<T>::load(lr, c);
+      Elem<T>::store(lr, c, cf * (expf(v - lse) - (c == tg ? 1.f : 0.f)));
+    }
+  }
+}
+
+__global__ void scatter_ce_kernel(const float* __restrict__ ce, const int32_t* __restrict__ sel,
+                                  const int32_t* __restrict__ n_rows, int64_t max_rows,
+                                  float* __restrict__ ce_full) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= max_rows || j >= n_rows[0]) return;
+  ce_full[sel[j]] = ce[j];
+}
+
+// partial[blk, 0:H] = sum_r dgate[r]*readout[r]; partial[blk, H] = sum_r dgate[r]
+template <typename T>
+__global__ void __launch_bounds__(64)
+gate_bwd_kernel(const float* __restrict__ dgate, const T* __restrict__ readout,
+                float* __restrict__ partial, int64_t rows, int64_t H, int64_t rows_per_block) {
+  extern __shared__ float acc[];
+  const int lane = threadIdx.x;
+  for (int64_t c = lane; c <= H; c += 64) acc[c] = 0.f;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+  float gsum = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float g = dgate[r];
+    if (g == 0.f) continue;
+    gsum += g;
+    for (int64_t c = lane; c < H; c += 64) acc[c] += g * Elem<T>::load(readout + r * H, c);
+  }
+  for (int64_t c = lane; c < H; c += 64) partial[(int64_t)blockIdx.x * (H + 1) + c] = acc[c];
+  if (lane == 0) partial[(int64_t)blockIdx.x * (H + 1) + H] = gsum;
+}
+
+__global__ void gate_bwd_reduce_kernel(const float* __restrict__ partial, int64_t nparts, int64_t H,
+                                       float scale, float* __restrict__ gw, float* __restrict__ gb,
+                                       float* __restrict__ gdb) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c > H) return;
+  float s = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) s += partial[p * (H + 1) + c];
+  s *= scale;
+  if (c < H) gw[c] += s;
+  else { gb[0] += s; gdb[0] += s; }
+}
+
+static const int64_t kGateBwdRows = 256;
+
+extern "C" int alodlm_final_norm_gate(const void* x, const void* wf, const void* gate_w,
+                                      const void* gate_b, const void* depth_bias, int64_t depth,
+                                      void* readout, float* rstd, float* gate, int64_t rows,
+                                      int64_t hidden, float eps, int dtype, void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && hidden > 0, "final_norm_gate: bad shape");
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    final_norm_gate_kernel<T><<<ceil_div_u(rows, RO_WAVES), 64 * RO_WAVES, 0, as_stream(stream)>>>(
+        (const T*)x, (const T*)wf, (const T*)gate_w, (const T*)gate_b, (const T*)depth_bias,
+        depth, (T*)readout, rstd, gate, rows, hidden, eps);
+  });
+  ALODLM_CHECK_LAUNCH("final_norm_gate");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_carry_select(const void* x, const void* wf, const void* table,
+                                   const int64_t* original, const int32_t* exits, int64_t depth,
+                                   void* out, float* rstd, int64_t rows, int64_t hidden,
+                                   int64_t vocab, float eps, int dtype, void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && hidden > 0, "carry_select: bad shape");
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    carry_select_kernel<T><<<ceil_div_u(rows, RO_WAVES), 64 * RO_WAVES, 0, as_stream(stream)>>>(
+        (const T*)x, (const T*)wf, (const T*)table, original, exits, depth, (T*)out, rstd, rows,
+        hidden, eps, vocab);
+  });
+  ALODLM_CHECK_LAUNCH("carry_select");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_exit_update(const float* gate, const float* uniforms, const uint8_t* masked,
+                                  int32_t* exits, int64_t depth, int64_t max_depth, int64_t rows,
+                                  void* stream) {
+  ALODLM_CHECK_ARG(depth >= 0 && depth < max_depth - 1, "exit_update: depth out of range");
+  if (rows == 0) return ALODLM_OK;
+  exit_update_kernel<<<ceil_div_u(rows, 256), 256, 0, as_stream(stream)>>>(
+      gate, uniforms, masked, exits, (int32_t)depth, (int32_t)max_depth, rows);
+  ALODLM_CHECK_LAUNCH("exit_update");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_inverse_weight_sum(const uint8_t* masked, const float* mask_prob,
+                                         int64_t rows, float* wsum, void* stream) {
+  inverse_weight_sum_kernel<<<1, 1024, 0, as_stream(stream)>>>(masked, mask_prob, rows, wsum);
+  ALODLM_CHECK_LAUNCH("inverse_weight_sum");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_select_rows(const uint8_t* masked, const int32_t* exits,
+                                  const int64_t* original, const int32_t* ar_target,
+                                  const float* gates, const float* mask_prob, const float* wsum,
+                                  float ar_coef, int64_t depth, int64_t max_depth, int64_t rows,
+                                  int32_t* sel_rows, int32_t* sel_target, float* sel_coef,
+                                  int32_t* sel_count, void* stream) {
+  ALODLM_CHECK_ARG(depth >= 0 && depth < max_depth, "select_rows: depth out of range");
+  select_rows_kernel<<<1, 1024, 0, as_stream(stream)>>>(
+      masked, exits, original, ar_target, gates, mask_prob, wsum, ar_coef, (int32_t)depth,
+      (int32_t)max_depth, rows, sel_rows, sel_target, sel_coef, sel_count);
+  ALODLM_CHECK_LAUNCH("select_rows");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_gather_rows(const void* src, const int32_t* sel_rows, int64_t n_sel,
+                                  void* dst, int64_t hidden, int dtype, void* stream) {
+  if (n_sel == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    gather_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
+        (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
+  });
+  ALODLM_CHECK_LAUNCH("gather_rows");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_scatter_rows(const void* src, const int32_t* sel_rows, int64_t n_sel,
+                                   void* dst, int64_t rows, int64_t hidden, int dtype,
+                                   void* stream) {
+  ALODLM_DISPATCH(dtype, T, {
+    zero_kernel<T><<<ceil_div_u(rows * hidden, 256), 256, 0, as_stream(stream)>>>((T*)dst,
+                                                                                  rows * hidden);
+    if (n_sel > 0)
+      scatter_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
+  });
+  ALODLM_CHECK_LAUNCH("scatter_rows");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_cross_entropy(void* logits, const int32_t* target, const float* coef,
+                                    const int32_t* n_rows, int64_t max_rows, int64_t vocab,
+                                    float* ce, float* entropy, int dtype, void* stream) {
+  ALODLM_CHECK_ARG(vocab > 0, "cross_entropy: bad vocab");
+  if (max_rows == 0) return ALODLM_OK;
+  const bool v8 = vocab % 8 == 0 && aligned8(logits, dtype);
+  ALODLM_DISPATCH(dtype, T, {
+    if (v8) cross_entropy_kernel<T, true><<<(unsigned)max_rows, 256, 0, as_stream(stream)>>>(
+        (T*)logits, target, coef, n_rows, vocab, ce, entropy);
+    else cross_entropy_kernel<T, false><<<(unsigned)max_rows, 256, 0, as_stream(stream)>>>(
+        (T*)logits, target, coef, n_rows, vocab, ce, entropy);
+  });
+  ALODLM_CHECK_LAUNCH("cross_entropy");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n_rows,
+                                 int64_t max_rows, float* ce_full, int64_t rows, void* stream) {
+  (void)rows;
+  if (max_rows == 0) return ALODLM_OK;
+  scatter_ce_kernel<<<ceil_div_u(max_rows, 256), 256, 0, as_stream(stream)>>>(ce, sel_rows, n_rows,
+                                                                             max_rows, ce_full);
+  ALODLM_CHECK_LAUNCH("scatter_ce");
+  return ALODLM_OK;
+}
+
+extern "C" int64_t alodlm_gate_bwd_workspace(int64_t rows, int64_t hidden) {
+  return ((rows + kGateBwdRows - 1) / kGateBwdRows) * (hidden + 1);
+}
+
+extern "C" int alodlm_gate_bwd(const float* dgate, const void* readout, float scale,
+                               float* gw_accum, float* gb_accum, float* gdb_accum, int64_t depth,
+                               int64_t rows, int64_t hidden, float* workspace, int dtype,
+                               void* stream) {
+  ALODLM_CHECK_ARG(rows > 0 && hidden > 0, "gate_bwd: bad shape");
+  ALODLM_CHECK_ARG((hidden + 1) * 4 <= 64 * 1024, "gate_bwd: hidden too large");
+  const int64_t nparts = (rows + kGateBwdRows - 1) / kGateBwdRows;
+  hipStream_t st = as_stream(stream);
+  ALODLM_DISPATCH(dtype, T, {
+    gate_bwd_kernel<T><<<(unsigned)nparts, 64, (hidden + 1) * sizeof(float), st>>>(
+        dgate, (const T*)readout, workspace, rows, hidden, kGateBwdRows);
+  });
+  ALODLM_CHECK_LAUNCH("gate_bwd");
+  gate_bwd_reduce_kernel<<<ceil_div_u(hidden + 1, 256), 256, 0, st>>>(
+      workspace, nparts, hidden, scale, gw_accum, gb_accum, gdb_accum + depth);
+  ALODLM_CHECK_LAUNCH("gate_bwd_reduce");
+  return ALODLM_OK;
+}

@@ -1,0 +1,467 @@
+"""The fused ALoDLM training step on the HIP kernels.
+
+``StepEngine`` owns the parameter arena of one ``ALoDLM`` module and runs the
+whole step of alodlm/model.py:130-187 as an explicit schedule of kernel
+launches on the current stream:
+
+forward   embed -> prelude -> for each depth: (re-embed/carry) -> core -> coda
+          -> final norm + gate -> exit sampling -> loss-bearing row selection
+          -> LM head GEMM -> vocabulary CE (writes dL/dlogits in place)
+          -> objective kernel (loss, metrics, dL/dgate)
+backward  per depth in reverse: LM head dX/dW -> gate head -> final norm ->
+          coda -> carry/re-embed -> core; then prelude and the embedding.
+
+Activation policy: every layer application keeps its input, the q|k|v
+projections, the attention output and log-sum-exp, the post-attention
+residual and the gate|up projections; norm outputs, rotary q/k and the SwiGLU
+product are recomputed in the backward (cheap bandwidth-bound kernels), so no
+GEMM or attention forward is ever recomputed.  The gradient checkpointing
+settings of ModelConfig change memory in the reference, not results, and are
+ignored here.
+
+Parameters live in one contiguous arena per step engine (q|k|v and gate|up of
+every layer adjacent, so each pair is one GEMM); gradients accumulate in a
+float32 arena with the same offsets and are returned to autograd in the
+parameter dtype.
+"""
+
+from dataclasses import dataclass
+import math
+
+import torch
+
+from . import _lib
+from ._lib import EPI_ACCUM, EPI_RESIDUAL, EPI_STORE, call, ptr, query
+from .batch import build_batch
+
+METRIC_NAMES = ("denoising", "actor", "sampled_mean_depth", "prediction_cost",
+                "regularization_cost", "profile_mean_depth", "first_pass_halt_probability")
+
+
+@dataclass
+class Dims:
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    layers: int
+    eps: float
+    theta: float
+
+    @classmethod
+    def from_hf(cls, config):
+        head_dim = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+        rope = getattr(config, "rope_parameters", None) or {}
+        theta = rope.get("rope_theta", getattr(config, "rope_theta", 10000.0))
+        return cls(config.hidden_size, config.num_attention_heads, config.num_key_value_heads,
+                   head_dim, config.intermediate_size, config.vocab_size,
+                   config.num_hidden_layers, float(config.rms_norm_eps), float(theta))
+
+    @property
+    def qkv_width(self):
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+_LAYER_ORDER = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+                "mlp.down_proj.weight", "input_layernorm.weight",
+                "post_attention_layernorm.weight", "self_attn.q_norm.weight",
+                "self_attn.k_norm.weight")
+_ALIGN = 64  # elements
+
+
+class Arena:
+    """Parameters re-homed into one flat buffer, in a fixed order."""
+
+    def __init__(self, named_params, dims, device, dtype):
+        self.dims, self.device, self.dtype = dims, device, dtype
+        order = ["backbone.model.embed_tokens.weight"]
+        for i in range(dims.layers):
+            order += [f"backbone.model.layers.{i}.{s}" for s in _LAYER_ORDER]
+        order += ["backbone.model.norm.weight", "backbone.lm_head.weight",
+                  "exit_gate.net.weight", "exit_gate.net.bias", "exit_gate.depth_bias"]
+        params = dict(named_params)
+        missing = set(order) ^ set(params)
+        if missing:
+            raise ValueError(f"unexpected parameter set for the Qwen3 ALoDLM arena: {sorted(missing)[:5]}")
+        self.names = order
+        self.offsets, total = {}, 0
+        for name in order:
+            numel = params[name].numel()
+            keep_adjacent = name.endswith(("k_proj.weight", "v_proj.weight", "up_proj.weight"))
+            if not keep_adjacent:
+                total = (total + _ALIGN - 1) // _ALIGN * _ALIGN
+            self.offsets[name] = total
+            total += numel
+        self.total = (total + _ALIGN - 1) // _ALIGN * _ALIGN
+        self.flat = torch.empty(self.total, dtype=dtype, device=device)
+        self.params = []
+        for name in order:
+            p = params[name]
+            view = self.flat[self.offsets[name]:self.offsets[name] + p.numel()].view(p.shape)
+            view.copy_(p.detach().to(device=device, dtype=dtype))
+            p.data = view
+            self.params.append(p)
+        self.data_ptr = self.flat.data_ptr()
+
+    def view(self, buf, name):
+        p = self.params[self.names.index(name)]
+        off = self.offsets[name]
+        return buf[off:off + p.numel()].view(p.shape)
+
+    def valid(self):
+        return all(p.data.data_ptr() == self.flat.data_ptr() + self.offsets[n] * self.flat.element_size()
+                   for n, p in zip(self.names, self.params))
+
+
+class _Layer:
+    """Views of one decoder layer's weights (and gradients) in an arena buffer."""
+
+    def __init__(self, arena, buf, index):
+        d = arena.dims
+        pre = f"backbone.model.layers.{index}."
+        off = arena.offsets
+        q = off[pre + "self_attn.q_proj.weight"]
+        self.wqkv = buf[q:q + d.qkv_width * d.hidden].view(d.qkv_width, d.hidden)
+        g = off[pre + "mlp.gate_proj.weight"]
+        self.wgu = buf[g:g + 2 * d.intermediate * d.hidden].view(2 * d.intermediate, d.hidden)
+        self.wo = arena.view(buf, pre + "self_attn.o_proj.weight")
+        self.wd = arena.view(buf, pre + "mlp.down_proj.weight")
+        self.ln1 = arena.view(buf, pre + "input_layernorm.weight")
+        self.ln2 = arena.view(buf, pre + "post_attention_layernorm.weight")
+        self.qn = arena.view(buf, pre + "self_attn.q_norm.weight")
+        self.kn = arena.view(buf, pre + "self_attn.k_norm.weight")
+
+
+class StepEngine:
+    """Runs the ALoDLM step of one model on its GPU (see the module docstring)."""
+
+    def __init__(self, model):
+        backbone = model.backbone
+        self.model = model
+        self.cfg = model.config
+        self.dims = Dims.from_hf(backbone.config)
+        params = list(model.named_parameters())
+        self.device = params[0][1].device
+        self.dtype = params[0][1].dtype
+        if self.device.type != "cuda":
+            raise ValueError("the HIP training step needs the model on a CUDA (ROCm) device")
+        self.code = _lib.dtype_code(self.dtype)
+        _lib.load()
+        self.arena = Arena(params, self.dims, self.device, self.dtype)
+        d = self.dims
+        if d.head_dim % 2:
+            raise ValueError("head_dim must be even for the rotary embedding")
+        self.layers = [_Layer(self.arena, self.arena.flat, i) for i in range(d.layers)]
+        a = self.arena
+        self.embed = a.view(a.flat, "backbone.model.embed_tokens.weight")
+        self.final_norm = a.view(a.flat, "backbone.model.norm.weight")
+        self.lm_head = a.view(a.flat, "backbone.lm_head.weight")
+        self.gate_w = a.view(a.flat, "exit_gate.net.weight")
+        self.gate_b = a.view(a.flat, "exit_gate.net.bias")
+        self.depth_bias = a.view(a.flat, "exit_gate.depth_bias")
+        # rotary inverse frequencies exactly as [tf] modeling_qwen3.py:115-117 (float32)
+        inv = 1.0 / (d.theta ** (torch.arange(0, d.head_dim, 2, dtype=torch.float32) / d.head_dim))
+        self.inv_freq = inv.to(self.device)
+
+    # ------------------------------------------------------------------ helpers
+    def _stream(self):
+        return _lib.stream_handle(self.device)
+
+    def _empty(self, *shape, dtype=None):
+        return torch.empty(*shape, dtype=dtype or self.dtype, device=self.device)
+
+    def _gemm(self, A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=EPI_STORE, R=None,
+              ldr=0):
+        ws = None
+        need = query("alodlm_gemm_workspace", M, N, K, epi, self.code)
+        if need:
+            ws = self._workspace(need)
+        call("alodlm_gemm", ptr(A), lda, a_k, ptr(B), ldb, b_k, ptr(C), ldc, ptr(R), ldr, M, N, K,
+             alpha, epi, self.code, ptr(ws), self._stream())
+
+    def _attention_fwd(self, q, k, v, o, lse, b):
+        d = self.dims
+        call("alodlm_attention_fwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(b.boundaries),
+             ptr(b.row_segment), ptr(o), ptr(lse), q.shape[0], d.heads, d.kv_heads, d.head_dim,
+             self.cfg.block_size, self.code, self._stream())
+
+    def _attention_bwd(self, q, k, v, o, lse, do, dq, dk, dv, b):
+        d, N = self.dims, q.shape[0]
+        ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads))
+        call("alodlm_attention_bwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(o), ptr(lse),
+             ptr(do), ptr(b.boundaries), ptr(b.row_segment), ptr(dq), ptr(dk), ptr(dv),
+             d.qkv_width, ptr(ws), N, d.heads, d.kv_heads, d.head_dim, self.cfg.block_size,
+             self.code, self._stream())
+
+    def _attention_fwd_flops(self, q, k, v, o, lse, b):
+        """Algorithmic forward FLOPs: 4*dh per allowed (q, k) pair and head."""
+        return 4.0 * self.dims.head_dim * self.dims.heads * b.pairs
+
+    def _attention_bwd_flops(self, q, k, v, o, lse, do, dq, dk, dv, b):
+        """Algorithmic backward FLOPs: 8*dh per allowed pair and head."""
+        return 8.0 * self.dims.head_dim * self.dims.heads * b.pairs
+
+    def _workspace(self, n):
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(max(n, 1), dtype=torch.float32, device=self.device)
+        return self._ws
+
+    # ------------------------------------------------------------------ layer fwd/bwd
+    def _layer_fwd(self, li, x, b, save):
+        d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
+        w = self.layers[li]
+        H, W, I = d.hidden, d.qkv_width, d.intermediate
+        h1 = self._empty(N, H)
+        rstd1 = self._empty(N, dtype=torch.float32)
+        call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), ptr(rstd1), N, H, d.eps, c, st)
+        qkv = self._empty(N, W)
+        self._gemm(h1, H, 1, w.wqkv, H, 1, qkv, W, N, W, H)
+        del h1
+        q = self._empty(N, d.heads * d.head_dim)
+        k = self._empty(N, d.kv_heads * d.head_dim)
+        call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
+             ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
+        o = self._empty(N, d.heads * d.head_dim)
+        lse = self._empty(d.heads, N, dtype=torch.float32)
+        v = qkv[:, (d.heads + d.kv_heads) * d.head_dim:]
+        self._attention_fwd(q, k, v, o, lse, b)
+        del q, k
+        x1 = self._empty(N, H)
+        self._gemm(o, d.heads * d.head_dim, 1, w.wo, d.heads * d.head_dim, 1, x1, H, N, H,
+                   d.heads * d.head_dim, epi=EPI_RESIDUAL, R=x, ldr=H)
+        h2 = self._empty(N, H)
+        rstd2 = self._empty(N, dtype=torch.float32)
+        call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), ptr(rstd2), N, H, d.eps, c, st)
+        gu = self._empty(N, 2 * I)
+        self._gemm(h2, H, 1, w.wgu, H, 1, gu, 2 * I, N, 2 * I, H)
+        del h2
+        act = self._empty(N, I)
+        call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
+        y = self._empty(N, H)
+        self._gemm(act, I, 1, w.wd, I, 1, y, H, N, H, I, epi=EPI_RESIDUAL, R=x1, ldr=H)
+        if save is not None:
+            save.append((li, x, rstd1, qkv, o, lse, x1, rstd2, gu))
+        return y
+
+    def _layer_bwd(self, dy, saved, b, g):
+        li, x, rstd1, qkv, o, lse, x1, rstd2, gu = saved
+        d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
+        w, gw = self.layers[li], self.grad_layers[li]
+        H, W, I = d.hidden, d.qkv_width, d.intermediate
+        QD = d.heads * d.head_dim
+        # ---- MLP: y = x1 + act . Wd^T
+        act = self._empty(N, I)
+        call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
+        dact = self._empty(N, I)
+        self._gemm(dy, H, 1, w.wd, I, 0, dact, I, N, I, H)
+        self._gemm(dy, H, 0, act, I, 0, gw.wd, I, H, I, N, epi=EPI_ACCUM)
+        del act
+        dgu = self._empty(N, 2 * I)
+        call("alodlm_swiglu_bwd", ptr(dact), ptr(gu), ptr(dgu), N, I, c, st)
+        del dact
+        h2 = self._empty(N, H)
+        call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
+        dh2 = self._empty(N, H)
+        self._gemm(dgu, 2 * I, 1, w.wgu, H, 0, dh2, H, N, H, 2 * I)
+        self._gemm(dgu, 2 * I, 0, h2, H, 0, gw.wgu, H, 2 * I, H, N, epi=EPI_ACCUM)
+        del dgu, h2
+        dx1 = self._empty(N, H)
+        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        call("alodlm_rmsnorm_bwd", ptr(dh2), ptr(x1), ptr(rstd2), ptr(w.ln2), ptr(dy), ptr(dx1),
+             ptr(gw.ln2), ptr(ws), N, H, c, st)
+        del dh2
+        # ---- attention: x1 = x + o . Wo^T
+        do = self._empty(N, QD)
+        self._gemm(dx1, H, 1, w.wo, QD, 0, do, QD, N, QD, H)
+        self._gemm(dx1, H, 0, o, QD, 0, gw.wo, QD, H, QD, N, epi=EPI_ACCUM)
+        q = self._empty(N, QD)
+        k = self._empty(N, d.kv_heads * d.head_dim)
+        call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
+             ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
+        dq = self._empty(N, QD)
+        dk = self._empty(N, d.kv_heads * d.head_dim)
+        dqkv = self._empty(N, W)
+        v = qkv[:, (d.heads + d.kv_heads) * d.head_dim:]
+        dv = dqkv[:, (d.heads + d.kv_heads) * d.head_dim:]
+        self._attention_bwd(q, k, v, o, lse, do, dq, dk, dv, b)
+        del q, k, do
+        ws = self._workspace(query("alodlm_qknorm_rope_bwd_workspace", N, d.heads, d.kv_heads,
+                                   d.head_dim))
+        call("alodlm_qknorm_rope_bwd", ptr(dq), ptr(dk), ptr(qkv), ptr(w.qn), ptr(w.kn),
+             ptr(b.positions), ptr(self.inv_freq), ptr(dqkv), ptr(gw.qn), ptr(gw.kn), ptr(ws), N,
+             d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
+        del dq, dk
+        h1 = self._empty(N, H)
+        call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, N, H, d.eps, c, st)
+        dh1 = self._empty(N, H)
+        self._gemm(dqkv, W, 1, w.wqkv, H, 0, dh1, H, N, H, W)
+        self._gemm(dqkv, W, 0, h1, H, 0, gw.wqkv, H, W, H, N, epi=EPI_ACCUM)
+        del dqkv, h1
+        dx = self._empty(N, H)
+        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        call("alodlm_rmsnorm_bwd", ptr(dh1), ptr(x), ptr(rstd1), ptr(w.ln1), ptr(dx1), ptr(dx),
+             ptr(gw.ln1), ptr(ws), N, H, c, st)
+        return dx
+
+    # ------------------------------------------------------------------ step
+    def forward(self, ids, labels, boundaries, need_grad, exit_uniforms=None, draws=None,
+                generator=None):
+        """Run the forward of the step; returns (out[10] float tensor, state)."""
+        if not self.arena.valid():
+            raise RuntimeError("model parameters were moved after the step engine was built")
+        self._ws = None
+        cfg, d = self.cfg, self.dims
+        K = cfg.max_depth
+        st, c = self._stream(), self.code
+        ids = ids.to(self.device)
+        labels = labels.to(self.device)
+        b = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id,
+                        generator=generator, draws=draws)
+        N, H, V = b.ids.numel(), d.hidden, d.vocab
+        S = b.boundaries.numel() - 1
+        saves = [] if need_grad else None
+        x = self._empty(N, H)
+        call("alodlm_embed_gather", ptr(self.embed), ptr(b.ids), ptr(x), N, H, V, c, st)
+        for li in range(cfg.loop_start):
+            x = self._layer_fwd(li, x, b, saves)
+        gates = torch.empty(K, N, dtype=torch.float32, device=self.device)
+        exits = torch.full((N,), K, dtype=torch.int32, device=self.device)
+        ce_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
+        wsum = torch.empty(1, dtype=torch.float32, device=self.device)
+        call("alodlm_inverse_weight_sum", ptr(b.masked), ptr(b.mask_probability), N, ptr(wsum), st)
+        ar_coef = 0.5 / (K * b.ar_count) if b.ar_count else 0.0
+        depths = []
+        core_in = x
+        for depth in range(K):
+            rec = {}
+            if depth:
+                xin = self._empty(N, H)
+                rstd_c = self._empty(N, dtype=torch.float32)
+                call("alodlm_carry_select", ptr(core_out), ptr(self.final_norm), ptr(self.embed),
+                     ptr(b.original), ptr(exits), depth, ptr(xin), ptr(rstd_c), N, H, V, d.eps,
+                     c, st)
+                depths[-1]["carry_rstd"] = rstd_c
+                core_in = xin
+            h = core_in
+            rec["core_saves"] = [] if need_grad else None
+            for li in range(cfg.loop_start, cfg.loop_end):
+                h = self._layer_fwd(li, h, b, rec["core_saves"])
+            core_out = h
+            rec["core_out"] = core_out
+            r = core_out
+            rec["coda_saves"] = [] if need_grad else None
+            for li in range(cfg.loop_end, d.layers):
+                r = self._layer_fwd(li, r, b, rec["coda_saves"])
+            rec["final_in"] = r
+            readout = self._empty(N, H)
+            rstd_f = self._empty(N, dtype=torch.float32)
+            call("alodlm_final_norm_gate", ptr(r), ptr(self.final_norm), ptr(self.gate_w),
+                 ptr(self.gate_b), ptr(self.depth_bias), depth, ptr(readout), ptr(rstd_f),
+                 ptr(gates[depth]), N, H, d.eps, c, st)
+            rec["readout"], rec["rstd_f"] = readout, rstd_f
+            if depth < K - 1:
+                if exit_uniforms is not None:
+                    u = exit_uniforms[depth].to(device=self.device, dtype=torch.float32).contiguous()
+                else:
+                    u = torch.rand(N, device=self.device, generator=generator)
+                call("alodlm_exit_update", ptr(gates[depth]), ptr(u), ptr(b.masked), ptr(exits),
+                     depth, K, N, st)
+            sel_rows = torch.empty(N, dtype=torch.int32, device=self.device)
+            sel_target = torch.empty(N, dtype=torch.int32, device=self.device)
+            sel_coef = torch.empty(N, dtype=torch.float32, device=self.device)
+            sel_count = torch.empty(1, dtype=torch.int32, device=self.device)
+            call("alodlm_select_rows", ptr(b.masked), ptr(exits), ptr(b.original),
+                 ptr(b.ar_target), ptr(gates), ptr(b.mask_probability), ptr(wsum), ar_coef, depth,
+                 K, N, ptr(sel_rows), ptr(sel_target), ptr(sel_coef), ptr(sel_count), st)
+            R = int(sel_count.item())
+            rec["R"], rec["sel_rows"] = R, sel_rows
+            if R:
+                xsel = self._empty(R, H)
+                call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
+                logits = self._empty(R, V)
+                self._gemm(xsel, H, 1, self.lm_head, H, 1, logits, V, R, V, H)
+                ce = torch.empty(R, dtype=torch.float32, device=self.device)
+                call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
+                     ptr(sel_count), R, V, ptr(ce), None, c, st)
+                call("alodlm_scatter_ce", ptr(ce), ptr(sel_rows), ptr(sel_count), R,
+                     ptr(ce_all[depth]), N, st)
+                if need_grad:
+                    rec["xsel"], rec["dlogits"] = xsel, logits
+                else:
+                    del logits, xsel
+            depths.append(rec)
+        out = torch.empty(10, dtype=torch.float32, device=self.device)
+        dgate = torch.empty(K, N, dtype=torch.float32, device=self.device)
+        ws = self._workspace(query("alodlm_objective_workspace", N, S, K))
+        call("alodlm_objective", ptr(gates), ptr(exits), ptr(b.masked), ptr(b.mask_probability),
+             ptr(ce_all), ptr(ce_all), ptr(b.ar_target), ptr(b.boundaries), S, N, K,
+             cfg.depth_prior_c, cfg.kl_beta_mi, cfg.kl_beta_marg, ptr(out), ptr(dgate), ptr(ws), st)
+        self.last_rows = [rec["R"] for rec in depths]
+        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "dgate": dgate,
+                 "prelude": saves, "depths": depths}
+        return out, state
+
+    def backward(self, state, grad_scale):
+        """Backward of the step; returns float32 gradients in the arena layout."""
+        cfg, d = self.cfg, self.dims
+        K, st, c = cfg.max_depth, self._stream(), self.code
+        b = state["batch"]
+        N, H, V = b.ids.numel(), d.hidden, d.vocab
+        grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
+        self.grad_layers = [_Layer(self.arena, grads, i) for i in range(d.layers)]
+        a = self.arena
+        g_embed = a.view(grads, "backbone.model.embed_tokens.weight")
+        g_norm = a.view(grads, "backbone.model.norm.weight")
+        g_lm = a.view(grads, "backbone.lm_head.weight")
+        g_gw = a.view(grads, "exit_gate.net.weight")
+        g_gb = a.view(grads, "exit_gate.net.bias")
+        g_db = a.view(grads, "exit_gate.depth_bias")
+        exits = state["exits"]
+        dnext = None  # gradient at the core input of depth+1
+        for depth in reversed(range(K)):
+            rec = state["depths"][depth]
+            R = rec["R"]
+            dread = self._empty(N, H)
+            if R:
+                dsel = self._empty(R, H)
+                # d readout = dlogits . W_lm ; dW_lm += dlogits^T . readout
+                self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
+                           alpha=grad_scale)
+                self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H, R,
+                           alpha=grad_scale, epi=EPI_ACCUM)
+                call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
+                     c, st)
+                del dsel
+            else:
+                dread.zero_()
+            ws = self._workspace(query("alodlm_gate_bwd_workspace", N, H))
+            call("alodlm_gate_bwd", ptr(state["dgate"][depth]), ptr(rec["readout"]), grad_scale,
+                 ptr(g_gw), ptr(g_gb), ptr(g_db), depth, N, H, ptr(ws), c, st)
+            dr = self._empty(N, H)
+            ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+            call("alodlm_rmsnorm_bwd", ptr(dread), ptr(rec["final_in"]), ptr(rec["rstd_f"]),
+                 ptr(self.final_norm), None, ptr(dr), ptr(g_norm), ptr(ws), N, H, c, st)
+            del dread
+            for saved in reversed(rec["coda_saves"]):
+                dr = self._layer_bwd(dr, saved, b, grads)
+            if dnext is not None:
+                # x_in(depth+1) = exits <= depth+1 ? E[original] : norm(core_out(depth))
+                dcore = self._empty(N, H)
+                ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+                call("alodlm_carry_select_bwd", ptr(dnext), ptr(rec["core_out"]),
+                     ptr(rec["carry_rstd"]), ptr(self.final_norm), ptr(exits), depth + 1,
+                     ptr(b.original), ptr(dr), ptr(dcore), ptr(g_norm), ptr(g_embed), ptr(ws),
+                     N, H, V, c, st)
+                dr = dcore
+            for saved in reversed(rec["core_saves"]):
+                dr = self._layer_bwd(dr, saved, b, grads)
+            dnext = dr
+        dx = dnext
+        for saved in reversed(state["prelude"]):
+            dx = self._layer_bwd(dx, saved, b, grads)
+        call("alodlm_embed_scatter_add", ptr(dx), ptr(b.ids), None, 0, ptr(g_embed), N, H, V, c,
+             st)
+        return grads

@@ -1,0 +1,142 @@
+"""Recurrent Qwen3 ALoDLM (drop-in for alodlm/model.py).
+
+``ALoDLM(backbone, config)`` wraps a transformers ``Qwen3ForCausalLM`` exactly
+like the reference (same submodule names, so ``state_dict`` keys and the
+checkpoint layout are unchanged).  ``forward(ids, labels, boundaries)`` runs
+the whole training step - batch building, rollout over the recurrent depths,
+cross-entropies and the objective - on the gfx950 HIP kernels through
+``StepEngine`` and returns ``(loss, metrics)``; ``loss.backward()`` runs the
+hand-scheduled backward and fills every parameter's ``.grad``.
+"""
+
+import json
+import math
+from dataclasses import asdict
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+
+from .config import ModelConfig, local_dir
+from .engine import METRIC_NAMES, StepEngine
+
+
+class GateHead(nn.Module):
+    """Halting gate: a shared linear readout plus one bias per depth
+    (alodlm/model.py:22-38).  A fresh gate has zero weights and depth biases
+    equal to the logits of the conditional hazards mass/survival, the last
+    depth being forced."""
+
+    def __init__(self, hidden_size, initial_mass):
+        super().__init__()
+        self.net = nn.Linear(hidden_size, 1)
+        nn.init.zeros_(self.net.weight)
+        nn.init.zeros_(self.net.bias)
+        biases, survival = [], 1.0
+        for mass in initial_mass[:-1]:
+            hazard = mass / survival
+            biases.append(math.log(hazard / (1 - hazard)))
+            survival *= 1 - hazard
+        self.depth_bias = nn.Parameter(torch.tensor(biases + [0.0], dtype=torch.float32))
+
+    def forward(self, features, depth):
+        return self.net(features).squeeze(-1) + self.depth_bias[depth]
+
+
+class _Step(torch.autograd.Function):
+    """One autograd node for the whole step; inputs are the arena parameters."""
+
+    @staticmethod
+    def forward(ctx, engine, inputs, need_grad, *params):
+        ids, labels, boundaries, extra = inputs
+        out, state = engine.forward(ids, labels, boundaries, need_grad, **extra)
+        ctx.engine = engine
+        ctx.state = state if need_grad else None
+        metrics = out[1:].clone()
+        ctx.mark_non_differentiable(metrics)
+        return out[0].clone(), metrics
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_metrics):
+        engine, state = ctx.engine, ctx.state
+        if state is None:
+            raise RuntimeError("the step was run without gradient tracking")
+        scale = float(grad_loss)
+        grads = engine.backward(state, scale)
+        ctx.state = None
+        if engine.dtype == torch.float32:
+            flat = grads
+        else:
+            flat = torch.empty(engine.arena.total, dtype=engine.dtype, device=engine.device)
+            from . import _lib
+            _lib.call("alodlm_cast_f32", _lib.ptr(grads), _lib.ptr(flat), grads.numel(),
+                      engine.code, _lib.stream_handle(engine.device))
+        views = [engine.arena.view(flat, name) for name in engine.arena.names]
+        return (None, None, None, *views)
+
+
+class ALoDLM(nn.Module):
+    def __init__(self, backbone, config):
+        super().__init__()
+        config.validate(backbone)
+        self.backbone = backbone
+        self.config = config
+        self.exit_gate = GateHead(backbone.config.hidden_size, config.gate_init_pi)
+        self.exit_gate.to(dtype=backbone.dtype, device=backbone.device)
+        self._engine = None
+
+    @classmethod
+    def from_pretrained(cls, directory, config=None, dtype=torch.float32, require_gate=True):
+        """Load a checkpoint directory (alodlm/model.py:94-114)."""
+        from transformers import AutoModelForCausalLM
+        path = local_dir(directory)
+        metadata = path / "alodlm_config.json"
+        if config is None:
+            if not metadata.is_file():
+                raise ValueError("Checkpoint requires alodlm_config.json or an explicit ModelConfig")
+            config = ModelConfig(**json.loads(metadata.read_text()))
+        backbone = AutoModelForCausalLM.from_pretrained(
+            str(path), local_files_only=True, trust_remote_code=False, dtype=dtype,
+            attn_implementation="eager")
+        model = cls(backbone, config)
+        gate_file = path / "exit_gate.pt"
+        if gate_file.is_file():
+            model.exit_gate.load_state_dict(
+                torch.load(gate_file, map_location="cpu", weights_only=True), strict=True)
+        elif require_gate:
+            raise ValueError("Adaptive inference requires trained exit_gate.pt weights")
+        return model
+
+    def save_pretrained(self, directory, state_dict=None):
+        """HF backbone files, exit_gate.pt and alodlm_config.json (alodlm/model.py:116-128)."""
+        path = Path(directory)
+        path.mkdir(parents=True, exist_ok=True)
+        state = state_dict if state_dict is not None else self.state_dict()
+        backbone = {k[len("backbone."):]: v for k, v in state.items() if k.startswith("backbone.")}
+        gate = {k[len("exit_gate."):]: v for k, v in state.items() if k.startswith("exit_gate.")}
+        self.backbone.config._name_or_path = ""
+        self.backbone.save_pretrained(path, state_dict=backbone, safe_serialization=True)
+        torch.save(gate, path / "exit_gate.pt")
+        (path / "alodlm_config.json").write_text(json.dumps(asdict(self.config), indent=2) + "\n")
+
+    def engine(self):
+        """The step engine bound to the current parameter storage."""
+        if self._engine is None or not self._engine.arena.valid():
+            self._engine = StepEngine(self)
+        return self._engine
+
+    def forward(self, ids, labels, boundaries, exit_uniforms=None, draws=None, generator=None):
+        """The training step's forward (alodlm/model.py:171-187).
+
+        Returns ``(loss, metrics)``; ``loss.backward()`` fills parameter grads.
+        ``exit_uniforms`` / ``draws`` replay known randomness (tests);
+        ``generator`` replaces the device's default generator.
+        """
+        engine = self.engine()
+        params = engine.arena.params
+        need_grad = torch.is_grad_enabled() and any(p.requires_grad for p in params)
+        extra = {"exit_uniforms": exit_uniforms, "draws": draws, "generator": generator}
+        loss, metrics = _Step.apply(engine, (ids, labels, boundaries, extra), need_grad, *params)
+        values = dict(zip(METRIC_NAMES + ("ar_loss",), metrics[:8].unbind()))
+        values["loss"] = loss.detach()
+        return loss, values

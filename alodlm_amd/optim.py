@@ -1,0 +1,158 @@
+"""Clipped AdamW with float32 master weights on the HIP kernels.
+
+Drop-in for the optimizer sub-step of alodlm/train.py:42-56,138-148:
+``torch.optim.AdamW(groups, lr)`` with betas (0.9, 0.999), eps 1e-8 and the
+reference's two weight-decay groups, preceded by ``clip_grad_norm_(params,
+max_norm)``.  Differences by design: bf16 parameters keep a float32 master copy
+and float32 moments (the reference's plain bf16 run keeps bf16 parameters and
+moments; its ZeRO-2 run keeps float32 masters), and the clip coefficient is
+applied inside the AdamW kernel from a device-side norm, so no host sync is
+needed.
+"""
+
+import torch
+
+from . import _lib
+
+CHUNK = 1 << 16
+
+
+class _Table:
+    """Device tensor list (pointers, sizes) and its fixed-size chunk table."""
+
+    def __init__(self, tensors, device):
+        numels = [t.numel() for t in tensors]
+        chunk_tensor, chunk_start = [], []
+        for i, n in enumerate(numels):
+            for start in range(0, n, CHUNK):
+                chunk_tensor.append(i)
+                chunk_start.append(start)
+        self.n_chunks = len(chunk_tensor)
+        self.numels = torch.tensor(numels, dtype=torch.int64, device=device)
+        self.chunk_tensor = torch.tensor(chunk_tensor, dtype=torch.int32, device=device)
+        self.chunk_start = torch.tensor(chunk_start, dtype=torch.int64, device=device)
+
+    @staticmethod
+    def pointers(tensors, device):
+        return torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=device)
+
+
+class FusedAdamW(torch.optim.Optimizer):
+    """AdamW over float32 masters with an optional fused global-norm clip.
+
+    ``max_grad_norm``: when set, ``step()`` clips the gradients to this global
+    L2 norm (torch.nn.utils.clip_grad_norm_ semantics) inside the kernel; the
+    norm of the last step is ``self.last_grad_norm`` (a device scalar).
+    """
+
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01,
+                 max_grad_norm=None):
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay)
+        super().__init__(params, defaults)
+        self.max_grad_norm = max_grad_norm
+        self.last_grad_norm = None
+        self._tables = None
+
+    def _params(self):
+        return [p for g in self.param_groups for p in g["params"]]
+
+    def _prepare(self):
+        params = self._params()
+        dtypes = {p.dtype for p in params}
+        devices = {p.device for p in params}
+        if len(dtypes) != 1 or len(devices) != 1:
+            raise ValueError("FusedAdamW needs parameters of one dtype on one device")
+        device = devices.pop()
+        if device.type != "cuda":
+            raise ValueError("FusedAdamW runs on the GPU")
+        self._device, self._dtype = device, dtypes.pop()
+        self._code = _lib.dtype_code(self._dtype)
+        for p in params:
+            state = self.state[p]
+            if not state:
+                state["step"] = 0
+                state["master"] = (p.detach() if p.dtype == torch.float32
+                                   else p.detach().float().clone())
+                state["exp_avg"] = torch.zeros(p.shape, dtype=torch.float32, device=device)
+                state["exp_avg_sq"] = torch.zeros(p.shape, dtype=torch.float32, device=device)
+        self._tables = []
+        for group in self.param_groups:
+            ps = group["params"]
+            if not ps:
+                self._tables.append(None)
+                continue
+            table = _Table(ps, device)
+            table.params = _Table.pointers(ps, device)
+            table.master = _Table.pointers([self.state[p]["master"] for p in ps], device)
+            table.m = _Table.pointers([self.state[p]["exp_avg"] for p in ps], device)
+            table.v = _Table.pointers([self.state[p]["exp_avg_sq"] for p in ps], device)
+            table.wd = torch.full((len(ps),), float(group["weight_decay"]), dtype=torch.float32,
+                                  device=device)
+            self._tables.append(table)
+        self._all = _Table(params, device)
+        self._partial = torch.empty(self._all.n_chunks, dtype=torch.float32, device=device)
+        self._norm = torch.zeros(1, dtype=torch.float32, device=device)
+
+    def load_state_dict(self, state_dict):
+        super().load_state_dict(state_dict)
+        self._tables = None
+
+    def grad_norm(self):
+        """Global L2 norm of all gradients into a device scalar (no host sync)."""
+        if self._tables is None:
+            self._prepare()
+        params = self._params()
+        grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in params]
+        for g in grads:
+            if g.dtype != self._dtype or not g.is_contiguous():
+                raise ValueError("gradients must be contiguous and of the parameter dtype")
+        gptr = _Table.pointers(grads, self._device)
+        _lib.call("alodlm_grad_norm", _lib.ptr(gptr), _lib.ptr(self._all.chunk_tensor),
+                  _lib.ptr(self._all.chunk_start), _lib.ptr(self._all.numels),
+                  self._all.n_chunks, CHUNK, self._code, _lib.ptr(self._partial),
+                  _lib.ptr(self._norm), _lib.stream_handle(self._device))
+        self.last_grad_norm = self._norm[0]
+        return self._norm[0], grads
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = closure() if closure is not None else None
+        if self._tables is None:
+            self._prepare()
+        norm_ptr = None
+        if self.max_grad_norm is not None:
+            self.grad_norm()
+            norm_ptr = _lib.ptr(self._norm)
+        for group, table in zip(self.param_groups, self._tables):
+            if table is None:
+                continue
+            ps = group["params"]
+            grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in ps]
+            steps = {self.state[p]["step"] for p in ps}
+            if len(steps) != 1:
+                raise RuntimeError("parameters of one group must share their step count")
+            step = steps.pop() + 1
+            for p in ps:
+                self.state[p]["step"] = step
+            gptr = _Table.pointers(grads, self._device)
+            beta1, beta2 = group["betas"]
+            _lib.call("alodlm_adamw", _lib.ptr(table.params), _lib.ptr(table.master),
+                      _lib.ptr(table.m), _lib.ptr(table.v), _lib.ptr(gptr),
+                      _lib.ptr(table.chunk_tensor), _lib.ptr(table.chunk_start),
+                      _lib.ptr(table.numels), _lib.ptr(table.wd), table.n_chunks, CHUNK,
+                      norm_ptr, float(self.max_grad_norm or 0.0), float(group["lr"]),
+                      float(beta1), float(beta2), float(group["eps"]), step, self._code,
+                      _lib.stream_handle(self._device))
+        return loss
+
+
+def param_groups(model, weight_decay):
+    """The reference's two groups (alodlm/train.py:42-48): names containing
+    'bias', 'LayerNorm.weight' or 'layer_norm.weight' are not decayed."""
+    no_decay = ("bias", "LayerNorm.weight", "layer_norm.weight")
+    return [
+        {"params": [p for n, p in model.named_parameters() if not any(s in n for s in no_decay)],
+         "weight_decay": weight_decay},
+        {"params": [p for n, p in model.named_parameters() if any(s in n for s in no_decay)],
+         "weight_decay": 0.0},
+    ]

@@ -1,0 +1,249 @@
+"""Benchmark: ALoDLM-1.7B full training step on one MI355X.
+
+One step = ALoDLM.forward on one pack of 8 x 2048 synthetic tokens (dual-stream
+N = 32768 rows, recurrent core = layers 0-28 run K = 4 times) + backward +
+global-norm clip + AdamW with float32 masters, all on the HIP kernels.
+
+Prints one JSON line (metric of BASELINE: train tokens/s) with:
+  roofline      the dominant kernel class (by time in the timed region, from
+                HIP events around its launches on the launch stream):
+                algorithmic FLOPs per launch / average launch time vs 2.5 PFLOP/s
+  mfu           whole-step algorithmic FLOPs / step time / bf16 dense peak
+  cpu_baseline  the CPU oracle timed on this host on a bounded sample (one
+                decoder layer fwd+bwd at 4096 x 2048 and one LM-head readout
+                fwd+bwd), extrapolated to the full step by layer-application
+                and readout-row counts.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+PEAK_BF16 = 2516.6e12   # dense bf16 MFMA FLOP/s of MI355X (256 CU x 4096 FLOP/clk x 2.4 GHz)
+PEAK_HBM = 8.0e12
+
+
+def qwen3_1p7b_config():
+    from transformers import Qwen3Config
+    return Qwen3Config(hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
+                       num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                       vocab_size=151936, max_position_embeddings=40960, rms_norm_eps=1e-6,
+                       rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+                       tie_word_embeddings=False, bos_token_id=151643, eos_token_id=151645)
+
+
+def build_model(device, dtype, seed=0):
+    """Random-init Qwen3-1.7B backbone (N(0, 0.02), unit norms) + a fresh gate,
+    topology loop 0-28 (the repo's 1.7B configuration)."""
+    from transformers import Qwen3ForCausalLM
+    from alodlm_amd.config import ModelConfig
+    from alodlm_amd.model import ALoDLM
+    with torch.device("meta"):
+        backbone = Qwen3ForCausalLM(qwen3_1p7b_config())
+    backbone = backbone.to_empty(device=device).to(dtype)
+    g = torch.Generator(device=device).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in backbone.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02, generator=g)
+    cfg = ModelConfig(loop_start=0, loop_end=28, max_depth=4, mask_token_id=151665,
+                      block_size=32)
+    return ALoDLM(backbone, cfg)
+
+
+def step_flops(dims, cfg, seg_lengths, rows_per_depth):
+    """Algorithmic FLOPs of one step (recompute not credited)."""
+    from alodlm_amd.batch import allowed_pairs
+    H, I, V = dims.hidden, dims.intermediate, dims.vocab
+    qd, kd = dims.heads * dims.head_dim, dims.kv_heads * dims.head_dim
+    p_layer = H * (qd + 2 * kd) + qd * H + 3 * H * I
+    n_rows = 2 * sum(seg_lengths)
+    apps = cfg.loop_start + cfg.max_depth * (dims.layers - cfg.loop_start)
+    pairs = sum(allowed_pairs(L, cfg.block_size) for L in seg_lengths)
+    gemm = apps * 6 * p_layer * n_rows
+    attn = apps * 12 * dims.head_dim * dims.heads * pairs
+    head = 6 * H * V * sum(rows_per_depth) + 6 * H * n_rows * cfg.max_depth
+    return gemm, attn, head
+
+
+class KernelTimer:
+    """HIP events around every GEMM / attention launch of the engine."""
+
+    def __init__(self):
+        self.records = {}
+
+    def wrap(self, engine):
+        timer = self
+        gemm, fwd, bwd = engine._gemm, engine._attention_fwd, engine._attention_bwd
+
+        def timed(kind, fn, flops_fn):
+            def run(*args, **kwargs):
+                start = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                start.record()
+                out = fn(*args, **kwargs)
+                end.record()
+                timer.records.setdefault(kind, []).append((start, end, flops_fn(*args, **kwargs)))
+                return out
+            return run
+
+        engine._gemm = timed("gemm_bf16", gemm, lambda *a, **k: 2.0 * a[8] * a[9] * a[10])
+        engine._attention_fwd = timed("attention_fwd", fwd, engine._attention_fwd_flops)
+        engine._attention_bwd = timed("attention_bwd", bwd, engine._attention_bwd_flops)
+
+    def summary(self):
+        out = {}
+        for kind, recs in self.records.items():
+            ms = sum(s.elapsed_time(e) for s, e, _ in recs)
+            flops = sum(f for _, _, f in recs)
+            out[kind] = {"launches": len(recs), "ms": ms, "flops": flops}
+        return out
+
+
+def cpu_baseline(dims_l, cfg_seg=2048, readout_rows=1024, threads=None):
+    """Time the CPU oracle (float32, torch eager on this host) on a bounded
+    sample and extrapolate to the full 1.7B step.  Returns (tokens/s, detail)."""
+    from oracle import step as O
+    threads = threads or os.cpu_count()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    d = O.Dims(hidden=2048, heads=16, kv_heads=8, head_dim=128, intermediate=6144,
+               vocab=151936, layers=1, eps=1e-6, theta=1e6)
+    pre = "model.layers.0."
+    shapes = {"self_attn.q_proj.weight": (2048, 2048), "self_attn.k_proj.weight": (1024, 2048),
+              "self_attn.v_proj.weight": (1024, 2048), "self_attn.o_proj.weight": (2048, 2048),
+              "mlp.gate_proj.weight": (6144, 2048), "mlp.up_proj.weight": (6144, 2048),
+              "mlp.down_proj.weight": (2048, 6144)}
+    p = {pre + k: (torch.randn(*s, generator=g) * 0.02).requires_grad_(True) for k, s in shapes.items()}
+    for k, n in (("input_layernorm.weight", 2048), ("post_attention_layernorm.weight", 2048),
+                 ("self_attn.q_norm.weight", 128), ("self_attn.k_norm.weight", 128)):
+        p[pre + k] = torch.ones(n).requires_grad_(True)
+    L = cfg_seg
+    rows = 2 * L
+    pos = torch.cat((torch.arange(L), torch.arange(L)))
+    cos, sin = O.rope_tables(pos, 128, 1e6)
+    allowed = torch.as_tensor(O.attention_mask(L, 32))
+    x = torch.randn(rows, 2048, generator=g).requires_grad_(True)
+    t0 = time.perf_counter()
+    y = O.layer_forward(p, pre, x, cos, sin, allowed, d)
+    y.backward(torch.randn_like(y))
+    t_layer = time.perf_counter() - t0
+    W = (torch.randn(151936, 2048, generator=g) * 0.02).requires_grad_(True)
+    X = torch.randn(readout_rows, 2048, generator=g).requires_grad_(True)
+    tgt = torch.randint(0, 151936, (readout_rows,), generator=g)
+    t0 = time.perf_counter()
+    loss = torch.nn.functional.cross_entropy(X @ W.T, tgt)
+    loss.backward()
+    t_readout = time.perf_counter() - t0
+    return t_layer, t_readout, threads
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-kernel-timing", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    dtype = torch.bfloat16
+    model = build_model(device, dtype)
+    engine = model.engine()
+    timer = None
+    gen = torch.Generator().manual_seed(0)
+    seg_lengths = [2048] * 8
+    ids = torch.randint(0, 151936, (sum(seg_lengths),), generator=gen).to(device)
+    labels = ids.clone()
+    bounds = torch.tensor([0] + [sum(seg_lengths[:i + 1]) for i in range(len(seg_lengths))])
+    torch.cuda.manual_seed(0)
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-5, max_grad_norm=1.0)
+
+    def one_step():
+        loss, metrics = model(ids, labels, bounds)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for i in range(args.warmup):
+        loss = one_step()
+        print(f"[bench] warmup step {i} loss {float(loss):.4f}", file=sys.stderr, flush=True)
+    if not args.no_kernel_timing:
+        timer = KernelTimer()
+        timer.wrap(engine)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rows = []
+    for i in range(args.steps):
+        loss = one_step()
+        rows.append(list(engine.last_rows))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    print(f"[bench] timed {args.steps} steps in {elapsed:.3f}s loss {float(loss):.4f}",
+          file=sys.stderr, flush=True)
+    ms = 1000.0 * elapsed / args.steps
+    tokens = sum(seg_lengths)
+    value = tokens * args.steps / elapsed
+    gemm_f, attn_f, head_f = step_flops(engine.dims, model.config, seg_lengths,
+                                        [sum(r) / len(rows) for r in zip(*rows)])
+    step_f = gemm_f + attn_f + head_f
+    line = {
+        "metric": "train tokens/s, ALoDLM-1.7B seq2048 on 1 MI355X",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "ALoDLM-1.7B full training step (fwd+bwd+clip+AdamW fp32 master)",
+                   "model": "Qwen3-1.7B random init, untied, loop 0-28, max_depth 4",
+                   "global_batch": 8, "seq_len": 2048, "dual_stream_rows": 2 * tokens,
+                   "parallelism": "none (1 GPU)"},
+        "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
+        "step_tflop": round(step_f / 1e12, 1),
+    }
+    if timer is not None:
+        summary = timer.summary()
+        dom = max(summary, key=lambda k: summary[k]["ms"])
+        s = summary[dom]
+        achieved = s["flops"] / s["launches"] / (s["ms"] / s["launches"] / 1000.0)
+        line["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 1),
+                            "peak": round(PEAK_BF16 / 1e12, 1), "unit": "TFLOP/s",
+                            "frac": round(achieved / PEAK_BF16, 4), "traffic": None}
+        line["kernel_classes"] = {k: {"ms_per_step": round(v["ms"] / args.steps, 1),
+                                      "tflops": round(v["flops"] / (v["ms"] / 1000) / 1e12, 1)}
+                                  for k, v in summary.items()}
+    if not args.no_cpu_baseline:
+        del opt, model, engine
+        torch.cuda.empty_cache()
+        t_layer, t_readout, threads = cpu_baseline(None)
+        apps = 112
+        # sample: one layer on 4096 rows (one 2048-token segment), readout on 1024 rows
+        t_step = apps * 8 * t_layer + (sum(sum(r) for r in rows) / len(rows) / 1024) * t_readout
+        line["cpu_baseline"] = {
+            "value": round(tokens / t_step, 4), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle fp32 eager: 1 decoder layer fwd+bwd on 4096x2048 rows "
+                       f"({t_layer:.2f}s) + LM head/CE fwd+bwd on 1024x2048x151936 "
+                       f"({t_readout:.2f}s); extrapolated x{apps * 8} layer samples and "
+                       f"readout rows/1024"),
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

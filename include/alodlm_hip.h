@@ -1,0 +1,292 @@
+/*
+ * alodlm_hip.h - C ABI of the MI355X (gfx950) kernels behind the ALoDLM
+ * training step.
+ *
+ * Conventions
+ *   - Every entry point is stateless, enqueues work on `stream` (a hipStream_t
+ *     passed as void*; NULL = the default stream) and returns ALODLM_OK or an
+ *     error code; alodlm_last_error() then holds a message.  Nothing
+ *     synchronises the device unless stated.
+ *   - Pointers are device pointers unless named host_*.  The caller owns all
+ *     memory: outputs and workspaces are allocated by the caller.
+ *   - `dtype` selects the storage type of activations and weights:
+ *     ALODLM_F32 (float) or ALODLM_BF16 (bfloat16, 2 bytes).  Arithmetic is
+ *     float32; bf16 results are rounded to nearest even at the same points
+ *     where the reference's bf16 eager ops round.
+ *   - Row-major matrices; `ld*` are row strides in elements.
+ *
+ * Citations name the reference function each entry point replaces
+ * (amazon-science/ALoDLM; [tf] = transformers' Qwen3 modules).
+ */
+#ifndef ALODLM_HIP_H
+#define ALODLM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ALODLM_ABI_VERSION 1
+
+enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
+enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
+
+/* Library identity and errors. */
+int alodlm_abi_version(void);
+const char* alodlm_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Dual-stream batch (alodlm/batch.py:34-85, build_batch).
+ * Given the host-drawn randomness (per-block mask probability `block_p`,
+ * per-block masked count `block_count` = round(n_candidates * p) and the
+ * concatenated randperm draws `perms` with per-block offsets `perm_offset`),
+ * writes the clean+noisy rows of every segment.  Segment s covers tokens
+ * [seg[s], seg[s+1]) and dual-stream rows [2*seg[s], 2*seg[s+1]); its blocks
+ * are [seg_block[s], seg_block[s+1]).  Outputs have 2*n_tokens rows:
+ * out_ids / out_original / out_positions (int64), out_masked (uint8),
+ * out_prob (float), row_segment (int32), ar_target (int32: the next-token
+ * label of a clean row or -1, alodlm/loss.py:20-25) and out_boundaries
+ * (int64, S+1).
+ * ------------------------------------------------------------------------ */
+int alodlm_batch_build(const int64_t* ids, const int64_t* labels, const int64_t* seg,
+                       const int32_t* seg_block, int64_t n_segments, int64_t n_blocks,
+                       int64_t block_size, int64_t mask_token_id, const float* block_p,
+                       const int32_t* block_count, const int64_t* perm_offset,
+                       const int64_t* perms, int64_t* out_ids, int64_t* out_original,
+                       int64_t* out_positions, uint8_t* out_masked, float* out_prob,
+                       int32_t* row_segment, int32_t* ar_target, int64_t* out_boundaries,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Embedding ([tf] modeling_qwen3.py:352; alodlm/model.py:133,149).
+ * gather: out[r] = table[ids[r]].  scatter_add (backward): dtable[ids[r]] +=
+ * dout[r] (float32 accumulate) for rows with row_exits == NULL or
+ * row_exits[r] <= max_exit.  Ids outside [0, vocab) give NaN rows (gather)
+ * or are skipped (scatter); they are never dereferenced.
+ * ------------------------------------------------------------------------ */
+int alodlm_embed_gather(const void* table, const int64_t* ids, void* out, int64_t rows,
+                        int64_t hidden, int64_t vocab, int dtype, void* stream);
+int alodlm_embed_scatter_add(const void* dout, const int64_t* ids, const int32_t* row_exits,
+                             int64_t max_exit, float* dtable, int64_t rows, int64_t hidden,
+                             int64_t vocab, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * RMSNorm ([tf] modeling_qwen3.py:59-64): y = w * cast(x * rsqrt(mean(x^2) + eps)).
+ * fwd writes y and rstd[rows] (float).
+ * bwd: dx = dres + d(norm)/dx . dy (dres may be NULL; dx may alias dres);
+ * dw_accum[cols] += sum_rows dy * cast(x*rstd) using `workspace` of
+ * alodlm_rmsnorm_bwd_workspace(rows, cols) floats (deterministic order).
+ * ------------------------------------------------------------------------ */
+int alodlm_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
+                       int64_t cols, float eps, int dtype, void* stream);
+int64_t alodlm_rmsnorm_bwd_workspace(int64_t rows, int64_t cols);
+int alodlm_rmsnorm_bwd(const void* dy, const void* x, const float* rstd, const void* w,
+                       const void* dres, void* dx, float* dw_accum, float* workspace,
+                       int64_t rows, int64_t cols, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * q_norm/k_norm + rotary (alodlm/model.py:41-46,58; [tf] :126-137).
+ * qkv: [rows, (nq+2*nkv)*dh] projections (q | k | v).  positions: int64 [rows].
+ * inv_freq: float [dh/2].  fwd writes q_out [rows, nq*dh] and k_out
+ * [rows, nkv*dh] (normalised, rotated).  bwd takes dq, dk of the rotated
+ * values, recomputes the forward, writes dqkv's q and k columns and adds the
+ * norm-weight gradients into dwq_accum/dwk_accum (float, dh each) using
+ * `workspace` of alodlm_qknorm_rope_bwd_workspace(rows, nq, nkv, dh) floats.
+ * ------------------------------------------------------------------------ */
+int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const void* wk,
+                           const int64_t* positions, const float* inv_freq, void* q_out,
+                           void* k_out, int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
+                           float eps, int dtype, void* stream);
+int64_t alodlm_qknorm_rope_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv, int64_t dh);
+int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv, const void* wq,
+                           const void* wk, const int64_t* positions, const float* inv_freq,
+                           void* dqkv, float* dwq_accum, float* dwk_accum, float* workspace,
+                           int64_t rows, int64_t nq, int64_t nkv, int64_t dh, float eps,
+                           int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GEMM for every linear layer (nn.Linear at alodlm/model.py:55-57,74-75,161;
+ * [tf] :81-83, replaced cuBLAS calls).
+ *   C[m, n] = alpha * sum_k A(m, k) * B(n, k)      (float32 accumulation)
+ * a_kmajor != 0: A(m,k) = A[m*lda + k]  (row-major [M,K]);
+ *          == 0: A(m,k) = A[k*lda + m]  (row-major [K,M]).
+ * b_kmajor != 0: B(n,k) = B[n*ldb + k]  (row-major [N,K], i.e. nn.Linear's W);
+ *          == 0: B(n,k) = B[k*ldb + n]  (row-major [K,N]).
+ * epilogue: ALODLM_EPI_STORE    C = alpha*acc                (C in dtype)
+ *           ALODLM_EPI_RESIDUAL C = R + cast(alpha*acc)       (C, R in dtype; may alias)
+ *           ALODLM_EPI_ACCUM    Cf32 += alpha*acc             (C is float)
+ * workspace: float scratch of alodlm_gemm_workspace(M, N, K, flags) floats for
+ * split-K reductions of ALODLM_EPI_ACCUM (may be NULL when that is 0).
+ * ------------------------------------------------------------------------ */
+enum { ALODLM_EPI_STORE = 0, ALODLM_EPI_RESIDUAL = 1, ALODLM_EPI_ACCUM = 2 };
+int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype);
+int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb,
+                int b_kmajor, void* C, int64_t ldc, const void* R, int64_t ldr, int64_t M,
+                int64_t N, int64_t K, float alpha, int epilogue, int dtype, float* workspace,
+                void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GQA attention under the dual-stream training mask (alodlm/model.py:62-73
+ * with the mask of alodlm/batch.py:23-31, or equivalently the range plan of
+ * alodlm/attention.py:12-30).  q: [rows, nq*dh]; k: [rows, nkv*dh];
+ * v: rows of stride ldv; o: [rows, nq*dh]; lse: float [nq, rows].
+ * Segment s spans dual-stream rows [bounds[s], bounds[s+1]) (clean half
+ * first); row_segment[r] = s.  Scale is dh^-0.5.
+ * bwd: dq [rows, nq*dh], dk [rows, nkv*dh], dv (stride lddv) from do.
+ * `workspace` holds alodlm_attention_bwd_workspace(rows, nq) floats.
+ * ------------------------------------------------------------------------ */
+int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
+                         const int64_t* bounds, const int32_t* row_segment, void* o,
+                         float* lse, int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
+                         int64_t block_size, int dtype, void* stream);
+int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq);
+int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
+                         const void* o, const float* lse, const void* dout,
+                         const int64_t* bounds, const int32_t* row_segment, void* dq,
+                         void* dk, void* dv, int64_t lddv, float* workspace, int64_t rows,
+                         int64_t nq, int64_t nkv, int64_t dh, int64_t block_size, int dtype,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * SwiGLU ([tf] modeling_qwen3.py:81-83): gu = [gate | up] of width 2*inter;
+ * fwd act = cast(cast(silu(gate)) * up); bwd dgu from dact.
+ * ------------------------------------------------------------------------ */
+int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_t inter, int dtype,
+                      void* stream);
+int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, int64_t rows, int64_t inter,
+                      int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Readout and halting (alodlm/model.py:152-168).
+ * final_norm_gate: readout = norm(x) (the model's final RMSNorm, weight wf)
+ *   and gate[r] = (readout . gate_w + gate_b) + depth_bias[depth]
+ *   (GateHead.forward, model.py:37-38), rounded like the reference; gate is
+ *   stored as float.  rstd: float [rows].
+ * carry_select: at depth d >= 1, out[r] = table[original[r]] if exits[r] <= d
+ *   (re-embedding, model.py:153-154) else norm(x)[r] (the carry, model.py:168);
+ *   writes rstd of the carry norm.
+ * exit_update (model.py:163-167): for d < K-1, exits[r] = d+1 where
+ *   u[r] < sigmoid(gate[r]) and masked[r] and exits[r] == K.
+ * ------------------------------------------------------------------------ */
+int alodlm_final_norm_gate(const void* x, const void* wf, const void* gate_w,
+                           const void* gate_b, const void* depth_bias, int64_t depth,
+                           void* readout, float* rstd, float* gate, int64_t rows,
+                           int64_t hidden, float eps, int dtype, void* stream);
+int alodlm_carry_select(const void* x, const void* wf, const void* table,
+                        const int64_t* original, const int32_t* exits, int64_t depth,
+                        void* out, float* rstd, int64_t rows, int64_t hidden, int64_t vocab,
+                        float eps, int dtype, void* stream);
+/* Backward of carry_select at depth d: rows with exits <= d add dy into
+ * dtable[original] (float); the others go through the carry norm:
+ * dx = dres + norm'(x) . dy, dwf_accum += ... (workspace as rmsnorm_bwd);
+ * re-embedded rows get dx = dres. */
+int alodlm_carry_select_bwd(const void* dy, const void* x, const float* rstd, const void* wf,
+                            const int32_t* exits, int64_t depth, const int64_t* original,
+                            const void* dres, void* dx, float* dwf_accum, float* dtable,
+                            float* workspace, int64_t rows, int64_t hidden, int64_t vocab,
+                            int dtype, void* stream);
+int alodlm_exit_update(const float* gate, const float* uniforms, const uint8_t* masked,
+                       int32_t* exits, int64_t depth, int64_t max_depth, int64_t rows,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Readout row selection for depth d (model.py:180-184; loss.py:12-32):
+ * a row carries loss at depth d if it is masked and not yet exited before d
+ * (target original[r], coefficient dL/dce = 0.5 * w_r * stick[d, r], from
+ * loss.py:55-61) or it is a clean row with an autoregressive target
+ * (target ar_target[r] >= 0, coefficient ar_coef).  Writes the selected row
+ * indices in ascending order, their targets and coefficients, and the count
+ * (device int32).  gates: float [K, rows]; wsum: device float holding
+ * sum over masked rows of 1/(p+1e-8).
+ * ------------------------------------------------------------------------ */
+int alodlm_select_rows(const uint8_t* masked, const int32_t* exits, const int64_t* original,
+                       const int32_t* ar_target, const float* gates, const float* mask_prob,
+                       const float* wsum, float ar_coef, int64_t depth, int64_t max_depth,
+                       int64_t rows, int32_t* sel_rows, int32_t* sel_target, float* sel_coef,
+                       int32_t* sel_count, void* stream);
+int alodlm_inverse_weight_sum(const uint8_t* masked, const float* mask_prob, int64_t rows,
+                              float* wsum, void* stream);
+
+/* Row gather/scatter between the full [rows, H] stream and the selected rows. */
+int alodlm_gather_rows(const void* src, const int32_t* sel_rows, int64_t n_sel, void* dst,
+                       int64_t hidden, int dtype, void* stream);
+int alodlm_scatter_rows(const void* src, const int32_t* sel_rows, int64_t n_sel, void* dst,
+                        int64_t rows, int64_t hidden, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Cross-entropy over the vocabulary for the selected rows (F.cross_entropy
+ * at model.py:180 and loss.py:24-25), fused with token entropy:
+ * logits [n, V] (dtype) -> ce[n] = lse - logit[target] (rounded to dtype like
+ * the reference's CE output), entropy[n] = lse - sum p*logit, and in place
+ * logits <- coef * (softmax - onehot(target)), i.e. dL/dlogits per unit of
+ * upstream gradient.  Rows beyond n_rows (device count) are untouched.
+ * ------------------------------------------------------------------------ */
+int alodlm_cross_entropy(void* logits, const int32_t* target, const float* coef,
+                         const int32_t* n_rows, int64_t max_rows, int64_t vocab, float* ce,
+                         float* entropy, int dtype, void* stream);
+/* Scatter ce of the selected rows into ce_full[depth, rows]. */
+int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n_rows,
+                      int64_t max_rows, float* ce_full, int64_t rows, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Objective (alodlm/loss.py:35-90, alodlm/credit.py:7-40, model.py:183-187).
+ * Inputs over all rows: gates [K, rows], exits, masked, mask_prob,
+ * ce_full [K, rows] (valid where masked and d < z), ar_ce [K, rows]
+ * (valid where ar_target >= 0), row_segment, bounds [S+1].
+ * out[0..9] = total, denoising, actor, sampled_mean_depth, prediction_cost,
+ *   regularization_cost, profile_mean_depth, first_pass_halt_probability,
+ *   ar_loss, masked_count.
+ * dgate [K, rows] = d total / d gate (unit upstream gradient).
+ * One workgroup; `workspace` holds alodlm_objective_workspace(rows, S, K) floats.
+ * ------------------------------------------------------------------------ */
+int64_t alodlm_objective_workspace(int64_t rows, int64_t n_segments, int64_t max_depth);
+int alodlm_objective(const float* gates, const int32_t* exits, const uint8_t* masked,
+                     const float* mask_prob, const float* ce_full, const float* ar_ce,
+                     const int32_t* ar_target, const int64_t* bounds, int64_t n_segments,
+                     int64_t rows, int64_t max_depth, float depth_prior_c, float kl_beta_mi,
+                     float kl_beta_marg, float* out, float* dgate, float* workspace,
+                     void* stream);
+
+/* Gate-head backward (GateHead.forward, model.py:37-38, differentiated):
+ * gw_accum[H] += scale * sum_r dgate[r]*readout[r]; gb_accum[0] and
+ * gdb_accum[depth] += scale * sum_r dgate[r].  `workspace` holds
+ * alodlm_gate_bwd_workspace(rows, hidden) floats. */
+int64_t alodlm_gate_bwd_workspace(int64_t rows, int64_t hidden);
+int alodlm_gate_bwd(const float* dgate, const void* readout, float scale, float* gw_accum,
+                    float* gb_accum, float* gdb_accum, int64_t depth, int64_t rows,
+                    int64_t hidden, float* workspace, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Optimizer (torch.nn.utils.clip_grad_norm_ and torch.optim.AdamW as called
+ * at alodlm/train.py:49,140,143).  The tensor list is given by device arrays
+ * of per-tensor pointers and numels and a chunk table: chunk c covers
+ * elements [chunk_start[c], chunk_start[c] + chunk_size) of tensor
+ * chunk_tensor[c].
+ * grad_norm: total_norm[0] = sqrt(sum g^2); `partial` holds n_chunks floats.
+ * adamw: decoupled decay p *= 1 - lr*wd[t], then Adam with bias correction
+ * for `step` (>= 1) on the float master; m and v float; the dtype param is
+ * rewritten from the master when it is a separate tensor.  If total_norm is
+ * not NULL the gradient is scaled by min(1, max_norm/(total_norm+1e-6)),
+ * read on the device.
+ * ------------------------------------------------------------------------ */
+int alodlm_grad_norm(const void* const* grads, const int32_t* chunk_tensor,
+                     const int64_t* chunk_start, const int64_t* numels, int64_t n_chunks,
+                     int64_t chunk_size, int dtype, float* partial, float* total_norm,
+                     void* stream);
+int alodlm_adamw(void* const* params, float* const* master, float* const* exp_avg,
+                 float* const* exp_avg_sq, const void* const* grads,
+                 const int32_t* chunk_tensor, const int64_t* chunk_start, const int64_t* numels,
+                 const float* weight_decay, int64_t n_chunks, int64_t chunk_size,
+                 const float* total_norm, float max_norm, float lr, float beta1, float beta2,
+                 float eps, int64_t step, int dtype, void* stream);
+
+/* Elementwise helpers. */
+int alodlm_cast_f32(const float* src, void* dst, int64_t n, int dtype, void* stream);
+int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALODLM_HIP_H */

@@ -368,7 +368,16 @@ def outcome_loss(ce, gates, exits, masked, mask_probability, packed_boundaries, 
     return denoising + actor, metrics
 
 
-def autoregressive_loss(logits, labels, packed_boundaries):
+def _round_through(x, dtype):
+    """Round values to `dtype` (gradient passes unchanged), as a CE evaluated in
+    that dtype returns them (alodlm/model.py:180 and alodlm/loss.py:24 run
+    F.cross_entropy in the parameter dtype)."""
+    if dtype is None:
+        return x
+    return x + (x.to(dtype).to(x.dtype) - x).detach()
+
+
+def autoregressive_loss(logits, labels, packed_boundaries, ce_dtype=None):
     """Count-weighted next-token CE on each segment's clean stream (alodlm/loss.py:12-32)."""
     labels = torch.as_tensor(labels)
     total = logits.new_zeros(())
@@ -384,27 +393,32 @@ def autoregressive_loss(logits, labels, packed_boundaries):
             continue
         token = F.cross_entropy(logits[start:start + length - 1], targets,
                                 reduction="none", ignore_index=-100)
-        total = total + token.sum()
+        total = total + _round_through(token, ce_dtype).sum()
         count += n
     if count:
         return total / count
     return logits.new_zeros((), requires_grad=True)
 
 
-def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms):
+def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms, ce_dtype=None):
     """The full ALoDLM._forward_loss (alodlm/model.py:176-187) from explicit draws.
 
+    ``ce_dtype`` (e.g. torch.bfloat16) rounds every per-token cross-entropy to
+    that dtype, as the reference's bf16 run does; None keeps full precision.
     Returns (total loss, metrics dict, extras dict with batch/gates/exits/ce).
     """
     batch = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id, draws)
     logits, gates, exits = rollout(p, batch, dims, cfg, exit_uniforms)
+    logits = [_round_through(lg, ce_dtype) for lg in logits]  # bf16 LM-head output
     masked = torch.as_tensor(batch["masked"])
     original = torch.as_tensor(batch["original"])
-    ce = torch.stack([F.cross_entropy(lg[masked], original[masked], reduction="none")
+    ce = torch.stack([_round_through(F.cross_entropy(lg[masked], original[masked],
+                                                     reduction="none"), ce_dtype)
                       for lg in logits])
     den_actor, metrics = outcome_loss(ce, gates, exits, masked, batch["mask_probability"],
                                       batch["boundaries"], cfg)
-    ar = torch.stack([autoregressive_loss(lg, labels, batch["boundaries"]) for lg in logits]).mean()
+    ar = torch.stack([autoregressive_loss(lg, labels, batch["boundaries"], ce_dtype)
+                      for lg in logits]).mean()
     total = (den_actor + ar) / 2
     total = total + 0.0 * sum(t.sum() for t in logits + gates)
     metrics = {**metrics, "ar_loss": ar.detach(), "loss": total.detach()}

@@ -1,0 +1,56 @@
+"""The C ABI: every entry point declared in include/alodlm_hip.h is exported by
+the built library and bound in alodlm_amd._lib with the same arity (no GPU
+work is launched here)."""
+
+import ctypes
+from pathlib import Path
+import re
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "alodlm_hip.h"
+
+
+def declarations():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for ret, name, args in re.findall(r"(int64_t|int|const char\*)\s+(alodlm_\w+)\(([^;]*?)\);", text):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_header_declares_entry_points():
+    decls = declarations()
+    assert len(decls) >= 30
+    assert "alodlm_gemm" in decls and "alodlm_attention_fwd" in decls
+
+
+def test_library_exports_every_declared_symbol():
+    from alodlm_amd import _lib
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built (run python -m alodlm_amd.build)")
+    lib = ctypes.CDLL(str(_lib.LIBRARY))
+    for name in declarations():
+        assert hasattr(lib, name), name
+
+
+def test_bindings_match_header_arity():
+    from alodlm_amd import _lib
+    decls = declarations()
+    assert set(decls) == set(_lib.SIGNATURES), set(decls) ^ set(_lib.SIGNATURES)
+    for name, nargs in decls.items():
+        assert len(_lib.SIGNATURES[name]) == nargs, name
+
+
+def test_library_loads_and_reports_abi():
+    from alodlm_amd import _lib
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    lib = _lib.load()
+    assert lib.alodlm_abi_version() == _lib.ABI_VERSION
+    # argument validation runs on the host and returns ALODLM_EINVAL without a GPU
+    with pytest.raises(ValueError):
+        _lib.call("alodlm_objective", None, None, None, None, None, None, None, None, 1, 4, 99,
+                  0.4, 0.1, 1.0, None, None, None, None)

@@ -1,0 +1,316 @@
+"""Kernel-level parity of the HIP library against float64 references on the CPU.
+
+Each test calls the C ABI through alodlm_amd._lib on seeded inputs and checks
+the result against the oracle's arithmetic (or a torch float64 product for the
+GEMM).  bf16 tolerances are stated per test.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import step as O
+from tests.helpers import log
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def lib():
+    from alodlm_amd import _lib
+    _lib.load()
+    return _lib
+
+
+def st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+GEMM_CASES = [
+    # (M, N, K, a_kmajor, b_kmajor, dtype)
+    (256, 256, 128, 1, 1, torch.bfloat16),
+    (200, 136, 64, 1, 1, torch.bfloat16),
+    (384, 128, 320, 1, 0, torch.bfloat16),
+    (128, 264, 192, 0, 1, torch.bfloat16),
+    (256, 512, 1000, 0, 0, torch.bfloat16),
+    (96, 80, 40, 1, 0, torch.bfloat16),
+    (70, 33, 19, 0, 0, torch.float32),
+    (130, 65, 48, 1, 1, torch.float32),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ak,bk,dtype", GEMM_CASES)
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_layouts_and_epilogues(M, N, K, ak, bk, dtype, epi):
+    L = lib()
+    log(f"gemm M={M} N={N} K={K} ak={ak} bk={bk} {dtype} epi={epi}")
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(N, K, generator=g).to(dtype)
+    Ad = (A if ak else A.T.contiguous()).to(DEV)
+    Bd = (B if bk else B.T.contiguous()).to(DEV)
+    lda = K if ak else M
+    ldb = K if bk else N
+    ref = A.double() @ B.double().T * 0.5
+    R = torch.randn(M, N, generator=g).to(dtype)
+    if epi == 2:
+        C = torch.randn(M, N, generator=g).float().to(DEV)
+        expected = C.cpu().double() + ref
+        ws_n = L.query("alodlm_gemm_workspace", M, N, K, epi, L.dtype_code(dtype))
+        ws = torch.empty(max(ws_n, 1), dtype=torch.float32, device=DEV)
+    else:
+        C = torch.empty(M, N, dtype=dtype, device=DEV)
+        ws = None
+        expected = ref if epi == 0 else R.double() + ref.to(dtype).double()
+    Rd = R.to(DEV)
+    L.call("alodlm_gemm", L.ptr(Ad), lda, ak, L.ptr(Bd), ldb, bk, L.ptr(C), N, L.ptr(Rd), N, M,
+           N, K, 0.5, epi, L.dtype_code(dtype), L.ptr(ws), st())
+    torch.cuda.synchronize()
+    out = C.cpu().double()
+    scale = ref.abs().max().item() + 1e-6
+    tol = 1e-5 if (dtype == torch.float32 or epi == 2) else 8e-3
+    err = (out - expected).abs().max().item() / scale
+    assert err <= tol, f"max rel err {err}"
+
+
+def test_gemm_splitk_accumulates_large_k():
+    """dW-shaped product (both operands m/n-contiguous, K = 8192 rows) uses split-K."""
+    L = lib()
+    M, N, K = 256, 384, 8192
+    log(f"gemm splitk M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(5)
+    dY = torch.randn(K, M, generator=g).to(torch.bfloat16)
+    X = torch.randn(K, N, generator=g).to(torch.bfloat16)
+    C = torch.ones(M, N, dtype=torch.float32, device=DEV)
+    need = L.query("alodlm_gemm_workspace", M, N, K, 2, 1)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.float32, device=DEV)
+    dYd, Xd = dY.to(DEV), X.to(DEV)  # named: the pointers must outlive the call
+    L.call("alodlm_gemm", L.ptr(dYd), M, 0, L.ptr(Xd), N, 0, L.ptr(C), N, None, 0,
+           M, N, K, 1.0, 2, 1, L.ptr(ws), st())
+    torch.cuda.synchronize()
+    ref = 1.0 + dY.double().T @ X.double()
+    err = (C.cpu().double() - ref).abs().max().item() / ref.abs().max().item()
+    assert err < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(37, 256), (64, 2048), (5, 100)])
+def test_rmsnorm_fwd_bwd(dtype, rows, cols):
+    L = lib()
+    log(f"rmsnorm rows={rows} cols={cols} {dtype}")
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).to(dtype)
+    dy = torch.randn(rows, cols, generator=g).to(dtype)
+    dres = torch.randn(rows, cols, generator=g).to(dtype)
+    xd, wd, dyd, dresd = (t.to(DEV) for t in (x, w, dy, dres))
+    y = torch.empty_like(xd)
+    rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
+    code = L.dtype_code(dtype)
+    L.call("alodlm_rmsnorm_fwd", L.ptr(xd), L.ptr(wd), L.ptr(y), L.ptr(rstd), rows, cols, 1e-6,
+           code, st())
+    dx = torch.empty_like(xd)
+    dw = torch.zeros(cols, dtype=torch.float32, device=DEV)
+    ws = torch.empty(L.query("alodlm_rmsnorm_bwd_workspace", rows, cols), dtype=torch.float32,
+                     device=DEV)
+    L.call("alodlm_rmsnorm_bwd", L.ptr(dyd), L.ptr(xd), L.ptr(rstd), L.ptr(wd), L.ptr(dresd),
+           L.ptr(dx), L.ptr(dw), L.ptr(ws), rows, cols, code, st())
+    torch.cuda.synchronize()
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    yr = O.rmsnorm(xr, wr, 1e-6)
+    gx, gw = torch.autograd.grad(yr, (xr, wr), dy.double())
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(y.cpu().double(), yr.detach(), rtol=tol, atol=tol)
+    torch.testing.assert_close(dx.cpu().double(), gx + dres.double(), rtol=tol, atol=tol * 4)
+    torch.testing.assert_close(dw.cpu().double(), gw, rtol=tol, atol=tol * math.sqrt(rows))
+
+
+def _dual_stream(bounds_tokens, block, seed):
+    """Random dual-stream positions for a pack (clean positions 0..L-1, noisy
+    positions a per-block permutation)."""
+    g = torch.Generator().manual_seed(seed)
+    pos, seg = [], []
+    for s, (a, b) in enumerate(zip(bounds_tokens, bounds_tokens[1:])):
+        L = b - a
+        pos.append(torch.arange(L))
+        noisy = []
+        for left in range(0, L, block):
+            right = min(left + block, L)
+            noisy.append(left + torch.randperm(right - left, generator=g))
+        pos.append(torch.cat(noisy))
+        seg += [s] * (2 * L)
+    packed = [2 * v for v in bounds_tokens]
+    return torch.cat(pos), torch.tensor(seg, dtype=torch.int32), torch.tensor(packed)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nq,nkv,dh,bounds,block", [
+    (4, 2, 64, [0, 40, 41, 100], 8),
+    (2, 1, 128, [0, 64, 160], 32),
+    (4, 4, 8, [0, 7, 20], 3),
+])
+def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block):
+    """Attention (dual-stream mask) with q/k norm + rotary, forward and backward,
+    against autograd through the oracle's restatement in float64."""
+    L = lib()
+    log(f"attention nq={nq} nkv={nkv} dh={dh} bounds={bounds} block={block} {dtype}")
+    g = torch.Generator().manual_seed(dh + nq)
+    positions, row_seg, packed = _dual_stream(bounds, block, dh)
+    N = len(positions)
+    W = (nq + 2 * nkv) * dh
+    qkv = torch.randn(N, W, generator=g).to(dtype)
+    wq = (1 + 0.2 * torch.randn(dh, generator=g)).to(dtype)
+    wk = (1 + 0.2 * torch.randn(dh, generator=g)).to(dtype)
+    dout = torch.randn(N, nq * dh, generator=g).to(dtype)
+    code = L.dtype_code(dtype)
+    theta = 1e4
+    inv = (1.0 / (theta ** (torch.arange(0, dh, 2, dtype=torch.float32) / dh))).to(DEV)
+    qkv_d, wq_d, wk_d = qkv.to(DEV), wq.to(DEV), wk.to(DEV)
+    pos_d, seg_d, bnd_d = positions.to(DEV), row_seg.to(DEV), packed.to(DEV)
+    q = torch.empty(N, nq * dh, dtype=dtype, device=DEV)
+    k = torch.empty(N, nkv * dh, dtype=dtype, device=DEV)
+    L.call("alodlm_qknorm_rope_fwd", L.ptr(qkv_d), L.ptr(wq_d), L.ptr(wk_d), L.ptr(pos_d),
+           L.ptr(inv), L.ptr(q), L.ptr(k), N, nq, nkv, dh, 1e-6, code, st())
+    v = qkv_d[:, (nq + nkv) * dh:]
+    o = torch.empty(N, nq * dh, dtype=dtype, device=DEV)
+    lse = torch.empty(nq, N, dtype=torch.float32, device=DEV)
+    L.call("alodlm_attention_fwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(bnd_d), L.ptr(seg_d),
+           L.ptr(o), L.ptr(lse), N, nq, nkv, dh, block, code, st())
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dqkv = torch.zeros(N, W, dtype=dtype, device=DEV)
+    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq), dtype=torch.float32,
+                     device=DEV)
+    dout_d = dout.to(DEV)
+    L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
+           L.ptr(dout_d), L.ptr(bnd_d), L.ptr(seg_d), L.ptr(dq), L.ptr(dk),
+           L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block, code, st())
+    dwq = torch.zeros(dh, dtype=torch.float32, device=DEV)
+    dwk = torch.zeros(dh, dtype=torch.float32, device=DEV)
+    ws2 = torch.empty(L.query("alodlm_qknorm_rope_bwd_workspace", N, nq, nkv, dh) * 2 + 16,
+                      dtype=torch.float32, device=DEV)
+    L.call("alodlm_qknorm_rope_bwd", L.ptr(dq), L.ptr(dk), L.ptr(qkv_d), L.ptr(wq_d), L.ptr(wk_d),
+           L.ptr(pos_d), L.ptr(inv), L.ptr(dqkv), L.ptr(dwq), L.ptr(dwk), L.ptr(ws2), N, nq, nkv,
+           dh, 1e-6, code, st())
+    torch.cuda.synchronize()
+    # float64 reference through the oracle's formulas
+    X = qkv.double().requires_grad_(True)
+    WQ = wq.double().requires_grad_(True)
+    WK = wk.double().requires_grad_(True)
+    qr = O.rmsnorm(X[:, :nq * dh].reshape(N, nq, dh), WQ, 1e-6)
+    kr = O.rmsnorm(X[:, nq * dh:(nq + nkv) * dh].reshape(N, nkv, dh), WK, 1e-6)
+    cos, sin = O.rope_tables(positions, dh, theta, torch.float64)
+    rot = lambda t: torch.cat((-t[..., dh // 2:], t[..., :dh // 2]), -1)
+    qr = qr * cos[:, None] + rot(qr) * sin[:, None]
+    kr = kr * cos[:, None] + rot(kr) * sin[:, None]
+    vr = X[:, (nq + nkv) * dh:].reshape(N, nkv, dh)
+    mask = torch.as_tensor(O.packed_attention_mask(packed, block))
+    heads = []
+    for h in range(nq):
+        s = (qr[:, h] @ kr[:, h // (nq // nkv)].T) * dh ** -0.5
+        heads.append(torch.softmax(s.masked_fill(~mask, float("-inf")), -1) @ vr[:, h // (nq // nkv)])
+    ref_o = torch.stack(heads, 1).reshape(N, nq * dh)
+    gX, gWQ, gWK = torch.autograd.grad(ref_o, (X, WQ, WK), dout.double())
+    tol = 2e-5 if dtype == torch.float32 else 3e-2
+    torch.testing.assert_close(q.cpu().double(), qr.detach().reshape(N, -1), rtol=tol, atol=tol)
+    torch.testing.assert_close(o.cpu().double(), ref_o.detach(), rtol=tol, atol=tol)
+    scale = gX.abs().max().item()
+    assert (dqkv.cpu().double() - gX).abs().max().item() <= tol * 2 * scale
+    sw = max(gWQ.abs().max().item(), gWK.abs().max().item())
+    assert (dwq.cpu().double() - gWQ).abs().max().item() <= tol * 2 * sw
+    assert (dwk.cpu().double() - gWK).abs().max().item() <= tol * 2 * sw
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cross_entropy_rows(dtype):
+    L = lib()
+    R, V = 37, 1000
+    log(f"cross_entropy R={R} V={V} {dtype}")
+    g = torch.Generator().manual_seed(9)
+    logits = (3 * torch.randn(R, V, generator=g)).to(dtype)
+    target = torch.randint(0, V, (R,), generator=g, dtype=torch.int32)
+    coef = torch.rand(R, generator=g)
+    ld = logits.to(DEV).contiguous()
+    count = torch.tensor([R - 3], dtype=torch.int32, device=DEV)
+    ce = torch.zeros(R, dtype=torch.float32, device=DEV)
+    ent = torch.zeros(R, dtype=torch.float32, device=DEV)
+    target_d, coef_d = target.to(DEV), coef.to(DEV)
+    L.call("alodlm_cross_entropy", L.ptr(ld), L.ptr(target_d), L.ptr(coef_d),
+           L.ptr(count), R, V, L.ptr(ce), L.ptr(ent), L.dtype_code(dtype), st())
+    torch.cuda.synchronize()
+    x = logits.double()[:R - 3]
+    ref_ce = F.cross_entropy(x, target[:R - 3].long(), reduction="none")
+    p = torch.softmax(x, -1)
+    ref_ent = -(p * torch.log_softmax(x, -1)).sum(-1)
+    grad = coef[:R - 3, None].double() * (p - F.one_hot(target[:R - 3].long(), V).double())
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(ce.cpu()[:R - 3].double(), ref_ce, rtol=tol, atol=tol)
+    torch.testing.assert_close(ent.cpu()[:R - 3].double(), ref_ent, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(ld.cpu()[:R - 3].double(), grad, rtol=tol, atol=tol * 0.01)
+    torch.testing.assert_close(ld.cpu()[R - 3:], logits[R - 3:])  # rows past the count untouched
+
+
+@pytest.mark.parametrize("K,depths", [(3, [1, 2, 3, 2]), (4, [4, 1, 3, 2])])
+def test_objective_kernel_matches_oracle(K, depths):
+    """The objective kernel against the oracle's outcome loss (itself pinned by
+    the reference's analytic restatement, test_objective.py:32-74)."""
+    L = lib()
+    log(f"objective K={K}")
+    cfg = O.Objective(max_depth=K, gate_init_pi=(1 / K,) * K)
+    base = [[3., 4., 5., 6.], [2., 3., 3., 4.], [1., 2., 2., 3.], [1.5, .5, 2.5, 1.]]
+    # embed the 4 masked rows in 9 rows with 3 segments; rows 0,1,5 are AR rows
+    rows = 9
+    masked = torch.zeros(rows, dtype=torch.bool)
+    mrows = [2, 3, 6, 8]
+    masked[mrows] = True
+    ce_m = torch.tensor(base[:K], dtype=torch.float64, requires_grad=True)
+    gates_m = torch.tensor([[-.4, .2, -.3, .7], [.1, -.6, .9, .0], [.3, .3, -.2, -.8],
+                            [0., 0., 0., 0.]][:K], dtype=torch.float64, requires_grad=True)
+    gates_full = torch.zeros(K, rows, dtype=torch.float64)
+    gates_full[:, mrows] = gates_m.detach()
+    gates_full[:, [0, 1]] = 0.3
+    ce_full = torch.zeros(K, rows, dtype=torch.float64)
+    ce_full[:, mrows] = ce_m.detach()
+    ar_target = torch.full((rows,), -1, dtype=torch.int32)
+    ar_target[[0, 1, 5]] = 7
+    ce_full[:, [0, 1, 5]] = torch.tensor([[1.0, 2.0, 3.0]] * K, dtype=torch.float64)
+    exits = torch.full((rows,), K, dtype=torch.int64)
+    exits[mrows] = torch.tensor(depths)
+    prob = torch.zeros(rows)
+    prob[mrows] = torch.tensor([.2, .4, .5, .8])
+    bounds = torch.tensor([0, 4, 7, 9])
+    # oracle (float64)
+    gate_list = [gates_full[d].clone() for d in range(K)]
+    for d in range(K):
+        gate_list[d] = gate_list[d].index_put((torch.tensor(mrows),), gates_m[d])
+    ref, metrics = O.outcome_loss(ce_m, gate_list, exits, masked, prob.double(), bounds, cfg)
+    ar = ce_full[:, [0, 1, 5]].sum() / (3 * K)
+    total = (ref + ar) / 2
+    dg = torch.autograd.grad(total, gates_m)[0]
+    out = torch.zeros(10, dtype=torch.float32, device=DEV)
+    dgate = torch.zeros(K, rows, dtype=torch.float32, device=DEV)
+    ws = torch.empty(L.query("alodlm_objective_workspace", rows, 3, K), dtype=torch.float32,
+                     device=DEV)
+    cfd = ce_full.float().to(DEV)
+    gd, ed, md, pd = (gates_full.float().to(DEV), exits.int().to(DEV), masked.to(DEV),
+                      prob.to(DEV))
+    ad, bd = ar_target.to(DEV), bounds.to(DEV)
+    L.call("alodlm_objective", L.ptr(gd), L.ptr(ed), L.ptr(md), L.ptr(pd), L.ptr(cfd), L.ptr(cfd),
+           L.ptr(ad), L.ptr(bd), 3, rows, K, cfg.depth_prior_c,
+           cfg.kl_beta_mi, cfg.kl_beta_marg, L.ptr(out), L.ptr(dgate), L.ptr(ws), st())
+    torch.cuda.synchronize()
+    out = out.cpu().double()
+    assert abs(out[0] - total.item()) < 1e-5 * max(1, abs(total.item()))
+    names = ["denoising", "actor", "sampled_mean_depth", "prediction_cost",
+             "regularization_cost", "profile_mean_depth", "first_pass_halt_probability"]
+    for i, name in enumerate(names, 1):
+        assert abs(out[i] - metrics[name].item()) < 1e-5 * max(1, abs(metrics[name].item())), name
+    assert abs(out[8] - ar.item()) < 1e-6
+    torch.testing.assert_close(dgate.cpu().double()[:, mrows], dg, rtol=1e-5, atol=1e-7)
+    assert (dgate.cpu()[:, [0, 1, 4, 5, 7]] == 0).all()

@@ -1,0 +1,177 @@
+"""Full training-step parity on the GPU.
+
+* micro (the reference's tests/helpers.tiny_model, float32): loss, metrics,
+  gates, exits and every gradient against the reference's golden vectors.
+* tiny training-step configuration (hidden 256, 4 layers 1/2/1, 4 x 128
+  tokens), float32: against the reference's golden vectors and the oracle,
+  loss within 1e-5 relative.
+* the same configuration in bf16: loss within 1e-2 relative and gradient
+  cosine >= 0.999 against the float64 oracle run on the same bf16 weights;
+  masks and exits bit-exact.
+The draws (masking uniforms and permutations, exit uniforms) are consumed from
+the CPU generator in the reference's order and replayed on the GPU.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import step as O
+from tests import golden
+from tests.helpers import (cosine, cpu_draws, log, make_model, oracle_draws, oracle_name)
+
+pytestmark = pytest.mark.gpu
+
+MICRO = (O.Dims(hidden=32, heads=4, kv_heads=2, head_dim=8, intermediate=64, vocab=64, layers=3,
+                eps=1e-6, theta=1e4),
+         O.Objective(loop_start=1, loop_end=2, mask_token_id=3, block_size=4))
+TINY = (O.Dims(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=768, vocab=1024,
+               layers=4, eps=1e-6, theta=1e6),
+        O.Objective(loop_start=1, loop_end=3, mask_token_id=3, block_size=32))
+
+
+def _golden_name(name):
+    return name if name.startswith("exit_gate.") else "backbone." + name
+
+
+def _run_engine(model, ids, labels, bounds, draws, uniforms):
+    engine = model.engine()
+    out, state = engine.forward(ids.cuda(), labels.cuda(), bounds, True,
+                                exit_uniforms=[u.cuda() for u in uniforms], draws=draws)
+    grads = engine.backward(state, 1.0)
+    torch.cuda.synchronize()
+    named = {n: engine.arena.view(grads, n).cpu() for n in engine.arena.names}
+    return out.cpu().double(), state, named
+
+
+def _check_batch(state, g):
+    b = state["batch"]
+    np.testing.assert_array_equal(b.ids.cpu().numpy(), g["ids"])
+    np.testing.assert_array_equal(b.original.cpu().numpy(), g["original"])
+    np.testing.assert_array_equal(b.positions.cpu().numpy(), g["positions"])
+    np.testing.assert_array_equal(b.masked.cpu().numpy(), g["masked"])
+    np.testing.assert_array_equal(b.mask_probability.cpu().numpy(), g["mask_probability"])
+    np.testing.assert_array_equal(b.boundaries.cpu().numpy(), g["boundaries"])
+
+
+METRICS = ["denoising", "actor", "sampled_mean_depth", "prediction_cost", "regularization_cost",
+           "profile_mean_depth", "first_pass_halt_probability", "ar_loss"]
+
+
+@pytest.mark.parametrize("case", ["step_micro", "step_micro_ragged"])
+def test_micro_step_matches_reference_golden(case):
+    log(f"micro step {case}")
+    g = golden.load(case)
+    dims, obj = MICRO
+    params = {n: torch.as_tensor(g["param_" + _golden_name(n)]) for n in O.param_names(dims)}
+    model = make_model(dims, obj, params)
+    labels = torch.as_tensor(g["in_labels"])
+    draws, uniforms = cpu_draws(labels, g["in_boundaries"], obj.block_size, int(g["seed"]),
+                                obj.max_depth)
+    out, state, grads = _run_engine(model, torch.as_tensor(g["in_ids"]), labels,
+                                    torch.as_tensor(g["in_boundaries"]), draws, uniforms)
+    _check_batch(state, g)
+    np.testing.assert_array_equal(state["exits"].cpu().numpy(), g["exits"])
+    torch.testing.assert_close(state["gates"].cpu(), torch.as_tensor(g["gates"]), rtol=1e-5,
+                               atol=1e-6)
+    assert abs(out[0] - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
+    for i, key in enumerate(METRICS, 1):
+        ref = float(g["metric_" + key])
+        assert abs(out[i] - ref) <= 1e-5 * max(1.0, abs(ref)), key
+    for name in O.param_names(dims):
+        ref = torch.as_tensor(g["grad_" + _golden_name(name)])
+        torch.testing.assert_close(grads[_golden_name(name)], ref, rtol=1e-4, atol=1e-6,
+                                   msg=name)
+
+
+def test_micro_step_autograd_path_fills_grads():
+    """model(**item) + loss.backward() (alodlm/train.py:135,138) gives the engine's grads."""
+    log("micro step autograd")
+    g = golden.load("step_micro")
+    dims, obj = MICRO
+    params = {n: torch.as_tensor(g["param_" + _golden_name(n)]) for n in O.param_names(dims)}
+    model = make_model(dims, obj, params)
+    labels = torch.as_tensor(g["in_labels"])
+    draws, uniforms = cpu_draws(labels, g["in_boundaries"], obj.block_size, int(g["seed"]),
+                                obj.max_depth)
+    loss, metrics = model(torch.as_tensor(g["in_ids"]).cuda(), labels.cuda(),
+                          torch.as_tensor(g["in_boundaries"]),
+                          exit_uniforms=[u.cuda() for u in uniforms], draws=draws)
+    loss.backward()
+    assert abs(float(loss) - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
+    assert set(metrics) == set(METRICS) | {"loss"}
+    for name, p in model.named_parameters():
+        ref = torch.as_tensor(g["grad_" + name])
+        torch.testing.assert_close(p.grad.cpu(), ref, rtol=1e-4, atol=1e-6, msg=name)
+
+
+def _tiny_inputs(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, 1024, (512,), generator=g)
+    return ids, ids.clone(), torch.tensor([0, 128, 256, 384, 512])
+
+
+def test_tiny_fp32_step_matches_reference_golden_and_oracle():
+    log("tiny fp32 step")
+    g = golden.load("step_tiny")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=0)
+    model = make_model(dims, obj, params)
+    ids, labels, bounds = _tiny_inputs()
+    draws, uniforms = cpu_draws(labels, bounds, obj.block_size, 0, obj.max_depth)
+    out, state, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
+    _check_batch(state, g)
+    np.testing.assert_array_equal(state["exits"].cpu().numpy(), g["exits"])
+    assert abs(out[0] - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
+    for i, key in enumerate(METRICS, 1):
+        ref = float(g["metric_" + key])
+        assert abs(out[i] - ref) <= 1e-5 * max(1.0, abs(ref)), key
+    names = list(g["param_names"])
+    for index, gname in enumerate(names):
+        grad = grads[gname].double().flatten()
+        ref_norm = float(g["gnorm_" + gname])
+        assert abs(grad.norm().item() - ref_norm) <= 1e-4 * ref_norm + 1e-9, gname
+        proj = (grad * golden.projection_vector(index, grad.numel())).sum().item()
+        assert abs(proj - float(g["gproj_" + gname])) <= 1e-4 * ref_norm * grad.numel() ** 0.5 + 1e-9
+    # and against the oracle's full gradients
+    p = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    od = oracle_draws(draws, [int(v) for v in bounds], obj.block_size)
+    loss, _, _ = O.step_loss(p, ids, labels, bounds, dims, obj, od, uniforms)
+    loss.backward()
+    for name in O.param_names(dims):
+        mine, ref = grads[_golden_name(name)].double(), p[name].grad.double()
+        scale = ref.abs().max().item() + 1e-12
+        assert (mine - ref).abs().max().item() <= 1e-4 * scale, name
+
+
+def test_tiny_bf16_step_matches_oracle():
+    log("tiny bf16 step")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=0)
+    params = {k: v.to(torch.bfloat16) for k, v in params.items()}
+    model = make_model(dims, obj, {k: v.float() for k, v in params.items()}, dtype=torch.bfloat16)
+    ids, labels, bounds = _tiny_inputs()
+    draws, uniforms = cpu_draws(labels, bounds, obj.block_size, 0, obj.max_depth)
+    out, state, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
+    od = oracle_draws(draws, [int(v) for v in bounds], obj.block_size)
+    # float64 oracle on the same bf16 weights, with the reference's bf16 rounding of
+    # the LM-head logits and per-token CE (the values the actor's credit differences)
+    p = {k: v.double().requires_grad_(True) for k, v in params.items()}
+    loss, metrics, extra = O.step_loss(p, ids, labels, bounds, dims, obj, od, uniforms,
+                                       ce_dtype=torch.bfloat16)
+    loss.backward()
+    np.testing.assert_array_equal(state["exits"].cpu().numpy(), extra["exits"].numpy())
+    np.testing.assert_array_equal(state["batch"].masked.cpu().numpy(), extra["batch"]["masked"])
+    assert abs(out[0] - loss.item()) <= 1e-2 * abs(loss.item())
+    worst = 1.0
+    for name in O.param_names(dims):
+        c = cosine(grads[_golden_name(name)], p[name].grad)
+        worst = min(worst, c)
+        assert c >= 0.999, f"{name}: cosine {c}"
+    # for information: the same comparison without any bf16 rounding in the oracle
+    q = {k: v.double().requires_grad_(True) for k, v in params.items()}
+    exact, _, _ = O.step_loss(q, ids, labels, bounds, dims, obj, od, uniforms)
+    exact.backward()
+    worst_exact = min(cosine(grads[_golden_name(n)], q[n].grad) for n in O.param_names(dims))
+    log(f"tiny bf16: loss {out[0]:.6f} vs {loss.item():.6f} (unrounded {exact.item():.6f}); "
+        f"worst grad cosine {worst:.6f} (unrounded oracle {worst_exact:.6f})")
