@@ -36,10 +36,10 @@ SIGNATURES = {
     "alodlm_qknorm_rope_bwd": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
     "alodlm_gemm_workspace": [I64, I64, I64, I32, I32],
     "alodlm_gemm": [P, I64, I32, P, I64, I32, P, I64, P, I64, I64, I64, I64, F32, I32, I32, P, P],
-    "alodlm_attention_fwd": [P, P, P, I64, P, P, P, P, I64, I64, I64, I64, I64, I32, P],
+    "alodlm_attention_fwd": [P, P, P, I64, P, P, P, I64, P, P, I64, I64, I64, I64, I64, I32, P],
     "alodlm_attention_bwd_workspace": [I64, I64],
-    "alodlm_attention_bwd": [P, P, P, I64, P, P, P, P, P, P, P, P, I64, P, I64, I64, I64, I64,
-                             I64, I32, P],
+    "alodlm_attention_bwd": [P, P, P, I64, P, P, P, P, P, P, I64, P, P, P, I64, P, I64, I64, I64,
+                             I64, I64, I32, P],
     "alodlm_swiglu_fwd": [P, P, I64, I64, I32, P],
     "alodlm_swiglu_bwd": [P, P, P, I64, I64, I32, P],
     "alodlm_final_norm_gate": [P, P, P, P, P, I64, P, P, P, I64, I64, F32, I32, P],

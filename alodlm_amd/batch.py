@@ -39,6 +39,7 @@ class Batch:
     ar_target: torch.Tensor = None
     ar_count: int = 0
     pairs: int = 0
+    tiles: torch.Tensor = None
 
 
 def allowed_pairs(length, block_size):
@@ -156,5 +157,22 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     else:
         mask = plan_to_device(sparse_plan([2 * v for v in offsets], block_size, backend), device)
     pairs = sum(allowed_pairs(b - a, block_size) for a, b in zip(offsets, offsets[1:]))
+    tiles = torch.tensor(attention_tiles(offsets), dtype=torch.int32, device=device).view(-1, 2)
     return Batch(out["ids"], out["original"], out["positions"], out["masked"], out["prob"],
-                 out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count, pairs)
+                 out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count, pairs,
+                 tiles)
+
+
+TILE_ROWS = 128
+
+
+def attention_tiles(offsets):
+    """(segment, in-segment start) of every 128-row tile of each segment's clean
+    and noisy stream; tiles never cross a stream or a segment."""
+    out = []
+    for s, (a, b) in enumerate(zip(offsets, offsets[1:])):
+        length = b - a
+        for stream in (0, length):
+            for start in range(0, length, TILE_ROWS):
+                out += [s, stream + start]
+    return out

@@ -9,6 +9,8 @@
 // Reference kernels (any dtype, any head_dim): one wavefront per (query row,
 // head) in the forward and dQ passes and one per (key row, kv head) in the
 // dK/dV pass; the wavefront spreads head_dim over its lanes.
+#include <initializer_list>
+
 #include "common.h"
 
 #define ATT_MAX_PER_LANE 4  // head_dim <= 256
@@ -236,14 +238,41 @@ static int check_attn(int64_t rows, int64_t nq, int64_t nkv, int64_t dh, int64_t
   return ALODLM_OK;
 }
 
+int fa_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
+                  const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
+                  float* lse, int64_t N, int nq, int nkv, int dh, int B, float scale,
+                  hipStream_t st);
+int fa_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
+                  const float* lse, const float* delta, const bf16_t* dout,
+                  const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
+                  bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int dh,
+                  int B, float scale, hipStream_t st);
+
+// The MFMA kernels take bf16, head_dim 64 or 128, 16-byte aligned rows and a
+// tile table; everything else runs the reference kernels above.
+static bool use_mfma(int dtype, int64_t dh, const int32_t* tiles, int64_t ldv,
+                     std::initializer_list<const void*> ptrs) {
+  if (dtype != ALODLM_BF16 || tiles == nullptr || (dh != 64 && dh != 128) || ldv % 8) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16) return false;
+  return true;
+}
+
 extern "C" int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
-                                    const int64_t* bounds, const int32_t* row_segment, void* o,
-                                    float* lse, int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
+                                    const int64_t* bounds, const int32_t* row_segment,
+                                    const int32_t* tiles, int64_t n_tiles, void* o, float* lse,
+                                    int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
                                     int64_t block_size, int dtype, void* stream) {
   int rc = check_attn(rows, nq, nkv, dh, block_size);
   if (rc) return rc;
   if (rows == 0) return ALODLM_OK;
   const float scale = 1.0f / sqrtf((float)dh);
+  if (use_mfma(dtype, dh, tiles, ldv, {q, k, v, o})) {
+    if (n_tiles == 0) return ALODLM_OK;
+    return fa_fwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, bounds, tiles,
+                         n_tiles, (bf16_t*)o, lse, rows, (int)nq, (int)nkv, (int)dh,
+                         (int)block_size, scale, as_stream(stream));
+  }
   ALODLM_DISPATCH(dtype, T, {
     attn_fwd_ref_kernel<T><<<ceil_div_u(rows * nq, 4), 256, 0, as_stream(stream)>>>(
         (const T*)q, (const T*)k, (const T*)v, ldv, bounds, row_segment, (T*)o, lse, rows, nq,
@@ -257,10 +286,11 @@ extern "C" int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq) { re
 
 extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
                                     const void* o, const float* lse, const void* dout,
-                                    const int64_t* bounds, const int32_t* row_segment, void* dq,
-                                    void* dk, void* dv, int64_t lddv, float* workspace,
-                                    int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
-                                    int64_t block_size, int dtype, void* stream) {
+                                    const int64_t* bounds, const int32_t* row_segment,
+                                    const int32_t* tiles, int64_t n_tiles, void* dq, void* dk,
+                                    void* dv, int64_t lddv, float* workspace, int64_t rows,
+                                    int64_t nq, int64_t nkv, int64_t dh, int64_t block_size,
+                                    int dtype, void* stream) {
   int rc = check_attn(rows, nq, nkv, dh, block_size);
   if (rc) return rc;
   if (rows == 0) return ALODLM_OK;
@@ -270,6 +300,16 @@ extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v,
   ALODLM_DISPATCH(dtype, T, {
     attn_delta_kernel<T><<<ceil_div_u(rows * nq, 4), 256, 0, st>>>((const T*)o, (const T*)dout,
                                                                    delta, rows, nq, dh);
+  });
+  ALODLM_CHECK_LAUNCH("attention_delta");
+  if (use_mfma(dtype, dh, tiles, ldv, {q, k, v, o, dout, dq, dk, dv}) && lddv % 8 == 0) {
+    if (n_tiles == 0) return ALODLM_OK;
+    return fa_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse, delta,
+                         (const bf16_t*)dout, bounds, tiles, n_tiles, (bf16_t*)dq, (bf16_t*)dk,
+                         (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv, (int)dh, (int)block_size,
+                         scale, st);
+  }
+  ALODLM_DISPATCH(dtype, T, {
     attn_dq_ref_kernel<T><<<ceil_div_u(rows * nq, 4), 256, 0, st>>>(
         (const T*)q, (const T*)k, (const T*)v, ldv, lse, delta, (const T*)dout, bounds,
         row_segment, (T*)dq, rows, nq, nkv, dh, block_size, scale);

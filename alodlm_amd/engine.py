@@ -185,16 +185,16 @@ class StepEngine:
     def _attention_fwd(self, q, k, v, o, lse, b):
         d = self.dims
         call("alodlm_attention_fwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(b.boundaries),
-             ptr(b.row_segment), ptr(o), ptr(lse), q.shape[0], d.heads, d.kv_heads, d.head_dim,
-             self.cfg.block_size, self.code, self._stream())
+             ptr(b.row_segment), ptr(b.tiles), b.tiles.shape[0], ptr(o), ptr(lse), q.shape[0],
+             d.heads, d.kv_heads, d.head_dim, self.cfg.block_size, self.code, self._stream())
 
     def _attention_bwd(self, q, k, v, o, lse, do, dq, dk, dv, b):
         d, N = self.dims, q.shape[0]
         ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads))
         call("alodlm_attention_bwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(o), ptr(lse),
-             ptr(do), ptr(b.boundaries), ptr(b.row_segment), ptr(dq), ptr(dk), ptr(dv),
-             d.qkv_width, ptr(ws), N, d.heads, d.kv_heads, d.head_dim, self.cfg.block_size,
-             self.code, self._stream())
+             ptr(do), ptr(b.boundaries), ptr(b.row_segment), ptr(b.tiles), b.tiles.shape[0],
+             ptr(dq), ptr(dk), ptr(dv), d.qkv_width, ptr(ws), N, d.heads, d.kv_heads,
+             d.head_dim, self.cfg.block_size, self.code, self._stream())
 
     def _attention_fwd_flops(self, q, k, v, o, lse, b):
         """Algorithmic forward FLOPs: 4*dh per allowed (q, k) pair and head."""

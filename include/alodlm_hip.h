@@ -133,20 +133,25 @@ int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t
  * v: rows of stride ldv; o: [rows, nq*dh]; lse: float [nq, rows].
  * Segment s spans dual-stream rows [bounds[s], bounds[s+1]) (clean half
  * first); row_segment[r] = s.  Scale is dh^-0.5.
+ * tiles: int32 [n_tiles, 2] = (segment, in-segment start row) of every
+ * 128-row tile of every stream (a tile never crosses a stream); with tiles,
+ * bf16 and head_dim 64/128 the MFMA flash kernels run, otherwise (or with
+ * tiles == NULL) the reference kernels.
  * bwd: dq [rows, nq*dh], dk [rows, nkv*dh], dv (stride lddv) from do.
  * `workspace` holds alodlm_attention_bwd_workspace(rows, nq) floats.
  * ------------------------------------------------------------------------ */
 int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
-                         const int64_t* bounds, const int32_t* row_segment, void* o,
-                         float* lse, int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
-                         int64_t block_size, int dtype, void* stream);
+                         const int64_t* bounds, const int32_t* row_segment,
+                         const int32_t* tiles, int64_t n_tiles, void* o, float* lse,
+                         int64_t rows, int64_t nq, int64_t nkv, int64_t dh, int64_t block_size,
+                         int dtype, void* stream);
 int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq);
 int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const void* o, const float* lse, const void* dout,
-                         const int64_t* bounds, const int32_t* row_segment, void* dq,
-                         void* dk, void* dv, int64_t lddv, float* workspace, int64_t rows,
-                         int64_t nq, int64_t nkv, int64_t dh, int64_t block_size, int dtype,
-                         void* stream);
+                         const int64_t* bounds, const int32_t* row_segment,
+                         const int32_t* tiles, int64_t n_tiles, void* dq, void* dk, void* dv,
+                         int64_t lddv, float* workspace, int64_t rows, int64_t nq, int64_t nkv,
+                         int64_t dh, int64_t block_size, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * SwiGLU ([tf] modeling_qwen3.py:81-83): gu = [gate | up] of width 2*inter;

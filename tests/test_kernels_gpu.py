@@ -149,17 +149,31 @@ def _dual_stream(bounds_tokens, block, seed):
     return torch.cat(pos), torch.tensor(seg, dtype=torch.int32), torch.tensor(packed)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("nq,nkv,dh,bounds,block", [
-    (4, 2, 64, [0, 40, 41, 100], 8),
-    (2, 1, 128, [0, 64, 160], 32),
-    (4, 4, 8, [0, 7, 20], 3),
-])
-def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block):
+ATTN_CASES = [
+    # (dtype, nq, nkv, dh, token bounds, block, path)
+    (torch.float32, 4, 2, 64, [0, 40, 41, 100], 8, "ref"),
+    (torch.float32, 2, 1, 128, [0, 64, 160], 32, "ref"),
+    (torch.float32, 4, 4, 8, [0, 7, 20], 3, "ref"),
+    (torch.bfloat16, 4, 2, 64, [0, 40, 41, 100], 8, "ref"),
+    (torch.bfloat16, 2, 1, 128, [0, 64, 160], 32, "ref"),
+    (torch.bfloat16, 4, 2, 64, [0, 40, 41, 100], 8, "mfma"),
+    (torch.bfloat16, 2, 1, 128, [0, 64, 160], 32, "mfma"),
+    (torch.bfloat16, 4, 1, 128, [0, 300, 333], 32, "mfma"),
+    (torch.bfloat16, 2, 2, 64, [0, 200, 390], 24, "mfma"),
+    (torch.bfloat16, 2, 1, 128, [0, 1024], 32, "mfma"),
+]
+
+
+@pytest.mark.parametrize("dtype,nq,nkv,dh,bounds,block,path", ATTN_CASES)
+def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block, path):
     """Attention (dual-stream mask) with q/k norm + rotary, forward and backward,
-    against autograd through the oracle's restatement in float64."""
+    against autograd through the oracle's restatement in float64.  `path`
+    selects the reference kernels (no tile table) or the MFMA flash kernels."""
+    from alodlm_amd.batch import attention_tiles
     L = lib()
-    log(f"attention nq={nq} nkv={nkv} dh={dh} bounds={bounds} block={block} {dtype}")
+    log(f"attention nq={nq} nkv={nkv} dh={dh} bounds={bounds} block={block} {dtype} {path}")
+    tiles = torch.tensor(attention_tiles(bounds), dtype=torch.int32).view(-1, 2).to(DEV)
+    tiles_ptr = L.ptr(tiles) if path == "mfma" else None
     g = torch.Generator().manual_seed(dh + nq)
     positions, row_seg, packed = _dual_stream(bounds, block, dh)
     N = len(positions)
@@ -181,7 +195,7 @@ def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block):
     o = torch.empty(N, nq * dh, dtype=dtype, device=DEV)
     lse = torch.empty(nq, N, dtype=torch.float32, device=DEV)
     L.call("alodlm_attention_fwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(bnd_d), L.ptr(seg_d),
-           L.ptr(o), L.ptr(lse), N, nq, nkv, dh, block, code, st())
+           tiles_ptr, tiles.shape[0], L.ptr(o), L.ptr(lse), N, nq, nkv, dh, block, code, st())
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dqkv = torch.zeros(N, W, dtype=dtype, device=DEV)
@@ -189,8 +203,9 @@ def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block):
                      device=DEV)
     dout_d = dout.to(DEV)
     L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
-           L.ptr(dout_d), L.ptr(bnd_d), L.ptr(seg_d), L.ptr(dq), L.ptr(dk),
-           L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block, code, st())
+           L.ptr(dout_d), L.ptr(bnd_d), L.ptr(seg_d), tiles_ptr, tiles.shape[0], L.ptr(dq),
+           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block,
+           code, st())
     dwq = torch.zeros(dh, dtype=torch.float32, device=DEV)
     dwk = torch.zeros(dh, dtype=torch.float32, device=DEV)
     ws2 = torch.empty(L.query("alodlm_qknorm_rope_bwd_workspace", N, nq, nkv, dh) * 2 + 16,
