@@ -13,11 +13,17 @@
 // dQ) is staged through LDS transposed by an 8x4 register transpose.
 //
 // dK/dV: one workgroup = one 128-key tile of one kv head, four wavefronts of
-// 32 keys; it loops over the query heads of the group and the 32-row query
-// tiles that see the keys, with S = Q . K^T so that each lane owns a key.
+// 32 keys; K and V of the tile stay in LDS, and the workgroup walks the query
+// heads of the group and the 64-row query tiles that see the keys, with
+// S = Q . K^T so that each lane owns a key.
 //
-// Only key tiles that intersect the allowed region are visited; a tile whose
-// four corners are allowed skips the per-element mask.
+// VALU economy: within one stream pair the mask of a lane is an interval of
+// key (or query) indices, so masking is two compares; the softmax runs in the
+// log2 domain (one FMA + one v_exp_f32 per score) with a lazily raised
+// running maximum (accumulators are rescaled only when the maximum grows by
+// more than 2^8); bf16 packing is v_cvt_pk_bf16_f32.  Each kernel prefetches
+// the next tile's global loads into registers while it computes the current
+// one.
 #include "common.h"
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
@@ -25,20 +31,10 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 #define FA_THREADS 256
 #define FA_KT 64    // keys per tile (forward / dQ)
-#define FA_QT 32    // query rows per tile (dK/dV)
-
-// allowed(q, k) for in-segment dual-stream indices (alodlm/batch.py:23-31)
-__device__ __forceinline__ bool dual_allowed(int q, int k, int L, int B) {
-  const bool qn = q >= L, kn = k >= L;
-  const int qb = (qn ? q - L : q) / B, kb = (kn ? k - L : k) / B;
-  return (qb == kb && qn == kn && k <= q) || (kb < qb && !kn);
-}
-
-__device__ __forceinline__ bool rect_allowed(int q0, int q1, int k0, int k1, int L, int B) {
-  // [q0, q1] x [k0, k1] inclusive, within one stream pair: the corners decide
-  return dual_allowed(q0, k0, L, B) && dual_allowed(q0, k1, L, B) &&
-         dual_allowed(q1, k0, L, B) && dual_allowed(q1, k1, L, B);
-}
+#define FA_QT 64    // query rows per tile (dK/dV)
+#define FA_LOG2E 1.4426950408889634f
+#define FA_LN2 0.6931471805599453f
+#define FA_RESCALE 8.0f  // log2 headroom before the running maximum is raised
 
 __device__ __forceinline__ f32x16_t zero16() {
   f32x16_t z;
@@ -59,85 +55,155 @@ __device__ __forceinline__ bf16x8_t load_split_frag(const bf16_t* p) {
   return *reinterpret_cast<bf16x8_t*>(&u);
 }
 
-__device__ __forceinline__ bf16x8_t pack8(const float* v) {
-  uint4 u;
-  u.x = (uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16);
-  u.y = (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16);
-  u.z = (uint32_t)float_to_bf16(v[4]) | ((uint32_t)float_to_bf16(v[5]) << 16);
-  u.w = (uint32_t)float_to_bf16(v[6]) | ((uint32_t)float_to_bf16(v[7]) << 16);
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)float_to_bf16(a) | ((uint32_t)float_to_bf16(b) << 16);
+}
+
+// Elements [off, off + 8) of an accumulator as one bf16 MFMA operand.
+__device__ __forceinline__ bf16x8_t pack8(const f32x16_t& v, int off) {
+  uint4 u = make_uint4(pack2(v[off], v[off + 1]), pack2(v[off + 2], v[off + 3]),
+                       pack2(v[off + 4], v[off + 5]), pack2(v[off + 6], v[off + 7]));
   return *reinterpret_cast<bf16x8_t*>(&u);
 }
 
-// Stage `nrows` rows of width D (row stride `ld` elements in global memory)
-// into LDS rows of stride D + 8.  Rows at or beyond `row_limit` are zero.
-template <int D>
-__device__ __forceinline__ void stage_rows(bf16_t* lds, const bf16_t* g, int64_t ld, int64_t row0,
-                                           int nrows, int64_t row_limit) {
-  constexpr int CH = D / 8;
-  for (int c = threadIdx.x; c < nrows * CH; c += FA_THREADS) {
-    const int r = c / CH, cc = (c % CH) * 8;
-    const int64_t gr = row0 + r;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (gr < row_limit) v = *reinterpret_cast<const uint4*>(g + gr * ld + cc);
-    *reinterpret_cast<uint4*>(lds + r * (D + 8) + cc) = v;
-  }
-}
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Stage the transpose of `nrows` x D (rows = keys or queries) into LDS as
-// D rows of stride nrows + 8: each thread loads an 8(row) x 4(col) block with
-// 8-byte loads and writes four 16-byte runs.
-template <int D>
-__device__ __forceinline__ void stage_transposed(bf16_t* lds, const bf16_t* g, int64_t ld,
-                                                 int64_t row0, int nrows, int64_t row_limit) {
-  const int ldt = nrows + 8;
-  const int blocks = (nrows / 8) * (D / 4);
-  for (int b = threadIdx.x; b < blocks; b += FA_THREADS) {
-    const int cq = b % (D / 4), rq = b / (D / 4);
-    uint2 v[8];
+// ---------------------------------------------------------------------------
+// Register staging of an NR x D tile (rows of stride `ld` in global memory)
+// ---------------------------------------------------------------------------
+template <int D, int NR>
+struct RowStage {  // row-major copy into LDS rows of stride D + 8
+  static constexpr int CH = D / 8;
+  static constexpr int PER = (NR * CH + FA_THREADS - 1) / FA_THREADS;
+  uint4 v[PER];
+  __device__ __forceinline__ void load(const bf16_t* g, int64_t ld, int64_t row0, int64_t limit) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t gr = row0 + rq * 8 + j;
-      v[j] = (gr < row_limit) ? *reinterpret_cast<const uint2*>(g + gr * ld + cq * 4)
-                              : make_uint2(0, 0);
+    for (int p = 0; p < PER; ++p) {
+      const int c = threadIdx.x + FA_THREADS * p;
+      const int r = c / CH, cc = (c % CH) * 8;
+      const bool ok = c < NR * CH && row0 + r < limit;
+      const int64_t gr = ok ? row0 + r : row0;
+      uint4 x = *reinterpret_cast<const uint4*>(g + gr * ld + cc);
+      v[p] = ok ? x : make_uint4(0, 0, 0, 0);
     }
+  }
+  __device__ __forceinline__ void store(bf16_t* lds) const {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t w[4];
+    for (int p = 0; p < PER; ++p) {
+      const int c = threadIdx.x + FA_THREADS * p;
+      if (c < NR * CH) *reinterpret_cast<uint4*>(lds + (c / CH) * (D + 8) + (c % CH) * 8) = v[p];
+    }
+  }
+};
+
+template <int D, int NR>
+struct TStage {  // transposed copy: D rows of stride NR + 8, via 8(row) x 4(col) blocks
+  static constexpr int BLK = (NR / 8) * (D / 4);
+  static constexpr int PER = (BLK + FA_THREADS - 1) / FA_THREADS;
+  uint2 v[PER][8];
+  __device__ __forceinline__ void load(const bf16_t* g, int64_t ld, int64_t row0, int64_t limit) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint32_t a = (c < 2) ? v[2 * p].x : v[2 * p].y;
-        const uint32_t b2 = (c < 2) ? v[2 * p + 1].x : v[2 * p + 1].y;
-        w[p] = (c & 1) ? ((a >> 16) | (b2 & 0xffff0000u)) : ((a & 0xffffu) | (b2 << 16));
+    for (int p = 0; p < PER; ++p) {
+      const int b = threadIdx.x + FA_THREADS * p;
+      const int cq = b % (D / 4), rq = b / (D / 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t gr = row0 + rq * 8 + j;
+        const bool ok = b < BLK && gr < limit;
+        uint2 x = *reinterpret_cast<const uint2*>(g + (ok ? gr : row0) * ld + cq * 4);
+        v[p][j] = ok ? x : make_uint2(0, 0);
       }
-      *reinterpret_cast<uint4*>(lds + (cq * 4 + c) * ldt + rq * 8) = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
+  __device__ __forceinline__ void store(bf16_t* lds) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int b = threadIdx.x + FA_THREADS * p;
+      if (b >= BLK) continue;
+      const int cq = b % (D / 4), rq = b / (D / 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t a = (c < 2) ? v[p][2 * q].x : v[p][2 * q].y;
+          const uint32_t b2 = (c < 2) ? v[p][2 * q + 1].x : v[p][2 * q + 1].y;
+          w[q] = (c & 1) ? ((a >> 16) | (b2 & 0xffff0000u)) : ((a & 0xffffu) | (b2 << 16));
+        }
+        *reinterpret_cast<uint4*>(lds + (cq * 4 + c) * (NR + 8) + rq * 8) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Mask as intervals (alodlm/batch.py:23-31).  For a query row q (in-segment
+// index) the allowed keys form one interval per stream:
+//   clean q:            clean keys [0, q]
+//   noisy q, block b:   clean keys [0, b*B) and noisy keys [L + b*B, q]
+// and for a key k the allowed queries form one interval per stream:
+//   clean k, block b:   clean queries [k, L) and noisy queries [L + (b+1)*B, 2L)
+//   noisy k, block b:   noisy queries [k, L + (b+1)*B)
+// (b*B and (b+1)*B clamped to L).  Range 0 is the clean key (query) stream of
+// a tile, range 1 the noisy one.
+// ---------------------------------------------------------------------------
+struct Interval2 { int lo0, hi0, lo1, hi1; };
+
+__device__ __forceinline__ Interval2 keys_of_query(int q, bool valid, int L, int B) {
+  Interval2 r = {0, 0, 0, 0};
+  if (!valid) return r;
+  if (q < L) { r.hi0 = q + 1; return r; }
+  const int bb = ((q - L) / B) * B;
+  r.hi0 = bb < L ? bb : L;
+  r.lo1 = L + bb;
+  r.hi1 = q + 1;
+  return r;
 }
 
-// Key ranges (in-segment) seen by the query tile [q0, q1) of one stream.
-__device__ __forceinline__ void fa_key_ranges(int q0, int q1, int L, int B, int* lo, int* hi) {
-  if (q0 < L) {
-    lo[0] = 0; hi[0] = q1; lo[1] = hi[1] = 0;
-  } else {
-    const int j0 = q0 - L, j1 = q1 - L;
-    const int clean_end = ((j1 - 1) / B) * B;
-    lo[0] = 0; hi[0] = clean_end < L ? clean_end : L;
-    lo[1] = L + (j0 / B) * B; hi[1] = q1;
+__device__ __forceinline__ Interval2 queries_of_key(int k, bool valid, int L, int B) {
+  Interval2 r = {0, 0, 0, 0};
+  if (!valid) return r;
+  if (k < L) {
+    const int nb = (k / B + 1) * B;
+    r.lo0 = k; r.hi0 = L;
+    r.lo1 = L + (nb < L ? nb : L); r.hi1 = 2 * L;
+    return r;
   }
+  const int nb = ((k - L) / B + 1) * B;
+  r.lo0 = k; r.hi0 = L + (nb < L ? nb : L);
+  return r;
 }
 
-// Query ranges (in-segment) that see the key tile [k0, k1) of one stream.
-__device__ __forceinline__ void fa_query_ranges(int k0, int k1, int L, int B, int* lo, int* hi) {
-  if (k0 < L) {
-    lo[0] = k0; hi[0] = L;
-    const int first = (k0 / B + 1) * B;
-    lo[1] = L + (first < L ? first : L); hi[1] = 2 * L;
-  } else {
-    const int j1 = k1 - L;
-    const int end = ((j1 - 1) / B + 1) * B;
-    lo[0] = k0; hi[0] = L + (end < L ? end : L);
-    lo[1] = hi[1] = 0;
-  }
+// Tile ranges: keys seen by the query tile [q0, q1), queries that see the key
+// tile [k0, k1) - the union of the lane intervals.
+__device__ __forceinline__ Interval2 key_ranges(int q0, int q1, int L, int B) {
+  Interval2 a = keys_of_query(q1 - 1, true, L, B);  // the last row sees the most keys
+  if (q0 >= L) a.lo1 = keys_of_query(q0, true, L, B).lo1;
+  return a;
+}
+__device__ __forceinline__ Interval2 query_ranges(int k0, int k1, int L, int B) {
+  Interval2 a = queries_of_key(k0, true, L, B);  // the first key is seen by the most queries
+  if (k0 >= L) a.hi0 = queries_of_key(k1 - 1, true, L, B).hi0;
+  return a;
+}
+
+// Walk the tiles of the two ranges.
+__device__ __forceinline__ bool range_first(const Interval2& R, int& r, int& pos) {
+  r = 0;
+  pos = R.lo0;
+  if (pos < R.hi0) return true;
+  r = 1;
+  pos = R.lo1;
+  return pos < R.hi1;
+}
+__device__ __forceinline__ bool range_next(const Interval2& R, int step, int& r, int& pos) {
+  pos += step;
+  if (pos < (r ? R.hi1 : R.hi0)) return true;
+  if (r == 1) return false;
+  r = 1;
+  pos = R.lo1;
+  return pos < R.hi1;
 }
 
 // ---------------------------------------------------------------------------
@@ -161,6 +227,7 @@ fa_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const int qi = start + wave * 32 + col;
   const bool q_valid = qi < q1;
   const int64_t ldq = (int64_t)nq * D, ldk = (int64_t)nkv * D;
+  const float c = scale * FA_LOG2E;
 
   bf16x8_t qf[D / 16];
 #pragma unroll
@@ -171,72 +238,89 @@ fa_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   f32x16_t oacc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) oacc[i] = zero16();
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f;  // running maximum (log2 units) and sum
 
-  int rlo[2], rhi[2];
-  fa_key_ranges(start, q1, L, B, rlo, rhi);
+  const Interval2 mine = keys_of_query(qi, q_valid, L, B);
+  const Interval2 R = key_ranges(start, q1, L, B);
+  // keys allowed for every row of the tile (first row: smallest upper bounds,
+  // last row: largest lower bound)
+  const Interval2 first = keys_of_query(start, true, L, B), last = keys_of_query(q1 - 1, true, L, B);
+  int r, k0;
+  bool more = range_first(R, r, k0);
+  RowStage<D, FA_KT> sk;
+  TStage<D, FA_KT> sv;
+  if (more) {
+    sk.load(k + hk * D, ldk, base + k0, N);
+    sv.load(v + hk * D, ldv, base + k0, N);
+  }
+  while (more) {
+    __syncthreads();
+    sk.store(lds_k);
+    sv.store(lds_vt);
+    __syncthreads();
+    const int cur_k0 = k0;
+    const int klo = r ? mine.lo1 : mine.lo0, khi = r ? mine.hi1 : mine.hi0;
+    const bool full = cur_k0 >= (r ? last.lo1 : last.lo0) &&
+                      cur_k0 + FA_KT <= (r ? first.hi1 : first.hi0);
+    more = range_next(R, FA_KT, r, k0);
+    if (more) {
+      sk.load(k + hk * D, ldk, base + k0, N);
+      sv.load(v + hk * D, ldv, base + k0, N);
+    }
+    f32x16_t sacc[2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    for (int k0 = rlo[r]; k0 < rhi[r]; k0 += FA_KT) {
-      __syncthreads();
-      stage_rows<D>(lds_k, k + hk * D, ldk, base + k0, FA_KT, N);
-      stage_transposed<D>(lds_vt, v + hk * D, ldv, base + k0, FA_KT, N);
-      __syncthreads();
-      const bool full = k0 + FA_KT <= rhi[r] && rect_allowed(start, q1 - 1, k0, k0 + FA_KT - 1, L, B);
-      f32x16_t sacc[2];
+    for (int kb = 0; kb < 2; ++kb) sacc[kb] = zero16();
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb] = zero16();
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8_t a = load_frag(lds_k + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kb], 0, 0, 0);
-        }
+        const bf16x8_t a = load_frag(lds_k + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kb], 0, 0, 0);
       }
-      float mx = -INFINITY;
+    if (!full) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float s = sacc[kb][e] * scale;
-          if (!full) {
-            const int key = k0 + kb * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-            if (!(q_valid && key < rhi[r] && dual_allowed(qi, key, L, B))) s = -INFINITY;
-          }
-          sacc[kb][e] = s;
-          mx = fmaxf(mx, s);
+          const int key = cur_k0 + kb * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+          if (key < klo || key >= khi) sacc[kb][e] = -INFINITY;
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float corr = expf(m - m_use);
-      float rs = 0.f;
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = expf(sacc[kb][e] - m_use);
-          sacc[kb][e] = p;
-          rs += p;
-        }
-      rs += __shfl_xor(rs, 32, 64);
-      l = l * corr + rs;
-      m = m_new;
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+    if (__any(mx > m + FA_RESCALE)) {
+      const bool raise = mx > m + FA_RESCALE;
+      const float m_new = raise ? mx : m;
+      const float corr = raise ? fast_exp2(m - m_new) : 1.f;  // 0 when m was -inf
+      l *= corr;
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[i][e] *= corr;
+      m = m_new;
+    }
+    const float m_use = m == -INFINITY ? 0.f : m;
+    float rs = 0.f;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        float pv[8];
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) pv[t] = sacc[st >> 1][(st & 1) * 8 + t];
-        const bf16x8_t pb = pack8(pv);
+      for (int e = 0; e < 16; ++e) {
+        const float p = fast_exp2(fmaf(sacc[kb][e], c, -m_use));
+        sacc[kb][e] = p;
+        rs += p;
+      }
+    l += rs + __shfl_xor(rs, 32, 64);
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          const bf16x8_t a = load_split_frag(lds_vt + (db * 32 + col) * (FA_KT + 8) + st * 16 + half * 4);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, oacc[db], 0, 0, 0);
-        }
+    for (int st = 0; st < 4; ++st) {
+      const bf16x8_t pb = pack8(sacc[st >> 1], (st & 1) * 8);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        const bf16x8_t a = load_split_frag(lds_vt + (db * 32 + col) * (FA_KT + 8) + st * 16 + half * 4);
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, oacc[db], 0, 0, 0);
       }
     }
   }
@@ -248,14 +332,11 @@ fa_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = db * 32 + j * 8 + half * 4;
-        uint2 w;
-        w.x = (uint32_t)float_to_bf16(oacc[db][j * 4] * inv) |
-              ((uint32_t)float_to_bf16(oacc[db][j * 4 + 1] * inv) << 16);
-        w.y = (uint32_t)float_to_bf16(oacc[db][j * 4 + 2] * inv) |
-              ((uint32_t)float_to_bf16(oacc[db][j * 4 + 3] * inv) << 16);
-        *reinterpret_cast<uint2*>(orow + d) = w;
+        *reinterpret_cast<uint2*>(orow + d) =
+            make_uint2(pack2(oacc[db][j * 4] * inv, oacc[db][j * 4 + 1] * inv),
+                       pack2(oacc[db][j * 4 + 2] * inv, oacc[db][j * 4 + 3] * inv));
       }
-    if (half == 0) lse[(int64_t)h * N + base + qi] = m + logf(l);
+    if (half == 0) lse[(int64_t)h * N + base + qi] = m * FA_LN2 + logf(l);
   }
 }
 
@@ -282,6 +363,7 @@ fa_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const int qi = start + wave * 32 + col;
   const bool q_valid = qi < q1;
   const int64_t ldq = (int64_t)nq * D, ldk = (int64_t)nkv * D;
+  const float c = scale * FA_LOG2E;
 
   bf16x8_t qf[D / 16], df[D / 16];
 #pragma unroll
@@ -294,60 +376,71 @@ fa_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       df[kk] = qf[kk];
     }
   }
-  const float lse_q = q_valid ? lse[(int64_t)h * N + base + qi] : 0.f;
+  const float lse2 = q_valid ? lse[(int64_t)h * N + base + qi] * FA_LOG2E : 0.f;
   const float delta_q = q_valid ? delta[(int64_t)h * N + base + qi] : 0.f;
   f32x16_t acc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = zero16();
 
-  int rlo[2], rhi[2];
-  fa_key_ranges(start, q1, L, B, rlo, rhi);
+  const Interval2 mine = keys_of_query(qi, q_valid, L, B);
+  const Interval2 R = key_ranges(start, q1, L, B);
+  const Interval2 first = keys_of_query(start, true, L, B), last = keys_of_query(q1 - 1, true, L, B);
+  int r, k0;
+  bool more = range_first(R, r, k0);
+  RowStage<D, FA_KT> sk, sv;
+  TStage<D, FA_KT> skt;
+  if (more) {
+    sk.load(k + hk * D, ldk, base + k0, N);
+    sv.load(v + hk * D, ldv, base + k0, N);
+    skt.load(k + hk * D, ldk, base + k0, N);
+  }
+  while (more) {
+    __syncthreads();
+    sk.store(lds_k);
+    sv.store(lds_v);
+    skt.store(lds_kt);
+    __syncthreads();
+    const int cur_k0 = k0;
+    const int klo = r ? mine.lo1 : mine.lo0, khi = r ? mine.hi1 : mine.hi0;
+    const bool full = cur_k0 >= (r ? last.lo1 : last.lo0) &&
+                      cur_k0 + FA_KT <= (r ? first.hi1 : first.hi0);
+    more = range_next(R, FA_KT, r, k0);
+    if (more) {
+      sk.load(k + hk * D, ldk, base + k0, N);
+      sv.load(v + hk * D, ldv, base + k0, N);
+      skt.load(k + hk * D, ldk, base + k0, N);
+    }
+    f32x16_t sacc[2], pacc[2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    for (int k0 = rlo[r]; k0 < rhi[r]; k0 += FA_KT) {
-      __syncthreads();
-      stage_rows<D>(lds_k, k + hk * D, ldk, base + k0, FA_KT, N);
-      stage_rows<D>(lds_v, v + hk * D, ldv, base + k0, FA_KT, N);
-      stage_transposed<D>(lds_kt, k + hk * D, ldk, base + k0, FA_KT, N);
-      __syncthreads();
-      const bool full = k0 + FA_KT <= rhi[r] && rect_allowed(start, q1 - 1, k0, k0 + FA_KT - 1, L, B);
-      f32x16_t sacc[2], pacc[2];
+    for (int kb = 0; kb < 2; ++kb) { sacc[kb] = zero16(); pacc[kb] = zero16(); }
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        sacc[kb] = zero16();
-        pacc[kb] = zero16();
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8_t a = load_frag(lds_k + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
-          sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kb], 0, 0, 0);
-          const bf16x8_t b = load_frag(lds_v + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
-          pacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, df[kk], pacc[kb], 0, 0, 0);
-        }
+        const bf16x8_t a = load_frag(lds_k + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc[kb], 0, 0, 0);
+        const bf16x8_t b = load_frag(lds_v + (kb * 32 + col) * (D + 8) + kk * 16 + half * 8);
+        pacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, df[kk], pacc[kb], 0, 0, 0);
       }
-      // dS^T = P^T * (dP^T - delta) with P^T = exp(S^T*scale - lse)
+    // dS^T = P^T * (dP^T - delta) with P^T = exp(S^T*scale - lse)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          bool ok = q_valid;
-          if (!full) {
-            const int key = k0 + kb * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-            ok = ok && key < rhi[r] && dual_allowed(qi, key, L, B);
-          }
-          const float p = ok ? expf(sacc[kb][e] * scale - lse_q) : 0.f;
-          sacc[kb][e] = p * (pacc[kb][e] - delta_q);
+      for (int e = 0; e < 16; ++e) {
+        float p = fast_exp2(fmaf(sacc[kb][e], c, -lse2));
+        if (!full) {
+          const int key = cur_k0 + kb * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+          if (key < klo || key >= khi) p = 0.f;
         }
+        sacc[kb][e] = p * (pacc[kb][e] - delta_q);
+      }
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        float dv[8];
+    for (int st = 0; st < 4; ++st) {
+      const bf16x8_t db8 = pack8(sacc[st >> 1], (st & 1) * 8);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) dv[t] = sacc[st >> 1][(st & 1) * 8 + t];
-        const bf16x8_t db8 = pack8(dv);
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          const bf16x8_t a = load_split_frag(lds_kt + (db * 32 + col) * (FA_KT + 8) + st * 16 + half * 4);
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db8, acc[db], 0, 0, 0);
-        }
+      for (int db = 0; db < D / 32; ++db) {
+        const bf16x8_t a = load_split_frag(lds_kt + (db * 32 + col) * (FA_KT + 8) + st * 16 + half * 4);
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, db8, acc[db], 0, 0, 0);
       }
     }
   }
@@ -358,12 +451,9 @@ fa_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = db * 32 + j * 8 + half * 4;
-        uint2 w;
-        w.x = (uint32_t)float_to_bf16(acc[db][j * 4] * scale) |
-              ((uint32_t)float_to_bf16(acc[db][j * 4 + 1] * scale) << 16);
-        w.y = (uint32_t)float_to_bf16(acc[db][j * 4 + 2] * scale) |
-              ((uint32_t)float_to_bf16(acc[db][j * 4 + 3] * scale) << 16);
-        *reinterpret_cast<uint2*>(row + d) = w;
+        *reinterpret_cast<uint2*>(row + d) =
+            make_uint2(pack2(acc[db][j * 4] * scale, acc[db][j * 4 + 1] * scale),
+                       pack2(acc[db][j * 4 + 2] * scale, acc[db][j * 4 + 3] * scale));
       }
   }
 }
@@ -379,11 +469,13 @@ fa_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv, int64_t N, int nq,
                int nkv, int B, float scale) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds_k[128 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) bf16_t lds_v[128 * (D + 8)];
   __shared__ __attribute__((aligned(16))) bf16_t lds_q[FA_QT * (D + 8)];
   __shared__ __attribute__((aligned(16))) bf16_t lds_do[FA_QT * (D + 8)];
   __shared__ __attribute__((aligned(16))) bf16_t lds_qt[D * (FA_QT + 8)];
   __shared__ __attribute__((aligned(16))) bf16_t lds_dot[D * (FA_QT + 8)];
-  __shared__ float lds_lse[FA_QT], lds_delta[FA_QT];
+  __shared__ __attribute__((aligned(16))) float lds_lse[FA_QT], lds_delta[FA_QT];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, col = lane & 31;
   const int hk = blockIdx.y, group = nq / nkv;
   const int seg = tiles[2 * blockIdx.x], start = tiles[2 * blockIdx.x + 1];
@@ -394,73 +486,108 @@ fa_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const int ki = start + wave * 32 + col;
   const bool k_valid = ki < k1;
   const int64_t ldq = (int64_t)nq * D, ldk = (int64_t)nkv * D;
+  const float c = scale * FA_LOG2E;
 
-  bf16x8_t kf[D / 16], vf[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    if (k_valid) {
-      kf[kk] = load_frag(k + (base + ki) * ldk + hk * D + kk * 16 + half * 8);
-      vf[kk] = load_frag(v + (base + ki) * ldv + hk * D + kk * 16 + half * 8);
-    } else {
-      kf[kk] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      vf[kk] = kf[kk];
-    }
+  {  // K and V of the key tile, once
+    RowStage<D, 128> s;
+    s.load(k + hk * D, ldk, base + start, base + k1);
+    s.store(lds_k);
+    s.load(v + hk * D, ldv, base + start, base + k1);
+    s.store(lds_v);
   }
   f32x16_t dkacc[D / 32], dvacc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) { dkacc[i] = zero16(); dvacc[i] = zero16(); }
 
-  int rlo[2], rhi[2];
-  fa_query_ranges(start, k1, L, B, rlo, rhi);
-  for (int h = hk * group; h < (hk + 1) * group; ++h) {
+  const Interval2 mine = queries_of_key(ki, k_valid, L, B);
+  const Interval2 R = query_ranges(start, k1, L, B);
+  // queries allowed for every key of the tile
+  const Interval2 first = queries_of_key(start, true, L, B), last = queries_of_key(k1 - 1, true, L, B);
+  int r = 0, q0 = 0, h = hk * group;
+  bool more = range_first(R, r, q0);
+  RowStage<D, FA_QT> sq, sdo;
+  TStage<D, FA_QT> sqt, sdot;
+  float pre_lse = 0.f, pre_delta = 0.f;
+  auto prefetch = [&](int hh, int rr, int qq) {
+    const int hi = rr ? R.hi1 : R.hi0;
+    const int64_t lim = base + hi;
+    sq.load(q + hh * D, ldq, base + qq, lim);
+    sdo.load(dout + hh * D, ldq, base + qq, lim);
+    sqt.load(q + hh * D, ldq, base + qq, lim);
+    sdot.load(dout + hh * D, ldq, base + qq, lim);
+    if (threadIdx.x < FA_QT) {
+      const bool ok = qq + (int)threadIdx.x < hi;
+      const int64_t row = base + qq + (ok ? (int)threadIdx.x : 0);
+      const float a = lse[(int64_t)hh * N + row], b = delta[(int64_t)hh * N + row];
+      pre_lse = ok ? a * FA_LOG2E : 0.f;
+      pre_delta = ok ? b : 0.f;
+    }
+  };
+  if (more) prefetch(h, r, q0);
+  while (more) {
+    __syncthreads();
+    sq.store(lds_q);
+    sdo.store(lds_do);
+    sqt.store(lds_qt);
+    sdot.store(lds_dot);
+    if (threadIdx.x < FA_QT) { lds_lse[threadIdx.x] = pre_lse; lds_delta[threadIdx.x] = pre_delta; }
+    __syncthreads();
+    const int cur_q0 = q0;
+    const int qlo = r ? mine.lo1 : mine.lo0, qhi = r ? mine.hi1 : mine.hi0;
+    const bool full = k1 - start == 128 && cur_q0 >= (r ? last.lo1 : last.lo0) &&
+                      cur_q0 + FA_QT <= (r ? first.hi1 : first.hi0);
+    more = range_next(R, FA_QT, r, q0);
+    if (!more && h + 1 < (hk + 1) * group) {
+      ++h;
+      more = range_first(R, r, q0);
+    }
+    if (more) prefetch(h, r, q0);
+    f32x16_t sacc[2], pacc[2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      for (int q0 = rlo[r]; q0 < rhi[r]; q0 += FA_QT) {
-        __syncthreads();
-        stage_rows<D>(lds_q, q + h * D, ldq, base + q0, FA_QT, N);
-        stage_rows<D>(lds_do, dout + h * D, ldq, base + q0, FA_QT, N);
-        stage_transposed<D>(lds_qt, q + h * D, ldq, base + q0, FA_QT, N);
-        stage_transposed<D>(lds_dot, dout + h * D, ldq, base + q0, FA_QT, N);
-        if (threadIdx.x < FA_QT) {
-          const int64_t row = base + q0 + threadIdx.x;
-          const bool ok = q0 + (int)threadIdx.x < rhi[r];
-          lds_lse[threadIdx.x] = ok ? lse[(int64_t)h * N + row] : 0.f;
-          lds_delta[threadIdx.x] = ok ? delta[(int64_t)h * N + row] : 0.f;
-        }
-        __syncthreads();
-        const bool full = q0 + FA_QT <= rhi[r] && start + 128 <= k1 &&
-                          rect_allowed(q0, q0 + FA_QT - 1, start, k1 - 1, L, B);
-        f32x16_t sacc = zero16(), pacc = zero16();
+    for (int qb = 0; qb < 2; ++qb) { sacc[qb] = zero16(); pacc[qb] = zero16(); }
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8_t a = load_frag(lds_q + col * (D + 8) + kk * 16 + half * 8);
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[kk], sacc, 0, 0, 0);
-          const bf16x8_t b = load_frag(lds_do + col * (D + 8) + kk * 16 + half * 8);
-          pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vf[kk], pacc, 0, 0, 0);
-        }
-        // S[q, key]: lane owns key column; rows q0 + 8j + 4*half + i
-        float pv[16], dsv[16];
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const bf16x8_t kb = load_frag(lds_k + (wave * 32 + col) * (D + 8) + kk * 16 + half * 8);
+      const bf16x8_t vb = load_frag(lds_v + (wave * 32 + col) * (D + 8) + kk * 16 + half * 8);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int qo = (e >> 2) * 8 + half * 4 + (e & 3);
-          bool ok = k_valid;
-          if (!full) ok = ok && q0 + qo < rhi[r] && dual_allowed(q0 + qo, ki, L, B);
-          const float p = ok ? expf(sacc[e] * scale - lds_lse[qo]) : 0.f;
-          pv[e] = p;
-          dsv[e] = p * (pacc[e] - lds_delta[qo]);
-        }
+      for (int qb = 0; qb < 2; ++qb) {
+        const bf16x8_t a = load_frag(lds_q + (qb * 32 + col) * (D + 8) + kk * 16 + half * 8);
+        sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kb, sacc[qb], 0, 0, 0);
+        const bf16x8_t b = load_frag(lds_do + (qb * 32 + col) * (D + 8) + kk * 16 + half * 8);
+        pacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vb, pacc[qb], 0, 0, 0);
+      }
+    }
+    // S[q, key]: lane owns key column; rows cur_q0 + qb*32 + 8j + 4*half + i
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const bf16x8_t pb = pack8(pv + st * 8);
-          const bf16x8_t sb = pack8(dsv + st * 8);
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int db = 0; db < D / 32; ++db) {
-            const bf16x8_t a = load_split_frag(lds_dot + (db * 32 + col) * (FA_QT + 8) + st * 16 + half * 4);
-            dvacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, dvacc[db], 0, 0, 0);
-            const bf16x8_t b = load_split_frag(lds_qt + (db * 32 + col) * (FA_QT + 8) + st * 16 + half * 4);
-            dkacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, sb, dkacc[db], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        const int qo = qb * 32 + j * 8 + half * 4;
+        const float4 ls = *reinterpret_cast<const float4*>(lds_lse + qo);
+        const float4 dl = *reinterpret_cast<const float4*>(lds_delta + qo);
+        const float lsv[4] = {ls.x, ls.y, ls.z, ls.w}, dlv[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = j * 4 + i;
+          float p = fast_exp2(fmaf(sacc[qb][e], c, -lsv[i]));
+          if (!full) {
+            const int qq = cur_q0 + qo + i;
+            if (qq < qlo || qq >= qhi) p = 0.f;
           }
+          sacc[qb][e] = p;
+          pacc[qb][e] = p * (pacc[qb][e] - dlv[i]);
         }
+      }
+#pragma unroll
+    for (int st = 0; st < FA_QT / 16; ++st) {
+      const bf16x8_t pb = pack8(sacc[st >> 1], (st & 1) * 8);
+      const bf16x8_t sb = pack8(pacc[st >> 1], (st & 1) * 8);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        const bf16x8_t a = load_split_frag(lds_dot + (db * 32 + col) * (FA_QT + 8) + st * 16 + half * 4);
+        dvacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, dvacc[db], 0, 0, 0);
+        const bf16x8_t b = load_split_frag(lds_qt + (db * 32 + col) * (FA_QT + 8) + st * 16 + half * 4);
+        dkacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, sb, dkacc[db], 0, 0, 0);
       }
     }
   }
@@ -472,17 +599,12 @@ fa_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = db * 32 + j * 8 + half * 4;
-        uint2 a, b;
-        a.x = (uint32_t)float_to_bf16(dkacc[db][j * 4] * scale) |
-              ((uint32_t)float_to_bf16(dkacc[db][j * 4 + 1] * scale) << 16);
-        a.y = (uint32_t)float_to_bf16(dkacc[db][j * 4 + 2] * scale) |
-              ((uint32_t)float_to_bf16(dkacc[db][j * 4 + 3] * scale) << 16);
-        b.x = (uint32_t)float_to_bf16(dvacc[db][j * 4]) |
-              ((uint32_t)float_to_bf16(dvacc[db][j * 4 + 1]) << 16);
-        b.y = (uint32_t)float_to_bf16(dvacc[db][j * 4 + 2]) |
-              ((uint32_t)float_to_bf16(dvacc[db][j * 4 + 3]) << 16);
-        *reinterpret_cast<uint2*>(krow + d) = a;
-        *reinterpret_cast<uint2*>(vrow + d) = b;
+        *reinterpret_cast<uint2*>(krow + d) =
+            make_uint2(pack2(dkacc[db][j * 4] * scale, dkacc[db][j * 4 + 1] * scale),
+                       pack2(dkacc[db][j * 4 + 2] * scale, dkacc[db][j * 4 + 3] * scale));
+        *reinterpret_cast<uint2*>(vrow + d) =
+            make_uint2(pack2(dvacc[db][j * 4], dvacc[db][j * 4 + 1]),
+                       pack2(dvacc[db][j * 4 + 2], dvacc[db][j * 4 + 3]));
       }
   }
 }

@@ -24,12 +24,9 @@ __host__ __device__ __forceinline__ float bf16_to_float(bf16_t h) {
   return v.f;
 }
 
-__host__ __device__ __forceinline__ bf16_t float_to_bf16(float f) {
-  union { uint32_t u; float f; } v;
-  v.f = f;
-  if ((v.u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((v.u >> 16) | 0x40);  // quiet NaN
-  uint32_t rounding = 0x7fffu + ((v.u >> 16) & 1u);
-  return (bf16_t)((v.u + rounding) >> 16);
+// Round to nearest even (gfx950: one v_cvt_pk_bf16_f32 per pair of values).
+__device__ __forceinline__ bf16_t float_to_bf16(float f) {
+  return __builtin_bit_cast(bf16_t, (__bf16)f);
 }
 
 // Round a float to the nearest bf16 value and return it as float.

@@ -31,33 +31,59 @@ __global__ void embed_scatter_kernel(const T* __restrict__ dout, const int64_t* 
   for (int64_t c = lane; c < H; c += 64) atomicAdd(dst + c, Elem<T>::load(src, c));
 }
 
-// act = cast(cast(silu(gate)) * up)   ([tf] modeling_qwen3.py:81-83)
-template <typename T>
+// act = cast(cast(silu(gate)) * up)   ([tf] modeling_qwen3.py:81-83).
+// gu rows are [gate | up] of width 2I; W elements per thread (8 with 16-byte
+// vector access when I % 8 == 0, else 1).
+template <typename T, int W>
 __global__ void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ act, int64_t rows,
                                   int64_t I) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
   if (i >= rows * I) return;
   const int64_t r = i / I, c = i % I;
-  const float g = Elem<T>::load(gu, r * 2 * I + c);
-  const float u = Elem<T>::load(gu, r * 2 * I + I + c);
-  const float s = Elem<T>::round(g / (1.0f + expf(-g)));
-  Elem<T>::store(act, i, s * u);
+  float g[8], u[8], a[8];
+  if (W == 8) {
+    Vec8<T>::load(gu + r * 2 * I + c, g);
+    Vec8<T>::load(gu + r * 2 * I + I + c, u);
+  } else {
+    g[0] = Elem<T>::load(gu, r * 2 * I + c);
+    u[0] = Elem<T>::load(gu, r * 2 * I + I + c);
+  }
+#pragma unroll
+  for (int e = 0; e < W; ++e) a[e] = Elem<T>::round(g[e] / (1.0f + expf(-g[e]))) * u[e];
+  if (W == 8) Vec8<T>::store(act + i, a);
+  else Elem<T>::store(act, i, a[0]);
 }
 
 // dgate = dact * up * silu'(gate), dup = dact * silu(gate)
-template <typename T>
+template <typename T, int W>
 __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restrict__ gu,
                                   T* __restrict__ dgu, int64_t rows, int64_t I) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
   if (i >= rows * I) return;
   const int64_t r = i / I, c = i % I;
-  const float g = Elem<T>::load(gu, r * 2 * I + c);
-  const float u = Elem<T>::load(gu, r * 2 * I + I + c);
-  const float da = Elem<T>::load(dact, i);
-  const float sg = 1.0f / (1.0f + expf(-g));
-  const float silu = Elem<T>::round(g * sg);
-  Elem<T>::store(dgu, r * 2 * I + c, da * u * (sg * (1.0f + g * (1.0f - sg))));
-  Elem<T>::store(dgu, r * 2 * I + I + c, da * silu);
+  float g[8], u[8], da[8], dg[8], du[8];
+  if (W == 8) {
+    Vec8<T>::load(gu + r * 2 * I + c, g);
+    Vec8<T>::load(gu + r * 2 * I + I + c, u);
+    Vec8<T>::load(dact + i, da);
+  } else {
+    g[0] = Elem<T>::load(gu, r * 2 * I + c);
+    u[0] = Elem<T>::load(gu, r * 2 * I + I + c);
+    da[0] = Elem<T>::load(dact, i);
+  }
+#pragma unroll
+  for (int e = 0; e < W; ++e) {
+    const float sg = 1.0f / (1.0f + expf(-g[e]));
+    dg[e] = da[e] * u[e] * (sg * (1.0f + g[e] * (1.0f - sg)));
+    du[e] = da[e] * Elem<T>::round(g[e] * sg);
+  }
+  if (W == 8) {
+    Vec8<T>::store(dgu + r * 2 * I + c, dg);
+    Vec8<T>::store(dgu + r * 2 * I + I + c, du);
+  } else {
+    Elem<T>::store(dgu, r * 2 * I + c, dg[0]);
+    Elem<T>::store(dgu, r * 2 * I + I + c, du[0]);
+  }
 }
 
 template <typename T>
@@ -98,9 +124,14 @@ extern "C" int alodlm_embed_scatter_add(const void* dout, const int64_t* ids,
 extern "C" int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_t inter, int dtype,
                                  void* stream) {
   if (rows == 0) return ALODLM_OK;
+  const bool v8 = inter % 8 == 0 && aligned8(gu, dtype) && aligned8(act, dtype);
   ALODLM_DISPATCH(dtype, T, {
-    swiglu_fwd_kernel<T><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
-        (const T*)gu, (T*)act, rows, inter);
+    if (v8)
+      swiglu_fwd_kernel<T, 8><<<ceil_div_u(rows * inter / 8, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)gu, (T*)act, rows, inter);
+    else
+      swiglu_fwd_kernel<T, 1><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)gu, (T*)act, rows, inter);
   });
   ALODLM_CHECK_LAUNCH("swiglu_fwd");
   return ALODLM_OK;
@@ -109,9 +140,15 @@ extern "C" int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_
 extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, int64_t rows,
                                  int64_t inter, int dtype, void* stream) {
   if (rows == 0) return ALODLM_OK;
+  const bool v8 = inter % 8 == 0 && aligned8(gu, dtype) && aligned8(dact, dtype) &&
+                  aligned8(dgu, dtype);
   ALODLM_DISPATCH(dtype, T, {
-    swiglu_bwd_kernel<T><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
-        (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
+    if (v8)
+      swiglu_bwd_kernel<T, 8><<<ceil_div_u(rows * inter / 8, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
+    else
+      swiglu_bwd_kernel<T, 1><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
   });
   ALODLM_CHECK_LAUNCH("swiglu_bwd");
   return ALODLM_OK;

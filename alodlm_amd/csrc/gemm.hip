@@ -273,7 +273,10 @@ gemm_simple_kernel(const T* __restrict__ A, int64_t sam, int64_t sak, const T* _
 static bool mfma_eligible(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb,
                           int b_kmajor, int64_t M, int64_t N, int64_t K) {
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (!al16(A) || !al16(B) || K % 8 != 0) return false;
+  if (!al16(A) || !al16(B)) return false;
+  // k-contiguous operands are staged in 8-element chunks along K; m/n-contiguous
+  // ones guard every k row, so any K works for them
+  if ((a_kmajor || b_kmajor) && K % 8 != 0) return false;
   if (lda % 8 != 0 || ldb % 8 != 0) return false;
   if (!a_kmajor && M % 4 != 0) return false;
   if (!b_kmajor && N % 4 != 0) return false;

@@ -1,0 +1,220 @@
+// q_norm / k_norm fused with the rotary embedding, forward and backward
+// (alodlm/model.py:41-46,58; [tf] modeling_qwen3.py:59-64,126-144).
+//
+// One wavefront owns one row and walks its nq + nkv heads; a lane owns the
+// rotary pairs (i, i + dh/2) for i = lane, lane + 64 (dh <= 256), so the
+// angle pos * inv_freq[i] and its cos/sin are evaluated once per row and
+// reused by every head.  cos/sin are rounded to the storage type like the
+// reference's rotary table, and q*cos, rotate(q)*sin and their sum each round
+// to the storage type.
+#include "common.h"
+#include "norm.h"
+
+#define ROPE_WAVES 4
+#define ROPE_MAX_T 2  // pairs per lane: dh/2 <= 128
+
+template <typename T>
+__global__ void __launch_bounds__(64 * ROPE_WAVES)
+qknorm_rope_fwd_kernel(const T* __restrict__ qkv, const T* __restrict__ wq, const T* __restrict__ wk,
+                       const int64_t* __restrict__ positions, const float* __restrict__ inv_freq,
+                       T* __restrict__ q_out, T* __restrict__ k_out, int64_t rows, int nq, int nkv,
+                       int dh, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROPE_WAVES + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int half = dh / 2;
+  const float pos = (float)positions[row];
+  float cs[ROPE_MAX_T], sn[ROPE_MAX_T];
+  float wqa[ROPE_MAX_T], wqb[ROPE_MAX_T], wka[ROPE_MAX_T], wkb[ROPE_MAX_T];
+#pragma unroll
+  for (int t = 0; t < ROPE_MAX_T; ++t) {
+    const int i = lane + 64 * t;
+    if (i < half) {
+      const float ang = pos * inv_freq[i];
+      cs[t] = Elem<T>::round(cosf(ang));
+      sn[t] = Elem<T>::round(sinf(ang));
+      wqa[t] = Elem<T>::load(wq, i); wqb[t] = Elem<T>::load(wq, i + half);
+      wka[t] = Elem<T>::load(wk, i); wkb[t] = Elem<T>::load(wk, i + half);
+    }
+  }
+  const T* src = qkv + row * (int64_t)(nq + 2 * nkv) * dh;
+  for (int head = 0; head < nq + nkv; ++head) {
+    const bool is_q = head < nq;
+    const T* x = src + head * dh;
+    T* dst = is_q ? q_out + (row * nq + head) * dh : k_out + (row * nkv + head - nq) * dh;
+    float xa[ROPE_MAX_T], xb[ROPE_MAX_T];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < ROPE_MAX_T; ++t) {
+      const int i = lane + 64 * t;
+      xa[t] = xb[t] = 0.f;
+      if (i < half) {
+        xa[t] = Elem<T>::load(x, i);
+        xb[t] = Elem<T>::load(x, i + half);
+        ss += xa[t] * xa[t] + xb[t] * xb[t];
+      }
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)dh + eps);
+#pragma unroll
+    for (int t = 0; t < ROPE_MAX_T; ++t) {
+      const int i = lane + 64 * t;
+      if (i < half) {
+        const float a = Elem<T>::round((is_q ? wqa[t] : wka[t]) * Elem<T>::round(xa[t] * r));
+        const float b = Elem<T>::round((is_q ? wqb[t] : wkb[t]) * Elem<T>::round(xb[t] * r));
+        Elem<T>::store(dst, i, Elem<T>::round(a * cs[t]) + Elem<T>::round(-b * sn[t]));
+        Elem<T>::store(dst, i + half, Elem<T>::round(b * cs[t]) + Elem<T>::round(a * sn[t]));
+      }
+    }
+  }
+}
+
+// Backward: dt = rotary^T d(out), then the RMSNorm backward over dh.  Per-lane
+// norm-weight partials stay in registers; the block writes one partial row
+// [q grads (dh) | k grads (dh)].
+#define ROPE_BWD_ROWS 32
+
+template <typename T>
+__global__ void __launch_bounds__(64 * ROPE_WAVES)
+qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const T* __restrict__ qkv,
+                       const T* __restrict__ wq, const T* __restrict__ wk,
+                       const int64_t* __restrict__ positions, const float* __restrict__ inv_freq,
+                       T* __restrict__ dqkv, float* __restrict__ partial, int64_t rows, int nq,
+                       int nkv, int dh, float eps) {
+  extern __shared__ float lds[];  // [ROPE_WAVES][2*dh]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = dh / 2;
+  const int64_t width = (int64_t)(nq + 2 * nkv) * dh;
+  float wqa[ROPE_MAX_T], wqb[ROPE_MAX_T], wka[ROPE_MAX_T], wkb[ROPE_MAX_T];
+  float gqa[ROPE_MAX_T], gqb[ROPE_MAX_T], gka[ROPE_MAX_T], gkb[ROPE_MAX_T];
+#pragma unroll
+  for (int t = 0; t < ROPE_MAX_T; ++t) {
+    const int i = lane + 64 * t;
+    gqa[t] = gqb[t] = gka[t] = gkb[t] = 0.f;
+    wqa[t] = wqb[t] = wka[t] = wkb[t] = 0.f;
+    if (i < half) {
+      wqa[t] = Elem<T>::load(wq, i); wqb[t] = Elem<T>::load(wq, i + half);
+      wka[t] = Elem<T>::load(wk, i); wkb[t] = Elem<T>::load(wk, i + half);
+    }
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * ROPE_BWD_ROWS;
+  for (int64_t row = r0 + wave; row < r0 + ROPE_BWD_ROWS && row < rows; row += ROPE_WAVES) {
+    const float pos = (float)positions[row];
+    float cs[ROPE_MAX_T], sn[ROPE_MAX_T];
+#pragma unroll
+    for (int t = 0; t < ROPE_MAX_T; ++t) {
+      const int i = lane + 64 * t;
+      cs[t] = sn[t] = 0.f;
+      if (i < half) {
+        const float ang = pos * inv_freq[i];
+        cs[t] = Elem<T>::round(cosf(ang));
+        sn[t] = Elem<T>::round(sinf(ang));
+      }
+    }
+    for (int head = 0; head < nq + nkv; ++head) {
+      const bool is_q = head < nq;
+      const T* x = qkv + row * width + head * dh;
+      const T* g = is_q ? dq + (row * nq + head) * dh : dk + (row * nkv + head - nq) * dh;
+      float xa[ROPE_MAX_T], xb[ROPE_MAX_T], ta[ROPE_MAX_T], tb[ROPE_MAX_T];
+      float ss = 0.f, s = 0.f;
+#pragma unroll
+      for (int t = 0; t < ROPE_MAX_T; ++t) {
+        const int i = lane + 64 * t;
+        xa[t] = xb[t] = ta[t] = tb[t] = 0.f;
+        if (i < half) {
+          xa[t] = Elem<T>::load(x, i);
+          xb[t] = Elem<T>::load(x, i + half);
+          const float go = Elem<T>::load(g, i), gh = Elem<T>::load(g, i + half);
+          ta[t] = go * cs[t] + gh * sn[t];   // d/d t[i]
+          tb[t] = gh * cs[t] - go * sn[t];   // d/d t[i + half]
+          ss += xa[t] * xa[t] + xb[t] * xb[t];
+          s += ta[t] * (is_q ? wqa[t] : wka[t]) * xa[t] + tb[t] * (is_q ? wqb[t] : wkb[t]) * xb[t];
+        }
+      }
+      ss = wave_sum(ss);
+      s = wave_sum(s);
+      const float r = 1.0f / sqrtf(ss / (float)dh + eps);
+      const float k = s * r * r * r / (float)dh;
+      T* out = dqkv + row * width + head * dh;
+#pragma unroll
+      for (int t = 0; t < ROPE_MAX_T; ++t) {
+        const int i = lane + 64 * t;
+        if (i < half) {
+          const float na = Elem<T>::round(xa[t] * r), nb = Elem<T>::round(xb[t] * r);
+          if (is_q) { gqa[t] += ta[t] * na; gqb[t] += tb[t] * nb; }
+          else { gka[t] += ta[t] * na; gkb[t] += tb[t] * nb; }
+          Elem<T>::store(out, i, r * ta[t] * (is_q ? wqa[t] : wka[t]) - xa[t] * k);
+          Elem<T>::store(out, i + half, r * tb[t] * (is_q ? wqb[t] : wkb[t]) - xb[t] * k);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < ROPE_MAX_T; ++t) {
+    const int i = lane + 64 * t;
+    if (i < half) {
+      float* L = lds + wave * 2 * dh;
+      L[i] = gqa[t]; L[i + half] = gqb[t];
+      L[dh + i] = gka[t]; L[dh + i + half] = gkb[t];
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < 2 * dh; c += 64 * ROPE_WAVES) {
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < ROPE_WAVES; ++v) acc += lds[v * 2 * dh + c];
+    partial[(int64_t)blockIdx.x * 2 * dh + c] = acc;
+  }
+}
+
+static int check_rope(int64_t rows, int64_t nq, int64_t nkv, int64_t dh) {
+  ALODLM_CHECK_ARG(rows >= 0 && nq > 0 && nkv > 0, "qknorm_rope: bad head counts");
+  ALODLM_CHECK_ARG(dh > 0 && dh % 2 == 0 && dh <= 128 * ROPE_MAX_T,
+                   "qknorm_rope: head_dim must be even and <= %d", 128 * ROPE_MAX_T);
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const void* wk,
+                                      const int64_t* positions, const float* inv_freq, void* q_out,
+                                      void* k_out, int64_t rows, int64_t nq, int64_t nkv,
+                                      int64_t dh, float eps, int dtype, void* stream) {
+  int rc = check_rope(rows, nq, nkv, dh);
+  if (rc) return rc;
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    qknorm_rope_fwd_kernel<T><<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
+                                as_stream(stream)>>>(
+        (const T*)qkv, (const T*)wq, (const T*)wk, positions, inv_freq, (T*)q_out, (T*)k_out,
+        rows, (int)nq, (int)nkv, (int)dh, eps);
+  });
+  ALODLM_CHECK_LAUNCH("qknorm_rope_fwd");
+  return ALODLM_OK;
+}
+
+extern "C" int64_t alodlm_qknorm_rope_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv,
+                                                    int64_t dh) {
+  (void)nq; (void)nkv;
+  return ((rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS) * 2 * dh;
+}
+
+extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv,
+                                      const void* wq, const void* wk, const int64_t* positions,
+                                      const float* inv_freq, void* dqkv, float* dwq_accum,
+                                      float* dwk_accum, float* workspace, int64_t rows, int64_t nq,
+                                      int64_t nkv, int64_t dh, float eps, int dtype, void* stream) {
+  int rc = check_rope(rows, nq, nkv, dh);
+  if (rc) return rc;
+  if (rows == 0) return ALODLM_OK;
+  const int64_t nparts = (rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS;
+  hipStream_t st = as_stream(stream);
+  ALODLM_DISPATCH(dtype, T, {
+    qknorm_rope_bwd_kernel<T><<<(unsigned)nparts, 64 * ROPE_WAVES,
+                                ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
+        (const T*)dq, (const T*)dk, (const T*)qkv, (const T*)wq, (const T*)wk, positions,
+        inv_freq, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps);
+  });
+  ALODLM_CHECK_LAUNCH("qknorm_rope_bwd");
+  rc = column_reduce(workspace, nparts, 2 * dh, 0, dh, dwq_accum, st);
+  if (rc) return rc;
+  return column_reduce(workspace, nparts, 2 * dh, dh, dh, dwk_accum, st);
+}
