@@ -291,9 +291,22 @@ static int64_t splitk_count(int64_t M, int64_t N, int64_t K) {
   return splits;
 }
 
+int64_t gemm_big_splits(int64_t M, int64_t N, int64_t K);
+void gemm_big_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
+                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
+                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
+                     int64_t* nsplit_out, hipStream_t st);
+
+// The 256x256 kernel takes the products whose output fills at least one tile.
+static bool use_big(int64_t M, int64_t N, int64_t K) { return M >= 256 && N >= 256 && K >= 64; }
+
 extern "C" int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype) {
   if (epilogue != ALODLM_EPI_ACCUM || dtype != ALODLM_BF16) return 0;
-  const int64_t s = splitk_count(M, N, K);
+  int64_t s = splitk_count(M, N, K);
+  if (use_big(M, N, K)) {
+    const int64_t b = gemm_big_splits(M, N, K);
+    s = b > s ? b : s;
+  }
   return s > 1 ? s * M * N : 0;
 }
 
@@ -329,6 +342,24 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
   ALODLM_CHECK_ARG(epilogue != ALODLM_EPI_RESIDUAL || R != nullptr, "gemm: residual needs R");
   if (M == 0 || N == 0) return ALODLM_OK;
   hipStream_t st = as_stream(stream);
+  if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
+      use_big(M, N, K)) {
+    int64_t splits = 1;
+    if (epilogue == ALODLM_EPI_ACCUM) {
+      splits = gemm_big_splits(M, N, K);
+      if (splits > 1 && workspace == nullptr) splits = 1;
+    }
+    int64_t nsplit = 1;
+    gemm_big_launch((const bf16_t*)A, lda, a_kmajor, (const bf16_t*)B, ldb, b_kmajor, C, ldc,
+                    (const bf16_t*)R, ldr, M, N, K, alpha, epilogue, workspace, splits, &nsplit, st);
+    ALODLM_CHECK_LAUNCH("gemm_bf16_256");
+    if (epilogue == ALODLM_EPI_ACCUM && nsplit > 1) {
+      splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(workspace, nsplit, M, N,
+                                                                   (float*)C, ldc);
+      ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
+    }
+    return ALODLM_OK;
+  }
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K)) {
     int64_t splits = 1;
     if (epilogue == ALODLM_EPI_ACCUM) {
