@@ -9,9 +9,10 @@ Prints one JSON line (metric of BASELINE: train tokens/s) with:
                 HIP events around its launches on the launch stream):
                 algorithmic FLOPs per launch / average launch time vs 2.5 PFLOP/s
   mfu           whole-step algorithmic FLOPs / step time / bf16 dense peak
-  cpu_baseline  the CPU oracle timed on this host on a bounded sample (one
-                decoder layer fwd+bwd at 4096 x 2048 and one LM-head readout
-                fwd+bwd), extrapolated to the full step by layer-application
+  cpu_baseline  the CPU oracle timed on this host on a bounded sample (three
+                decoder-layer fwd+bwd passes over one 4096-row dual-stream
+                segment and one LM-head readout fwd+bwd over 2048 rows, about
+                10-30 s), extrapolated to the full step by layer-application
                 and readout-row counts.
 """
 
@@ -26,6 +27,8 @@ import torch
 
 PEAK_BF16 = 2516.6e12   # dense bf16 MFMA FLOP/s of MI355X (256 CU x 4096 FLOP/clk x 2.4 GHz)
 PEAK_HBM = 8.0e12
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_bf16_1p7b_step_traffic.md")
 
 
 def qwen3_1p7b_config():
@@ -78,6 +81,7 @@ class KernelTimer:
 
     def __init__(self):
         self.records = {}
+        self.gemm_bytes = 0
 
     def wrap(self, engine):
         timer = self
@@ -91,6 +95,8 @@ class KernelTimer:
                 out = fn(*args, **kwargs)
                 end.record()
                 timer.records.setdefault(kind, []).append((start, end, flops_fn(*args, **kwargs)))
+                if kind == "gemm_bf16":
+                    timer.gemm_bytes += gemm_bytes(*args, **kwargs)
                 return out
             return run
 
@@ -107,11 +113,34 @@ class KernelTimer:
         return out
 
 
-def cpu_baseline(dims_l, cfg_seg=2048, readout_rows=1024, threads=None):
+def gemm_bytes(A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=0, R=None, ldr=0):
+    """Algorithmic HBM bytes of one GEMM launch: A and B read once (bf16), C
+    written once (bf16 store), plus R read (residual) or the float32 C read and
+    written back (accumulate)."""
+    c_bytes = {0: 2 * M * N, 1: 4 * M * N, 2: 8 * M * N}[epi]
+    return 2 * (M * K + N * K) + c_bytes
+
+
+def profiled_traffic(path):
+    """HBM bytes per GEMM launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes over this benchmark, read from the committed profile summary."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     """Time the CPU oracle (float32, torch eager on this host) on a bounded
-    sample and extrapolate to the full 1.7B step.  Returns (tokens/s, detail)."""
+    sample: `layer_reps` decoder-layer fwd+bwd passes over one dual-stream
+    segment and one LM-head readout fwd+bwd over `readout_rows` rows.  Returns
+    (seconds per layer pass, seconds per readout row, threads)."""
     from oracle import step as O
-    threads = threads or os.cpu_count()
+    threads = threads or torch.get_num_threads()  # honours OMP_NUM_THREADS
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     d = O.Dims(hidden=2048, heads=16, kv_heads=8, head_dim=128, intermediate=6144,
@@ -131,17 +160,19 @@ def cpu_baseline(dims_l, cfg_seg=2048, readout_rows=1024, threads=None):
     cos, sin = O.rope_tables(pos, 128, 1e6)
     allowed = torch.as_tensor(O.attention_mask(L, 32))
     x = torch.randn(rows, 2048, generator=g).requires_grad_(True)
+    dy = torch.randn(rows, 2048, generator=g)
     t0 = time.perf_counter()
-    y = O.layer_forward(p, pre, x, cos, sin, allowed, d)
-    y.backward(torch.randn_like(y))
-    t_layer = time.perf_counter() - t0
+    for _ in range(layer_reps):
+        y = O.layer_forward(p, pre, x, cos, sin, allowed, d)
+        y.backward(dy)
+    t_layer = (time.perf_counter() - t0) / layer_reps
     W = (torch.randn(151936, 2048, generator=g) * 0.02).requires_grad_(True)
     X = torch.randn(readout_rows, 2048, generator=g).requires_grad_(True)
     tgt = torch.randint(0, 151936, (readout_rows,), generator=g)
     t0 = time.perf_counter()
     loss = torch.nn.functional.cross_entropy(X @ W.T, tgt)
     loss.backward()
-    t_readout = time.perf_counter() - t0
+    t_readout = (time.perf_counter() - t0) / readout_rows
     return t_layer, t_readout, threads
 
 
@@ -152,6 +183,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-kernel-timing", action="store_true")
+    parser.add_argument("--traffic-calibration", action="store_true",
+                        help="first run one plain 1 GiB device copy (read 1 GiB, write "
+                             "1 GiB) so that HBM byte counters can be scaled against it")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -163,6 +197,12 @@ def main():
     from alodlm_amd.optim import FusedAdamW, param_groups
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.traffic_calibration:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     dtype = torch.bfloat16
     model = build_model(device, dtype)
     engine = model.engine()
@@ -221,26 +261,37 @@ def main():
         dom = max(summary, key=lambda k: summary[k]["ms"])
         s = summary[dom]
         achieved = s["flops"] / s["launches"] / (s["ms"] / s["launches"] / 1000.0)
-        line["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 1),
+        line["roofline"] = {"bound": "mfma", "kernel": dom,
+                            "launches_per_step": s["launches"] // args.steps,
+                            "avg_launch_us": round(1000.0 * s["ms"] / s["launches"], 1),
+                            "achieved": round(achieved / 1e12, 1),
                             "peak": round(PEAK_BF16 / 1e12, 1), "unit": "TFLOP/s",
-                            "frac": round(achieved / PEAK_BF16, 4), "traffic": None}
+                            "frac": round(achieved / PEAK_BF16, 4),
+                            "traffic": None}
+        if dom == "gemm_bf16":
+            line["roofline"]["algorithmic_bytes_per_launch"] = timer.gemm_bytes // s["launches"]
+            line["roofline"]["traffic"] = profiled_traffic(TRAFFIC_PROFILE)
+            line["roofline"]["traffic_source"] = os.path.relpath(TRAFFIC_PROFILE, ROOT)
         line["kernel_classes"] = {k: {"ms_per_step": round(v["ms"] / args.steps, 1),
                                       "tflops": round(v["flops"] / (v["ms"] / 1000) / 1e12, 1)}
                                   for k, v in summary.items()}
     if not args.no_cpu_baseline:
+        cfg = model.config
+        model_apps = cfg.loop_start + cfg.max_depth * (engine.dims.layers - cfg.loop_start)
         del opt, model, engine
         torch.cuda.empty_cache()
-        t_layer, t_readout, threads = cpu_baseline(None)
-        apps = 112
-        # sample: one layer on 4096 rows (one 2048-token segment), readout on 1024 rows
-        t_step = apps * 8 * t_layer + (sum(sum(r) for r in rows) / len(rows) / 1024) * t_readout
+        t_layer, t_row, threads = cpu_baseline()
+        apps = model_apps
+        readout_rows = sum(sum(r) for r in rows) / len(rows)
+        t_step = apps * len(seg_lengths) * t_layer + readout_rows * t_row
         line["cpu_baseline"] = {
             "value": round(tokens / t_step, 4), "unit": "tokens/s", "cores": threads,
             "kind": "port",
-            "sample": (f"oracle fp32 eager: 1 decoder layer fwd+bwd on 4096x2048 rows "
-                       f"({t_layer:.2f}s) + LM head/CE fwd+bwd on 1024x2048x151936 "
-                       f"({t_readout:.2f}s); extrapolated x{apps * 8} layer samples and "
-                       f"readout rows/1024"),
+            "sample": (f"oracle fp32 eager: 3 decoder-layer fwd+bwd passes on one "
+                       f"4096x2048 dual-stream segment ({t_layer:.2f}s each) + LM head/CE "
+                       f"fwd+bwd on 2048 rows x 151936 ({1000 * t_row:.2f} ms/row); "
+                       f"step = {apps} layer applications x {len(seg_lengths)} segments "
+                       f"+ {readout_rows:.0f} readout rows"),
         }
     print(json.dumps(line), flush=True)
 
