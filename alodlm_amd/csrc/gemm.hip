@@ -298,7 +298,10 @@ void gemm_big_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B
                      int64_t* nsplit_out, hipStream_t st);
 
 // The 256x256 kernel takes the products whose output fills at least one tile.
-static bool use_big(int64_t M, int64_t N, int64_t K) { return M >= 256 && N >= 256 && K >= 64; }
+// The 256x256 kernel needs whole 64-deep k tiles for k-contiguous operands.
+static bool use_big(int64_t M, int64_t N, int64_t K, bool any_kmajor = false) {
+  return M >= 256 && N >= 256 && K >= 64 && (!any_kmajor || K % 64 == 0);
+}
 
 extern "C" int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype) {
   if (epilogue != ALODLM_EPI_ACCUM || dtype != ALODLM_BF16) return 0;
@@ -343,7 +346,7 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
   if (M == 0 || N == 0) return ALODLM_OK;
   hipStream_t st = as_stream(stream);
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
-      use_big(M, N, K)) {
+      use_big(M, N, K, a_kmajor || b_kmajor)) {
     int64_t splits = 1;
     if (epilogue == ALODLM_EPI_ACCUM) {
       splits = gemm_big_splits(M, N, K);
