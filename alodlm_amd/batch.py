@@ -168,11 +168,18 @@ TILE_ROWS = 128
 
 def attention_tiles(offsets):
     """(segment, in-segment start) of every 128-row tile of each segment's clean
-    and noisy stream; tiles never cross a stream or a segment."""
-    out = []
+    and noisy stream; tiles never cross a stream or a segment.
+
+    Tiles are listed by decreasing start within their stream.  A query tile's
+    key range grows with its start and a key tile's query range shrinks with
+    it, so the forward/dQ kernels (which take the list in order) and the dK/dV
+    kernel (which takes it in reverse) both dispatch their heaviest tiles
+    first."""
+    tiles = []
     for s, (a, b) in enumerate(zip(offsets, offsets[1:])):
         length = b - a
         for stream in (0, length):
             for start in range(0, length, TILE_ROWS):
-                out += [s, stream + start]
-    return out
+                tiles.append((start, s, stream + start))
+    tiles.sort(key=lambda t: -t[0])
+    return [v for _, s, start in tiles for v in (s, start)]

@@ -248,6 +248,15 @@ int fa_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv
                   bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int dh,
                   int B, float scale, hipStream_t st);
 
+int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
+                     const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
+                     float* lse, int64_t N, int nq, int nkv, int B, float scale, hipStream_t st);
+int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
+                     const float* lse, const float* delta, const bf16_t* dout,
+                     const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
+                     bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
+                     float scale, hipStream_t st);
+
 // The MFMA kernels take bf16, head_dim 64 or 128, 16-byte aligned rows and a
 // tile table; everything else runs the reference kernels above.
 static bool use_mfma(int dtype, int64_t dh, const int32_t* tiles, int64_t ldv,
@@ -269,6 +278,11 @@ extern "C" int alodlm_attention_fwd(const void* q, const void* k, const void* v,
   const float scale = 1.0f / sqrtf((float)dh);
   if (use_mfma(dtype, dh, tiles, ldv, {q, k, v, o})) {
     if (n_tiles == 0) return ALODLM_OK;
+    ALODLM_CHECK_ARG(n_tiles <= 65535, "attention: too many 128-row tiles (%lld)", (long long)n_tiles);
+    if (dh == 128)
+      return fa128_fwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, bounds,
+                              tiles, n_tiles, (bf16_t*)o, lse, rows, (int)nq, (int)nkv,
+                              (int)block_size, scale, as_stream(stream));
     return fa_fwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, bounds, tiles,
                          n_tiles, (bf16_t*)o, lse, rows, (int)nq, (int)nkv, (int)dh,
                          (int)block_size, scale, as_stream(stream));
@@ -304,6 +318,12 @@ extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v,
   ALODLM_CHECK_LAUNCH("attention_delta");
   if (use_mfma(dtype, dh, tiles, ldv, {q, k, v, o, dout, dq, dk, dv}) && lddv % 8 == 0) {
     if (n_tiles == 0) return ALODLM_OK;
+    ALODLM_CHECK_ARG(n_tiles <= 65535, "attention: too many 128-row tiles (%lld)", (long long)n_tiles);
+    if (dh == 128)
+      return fa128_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse,
+                              delta, (const bf16_t*)dout, bounds, tiles, n_tiles, (bf16_t*)dq,
+                              (bf16_t*)dk, (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv,
+                              (int)block_size, scale, st);
     return fa_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse, delta,
                          (const bf16_t*)dout, bounds, tiles, n_tiles, (bf16_t*)dq, (bf16_t*)dk,
                          (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv, (int)dh, (int)block_size,

@@ -164,6 +164,7 @@ ATTN_CASES = [
     (torch.bfloat16, 4, 1, 128, [0, 300, 333], 32, "mfma"),
     (torch.bfloat16, 2, 2, 64, [0, 200, 390], 24, "mfma"),
     (torch.bfloat16, 2, 1, 128, [0, 1024], 32, "mfma"),
+    (torch.bfloat16, 4, 2, 128, [0, 512, 1000, 1001], 32, "mfma"),
 ]
 
 
