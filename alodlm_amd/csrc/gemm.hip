@@ -297,6 +297,14 @@ void gemm_big_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B
                      int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
                      int64_t* nsplit_out, hipStream_t st);
 
+bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int64_t M, int64_t N,
+                      int64_t K);
+int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K);
+void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
+                    int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
+                    int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
+                    int64_t* nsplit_out, hipStream_t st);
+
 // The 256x256 kernel takes the products whose output fills at least one tile.
 // The 256x256 kernel needs whole 64-deep k tiles for k-contiguous operands.
 static bool use_big(int64_t M, int64_t N, int64_t K, bool any_kmajor = false) {
@@ -309,6 +317,10 @@ extern "C" int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int ep
   if (use_big(M, N, K)) {
     const int64_t b = gemm_big_splits(M, N, K);
     s = b > s ? b : s;
+  }
+  if (M >= 256 && N >= 256 && K % 32 == 0) {
+    const int64_t d = gemm_dl_splits(M, N, K);
+    s = d > s ? d : s;
   }
   return s > 1 ? s * M * N : 0;
 }
@@ -345,6 +357,24 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
   ALODLM_CHECK_ARG(epilogue != ALODLM_EPI_RESIDUAL || R != nullptr, "gemm: residual needs R");
   if (M == 0 || N == 0) return ALODLM_OK;
   hipStream_t st = as_stream(stream);
+  if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
+      gemm_dl_eligible(lda, a_kmajor, ldb, b_kmajor, M, N, K)) {
+    int64_t splits = 1;
+    if (epilogue == ALODLM_EPI_ACCUM) {
+      splits = gemm_dl_splits(M, N, K);
+      if (splits > 1 && workspace == nullptr) splits = 1;
+    }
+    int64_t nsplit = 1;
+    gemm_dl_launch((const bf16_t*)A, lda, a_kmajor, (const bf16_t*)B, ldb, b_kmajor, C, ldc,
+                   (const bf16_t*)R, ldr, M, N, K, alpha, epilogue, workspace, splits, &nsplit, st);
+    ALODLM_CHECK_LAUNCH("gemm_bf16_dl");
+    if (epilogue == ALODLM_EPI_ACCUM && nsplit > 1) {
+      splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(workspace, nsplit, M, N,
+                                                                   (float*)C, ldc);
+      ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
+    }
+    return ALODLM_OK;
+  }
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
       use_big(M, N, K, a_kmajor || b_kmajor)) {
     int64_t splits = 1;

@@ -40,6 +40,10 @@ GEMM_CASES = [
     (1040, 256, 1001, 0, 0, torch.bfloat16),   # LM-head dW shape class: K = selected rows
     (768, 640, 320, 1, 0, torch.bfloat16),     # 256x256 tiles with ragged edges
     (520, 768, 256, 0, 1, torch.bfloat16),
+    (256, 256, 32, 1, 1, torch.bfloat16),      # one 32-deep k stage
+    (512, 264, 64, 0, 0, torch.bfloat16),
+    (296, 512, 96, 1, 0, torch.bfloat16),
+    (1024, 768, 2048, 0, 1, torch.bfloat16),
     (96, 80, 40, 1, 0, torch.bfloat16),
     (70, 33, 19, 0, 0, torch.float32),
     (130, 65, 48, 1, 1, torch.float32),
