@@ -10,9 +10,9 @@
 //  * a transposed fragment (ds_read_b64_tr_b16; 32 lanes read 4 consecutive
 //    rows x 4 chunks) covers 16 distinct chunks as well.
 // Tiles are filled by direct global->LDS loads (global_load_lds_dwordx4: lane
-// i of a wavefront instruction writes the i-th 16-byte slot after the base),
-// so the swizzle is applied by the choice of source chunk and no register
-// staging or VALU work is spent on copies.  Tiles are double-buffered: the
+// i of a wavefront instruction writes the i-th 16-byte slot after the base;
+// issued through lds_dma.h), so the swizzle is applied by the choice of source
+// chunk and no register staging or VALU work is spent on copies.  Tiles are double-buffered: the
 // next tile's loads are issued right after the barrier that publishes the
 // current one and are complete (vmcnt) before the next barrier.
 //
@@ -34,6 +34,7 @@
 // them in that order and dK/dV in reverse, so the heaviest tiles of each pass
 // are dispatched first.
 #include "attention_common.h"
+#include "lds_dma.h"
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 #define LDS_AS __attribute__((address_space(3)))
@@ -57,7 +58,7 @@ __device__ __forceinline__ void dload4(char* tile, int r0, const bf16_t* g, int6
   const int c = (lane & 15) ^ swz(r);
   int64_t gr = g0 + r;
   gr = gr < gmax ? gr : gmax;
-  __builtin_amdgcn_global_load_lds(g + gr * ld + c * 8, (LDS_AS void*)(tile + r0 * ROWB), 16, 0, 0);
+  dma16_v(g + gr * ld + c * 8, lds_addr(tile + r0 * ROWB));
 }
 
 // A/B operand fragment from a row: 8 bf16 of chunk `chunk` of tile row `row`.
@@ -150,6 +151,9 @@ fa128_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   };
   int r, k0;
   bool more = range_first(R, r, k0);
+  // the register loads above are complete before any direct load is issued,
+  // so the compiler has no reason to wait inside the loop
+  __builtin_amdgcn_s_waitcnt(0);
   if (more) issue(0, k0);
   int stg = 0;
   while (more) {
@@ -281,6 +285,9 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   };
   int r, k0;
   bool more = range_first(R, r, k0);
+  // the register loads above are complete before any direct load is issued,
+  // so the compiler has no reason to wait inside the loop
+  __builtin_amdgcn_s_waitcnt(0);
   if (more) issue(0, k0);
   int stg = 0;
   while (more) {
@@ -394,11 +401,12 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       int64_t row = base + qq + col;
       row = row < gmax ? row : gmax;
       const float* src = (half ? delta : lse) + (int64_t)hh * N + row;
-      __builtin_amdgcn_global_load_lds(src, (LDS_AS void*)lds_ld[stg], 4, 0, 0);
+      dma4_v(src, lds_addr(lds_ld[stg]));
     }
   };
   int r = 0, q0 = 0, h = hk * group;
   bool more = range_first(R, r, q0);
+  __builtin_amdgcn_s_waitcnt(0);
   if (more) issue(0, h, r, q0);
   int stg = 0;
   while (more) {

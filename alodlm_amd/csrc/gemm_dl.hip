@@ -3,11 +3,11 @@
 // m/n-contiguous in any combination.
 //
 // 256x256 block tile, 32-deep k stages in a ring of STAGES LDS buffers.  Each
-// stage is filled by buffer_load_dwordx4 ... lds (lane i of an instruction
+// stage is filled by global_load_lds_dwordx4 (lane i of an instruction
 // writes the i-th 16-byte slot after the instruction's LDS base), issued
 // STAGES-1 tiles ahead; there are no staging registers and no VALU copies.
-// Buffer descriptors are re-based per tile, so lane offsets stay 32-bit and
-// loads past the operand's end read zeros.
+// Loads address a wave-uniform tile origin plus a 32-bit lane offset; rows and
+// columns past the operand's edge are clamped to its last valid row / chunk.
 //
 // LDS layouts (16-byte-chunk XOR swizzles, chosen by the source chunk of each
 // direct-load lane):
@@ -28,6 +28,7 @@
 // the tile sequence is dealt out in contiguous chunks per XCD, then swept in
 // groups of 8 tile rows.
 #include "common.h"
+#include "lds_dma.h"
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
@@ -37,75 +38,79 @@ typedef short v4s_t __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int TB = 256;              // block tile (m and n)
-constexpr int KD = 32;               // k depth of a stage
-constexpr int STAGES = 4;
-constexpr int OPB = TB * KD * 2;     // bytes of one operand's stage (16 KB)
-constexpr int NINST = OPB / 1024;    // direct-load instructions per operand and stage
+constexpr int KMIN = 32;             // k multiple every product must have
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const bf16_t* base, const bf16_t* end) {
-  const int64_t bytes = (int64_t)(end - base) * 2;
-  const int32_t nrec = bytes <= 0 ? 0 : (bytes >= 0xffffffffll ? -1 : (int32_t)(uint32_t)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, nrec, 0x00020000);
+// One direct-load instruction: 16 bytes per lane from base + off into the
+// 16-byte slot lane of `lds` (wave-uniform).
+__device__ __forceinline__ void dma16(const char* base, uint32_t off, char* lds) {
+  dma16_s(base, off, lds_addr(lds));
 }
 
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LDS_AS void*)lds, 16, voff, 0, 0, 0);
-}
+// Operand staging.  init() fixes this wave's lane offsets (relative to the
+// tile origin, clamped so that rows / columns past the operand re-read its
+// last valid row / chunk: they only feed outputs that are never stored);
+// issue() loads this wave's instructions of one stage; frag() reads one MFMA
+// operand.  Instruction j of a stage is issued by wave j % NW.
+template <bool KMAJ, int NW, int KD> struct Opnd;
 
-// Operand staging.  init() fixes the lane offsets; issue() loads instructions
-// j = first, first + step, ... of one stage; frag() reads one MFMA operand.
-template <bool KMAJ> struct Opnd;
-
-template <> struct Opnd<true> {  // P[rows][ld], k contiguous
-  uint32_t voff;
+// P[rows][ld], k contiguous: tile [256 rows][KD k], rows of 2*KD bytes
+// (CH = KD/8 chunks), chunk' = chunk ^ f(row) with f(row) = (row / (16/CH)) % CH,
+// so the 16 rows of a fragment read cover 16 distinct 4-bank groups.
+template <int NW, int KD> struct Opnd<true, NW, KD> {
+  static constexpr int CH = KD / 8, RB = 2 * KD, RPI = 1024 / RB;  // rows per instruction
+  static constexpr int NINST = TB / RPI, PER = NINST / NW;
+  uint32_t off[PER];
   int64_t ld;
-  __device__ __forceinline__ void init(int64_t ld_, int lane) {
+  static __device__ __forceinline__ int f(int row) { return (row / (16 / CH)) % CH; }
+  __device__ __forceinline__ void init(int64_t ld_, int64_t rows_left, int wave, int lane) {
     ld = ld_;
-    const int c = (lane & 3) ^ ((lane >> 4) & 3);  // row 16j + lane/4: (row >> 2) & 3 = (lane >> 4) & 3
-    voff = (uint32_t)(((lane >> 2) * ld + 8 * c) * 2);
-  }
-  // tile: rows r0.., k from k0
-  __device__ __forceinline__ const bf16_t* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
-    return P + r0 * ld + k0;
-  }
-  template <int NW>
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r, char* stage, int wave) const {
 #pragma unroll
-    for (int i = 0; i < NINST / NW; ++i) {
-      const int j = wave + NW * i;
-      dma16(r, stage + j * 1024, voff + (uint32_t)(j * 32 * ld));
+    for (int i = 0; i < PER; ++i) {
+      const int r = RPI * (wave + NW * i) + lane / CH;
+      const int c = (lane % CH) ^ f(r);
+      const int64_t rc = r < rows_left ? r : rows_left - 1;
+      off[i] = (uint32_t)((rc * ld + 8 * c) * 2);
     }
   }
-  // rows `row` (0..255) of the tile, k step ks (0..1), 8 k values at 8*half
+  // tile origin: rows r0.., k from k0
+  __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
+    return reinterpret_cast<const char*>(P + r0 * ld + k0);
+  }
+  __device__ __forceinline__ void issue(const char* o, char* stage, int wave) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
+  }
+  // row `row` (0..255) of the tile, k step ks, 8 k values at 8*half
   static __device__ __forceinline__ bf16x8_t frag(const char* stage, int row, int ks, int half, int lane) {
     (void)lane;
-    const int c = (2 * ks + half) ^ ((row >> 2) & 3);
-    return *reinterpret_cast<const bf16x8_t*>(stage + row * 64 + c * 16);
+    const int c = (2 * ks + half) ^ f(row);
+    return *reinterpret_cast<const bf16x8_t*>(stage + row * RB + c * 16);
   }
 };
 
-template <> struct Opnd<false> {  // P[k][ld], m/n contiguous
-  uint32_t voff[2];
+// P[k][ld], m/n contiguous: tile [KD k][256], 512-byte rows, chunk' = chunk ^ 4*(k & 3).
+template <int NW, int KD> struct Opnd<false, NW, KD> {
+  static constexpr int NINST = KD / 2, PER = NINST / NW;  // two k rows per instruction
+  uint32_t off[PER];
   int64_t ld;
-  __device__ __forceinline__ void init(int64_t ld_, int lane) {
+  __device__ __forceinline__ void init(int64_t ld_, int64_t cols_left, int wave, int lane) {
     ld = ld_;
+    const int last_chunk = (int)((cols_left < TB ? cols_left : TB) / 8) - 1;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {  // instruction parity: rows 2j + lane/32
-      const int row = 2 * p + (lane >> 5);
-      const int c = (lane & 31) ^ (4 * (row & 3));
-      voff[p] = (uint32_t)(((lane >> 5) * ld + 8 * c) * 2);
-    }
-  }
-  __device__ __forceinline__ const bf16_t* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
-    return P + k0 * ld + r0;
-  }
-  template <int NW>
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t r, char* stage, int wave) const {
-#pragma unroll
-    for (int i = 0; i < NINST / NW; ++i) {
+    for (int i = 0; i < PER; ++i) {
       const int j = wave + NW * i;
-      dma16(r, stage + j * 1024, voff[j & 1] + (uint32_t)(j * 4 * ld));
+      const int row = 2 * j + (lane >> 5);  // k row of the stage
+      int c = (lane & 31) ^ (4 * (row & 3));
+      c = c < last_chunk ? c : last_chunk;
+      off[i] = (uint32_t)((row * ld + 8 * c) * 2);
     }
+  }
+  __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
+    return reinterpret_cast<const char*>(P + k0 * ld + r0);
+  }
+  __device__ __forceinline__ void issue(const char* o, char* stage, int wave) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
   }
   // column `row` (0..255) of the tile, k step ks: two transposed reads of
   // k rows 16ks + 8half + {0..3} and {4..7}
@@ -122,9 +127,19 @@ template <> struct Opnd<false> {  // P[k][ld], m/n contiguous
 
 }  // namespace
 
-#define GDL_WAIT_BARRIER(n) asm volatile("s_waitcnt vmcnt(" #n ")\n\ts_barrier" ::: "memory")
+// Wait until this wave's LDS reads are back and at most N of its direct
+// loads are outstanding, then barrier; nothing is scheduled across it (so the
+// MFMAs written before it are issued before it).
+template <int N> __device__ __forceinline__ void wait_barrier() {
+  static_assert(N == 0 || N == 8 || N == 16, "add the vmcnt value");
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (N == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
-template <bool AK, bool BK, int EPI, int NW>
+template <bool AK, bool BK, int EPI, int NW, int KD, int STAGES>
 __global__ void __launch_bounds__(NW * 64, NW == 8 ? 2 : 1)
 gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
@@ -132,6 +147,9 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   constexpr int WM = 128, WN = NW == 8 ? 64 : 128;
   constexpr int FI = WM / 32, FJ = WN / 32;
   constexpr int WAVES_N = TB / WN;
+  constexpr int OPB = TB * KD * 2;   // bytes of one operand's stage
+  constexpr int KS = KD / 16;         // k steps per stage
+  constexpr int WAIT = (STAGES - 2) * KD / NW;  // loads of the later stages still in flight
   __shared__ __attribute__((aligned(1024))) char lds[STAGES][2][OPB];
 
   const int tiles_m = (int)((M + TB - 1) / TB), tiles_n = (int)((N + TB - 1) / TB);
@@ -153,23 +171,19 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int half = lane >> 5, col = lane & 31;
 
-  Opnd<AK> oa;
-  Opnd<BK> ob;
-  oa.init(lda, lane);
-  ob.init(ldb, lane);
-  const bf16_t* a_end = A + (AK ? (M - 1) * lda + K : (K - 1) * lda + M);
-  const bf16_t* b_end = B + (BK ? (N - 1) * ldb + K : (K - 1) * ldb + N);
+  Opnd<AK, NW, KD> oa;
+  Opnd<BK, NW, KD> ob;
+  oa.init(lda, M - m0, wave, lane);
+  ob.init(ldb, N - n0, wave, lane);
 
-  // Tile tt into stage tt % STAGES; tiles past the end load nothing (empty
-  // buffer view) but still count in vmcnt, which keeps the waits uniform.
+  // Tile tt into stage tt % STAGES.  Tiles past the end re-load the last
+  // tile into a stage that is never read, which keeps the vmcnt waits uniform.
   auto issue = [&](int tt) {
-    const bool live = tt < ntiles;
-    const int64_t k0 = kbeg + (int64_t)tt * KD;
+    const int live = tt < ntiles ? tt : ntiles - 1;
+    const int64_t k0 = kbeg + (int64_t)live * KD;
     char* st = lds[tt % STAGES][0];
-    const bf16_t* ao = oa.origin(A, m0, k0);
-    const bf16_t* bo = ob.origin(B, n0, k0);
-    oa.template issue<NW>(rsrc(ao, live ? a_end : ao), st, wave);
-    ob.template issue<NW>(rsrc(bo, live ? b_end : bo), st + OPB, wave);
+    oa.issue(oa.origin(A, m0, k0), st, wave);
+    ob.issue(ob.origin(B, n0, k0), st + OPB, wave);
   };
 
   f32x16_t acc[FI][FJ];
@@ -186,9 +200,9 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
     const char* sa = lds[stage][0];
     const char* sb = lds[stage][1];
 #pragma unroll
-    for (int i = 0; i < FI; ++i) fa[set][i] = Opnd<AK>::frag(sa, wm * WM + i * 32 + col, ks, half, lane);
+    for (int i = 0; i < FI; ++i) fa[set][i] = Opnd<AK, NW, KD>::frag(sa, wm * WM + i * 32 + col, ks, half, lane);
 #pragma unroll
-    for (int j = 0; j < FJ; ++j) fb[set][j] = Opnd<BK>::frag(sb, wn * WN + j * 32 + col, ks, half, lane);
+    for (int j = 0; j < FJ; ++j) fb[set][j] = Opnd<BK, NW, KD>::frag(sb, wn * WN + j * 32 + col, ks, half, lane);
   };
   auto mma = [&](int set) {
 #pragma unroll
@@ -200,33 +214,103 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 
   // Schedule per tile t (stage t % STAGES visible, F[0] = its k step 0):
   //   issue tile t + STAGES - 1 (into the stage of tile t - 1, fully read)
-  //   read F[1] = k step 1;  MFMAs of F[0]
-  //   wait for tile t + 1 and for F[1], barrier
-  //   read F[0] = tile t + 1, k step 0;  MFMAs of F[1]
-  // so every barrier has the MFMAs of one k step on each side of it.
+  //   k steps 0 .. KS-2: read the next step's fragments, MFMAs of this step
+  //   wait for tile t + 1 and for the last reads, barrier
+  //   read F[0] = tile t + 1, k step 0;  MFMAs of k step KS - 1
+  // so every barrier has MFMAs on each side of it.
+  if (ntiles > 0) {  // (every split of an eligible product has k tiles)
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue(s);
-  if constexpr (NW == 8) GDL_WAIT_BARRIER(8);
-  else GDL_WAIT_BARRIER(16);
-  read(0, 0, 0);
-  for (int tt = 0; tt < ntiles; ++tt) {
-    const int stage = tt % STAGES;
-    issue(tt + STAGES - 1);
-    read(1, stage, 1);
-    mma(0);
-    // this wave's loads of tile tt + 1 are done once at most the later
-    // STAGES - 2 tiles' loads are outstanding
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if constexpr (NW == 8) GDL_WAIT_BARRIER(8);
-    else GDL_WAIT_BARRIER(16);
-    if (tt + 1 < ntiles) read(0, (tt + 1) % STAGES, 0);
-    mma(1);
+    for (int s = 0; s < STAGES - 1; ++s) issue(s);
+    wait_barrier<WAIT>();
+    read(0, 0, 0);
+    for (int tt = 0; tt < ntiles; ++tt) {
+      const int stage = tt % STAGES;
+      issue(tt + STAGES - 1);
+#pragma unroll
+      for (int ks = 0; ks < KS - 1; ++ks) {
+        read((ks + 1) & 1, stage, ks + 1);
+        mma(ks & 1);
+      }
+      wait_barrier<WAIT>();
+      if (tt + 1 < ntiles) read(0, (tt + 1) % STAGES, 0);
+      mma((KS - 1) & 1);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // epilogue: lane owns row m = ... + col and columns n .. n+3 (n = 8*jj + 4*half)
-  float* Cf = reinterpret_cast<float*>(C);
+  // bf16 outputs (STORE / RESIDUAL) go through LDS, so that global traffic is
+  // whole 512-byte tile rows: the tile is written as bf16 into [256][256]
+  // (chunk' = chunk ^ (row & 31)), then each thread moves 16-byte chunks, 32
+  // threads per row (and reads the matching 16 bytes of R).
   bf16_t* Cb = reinterpret_cast<bf16_t*>(C);
+  if constexpr (EPI != ALODLM_EPI_ACCUM) {
+    const bool coalesced = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0 &&
+                           (EPI != ALODLM_EPI_RESIDUAL ||
+                            (ldr % 8 == 0 && reinterpret_cast<uintptr_t>(R) % 16 == 0));
+    if (coalesced) {
+      char* tile = lds[0][0];  // 128 KB: the whole stage ring
+      __syncthreads();         // every wave is done with the stages
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+        const int row = wm * WM + i * 32 + col;
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int chunk = (wn * WN + j * 32) / 8 + jj;
+            const f32x16_t& a = acc[i][j];
+            *reinterpret_cast<uint2*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4) + half * 8) =
+                make_uint2((uint32_t)float_to_bf16(alpha * a[jj * 4]) | ((uint32_t)float_to_bf16(alpha * a[jj * 4 + 1]) << 16),
+                           (uint32_t)float_to_bf16(alpha * a[jj * 4 + 2]) | ((uint32_t)float_to_bf16(alpha * a[jj * 4 + 3]) << 16));
+          }
+      }
+      __syncthreads();
+      const int chunk = threadIdx.x & 31;
+      const int64_t n = n0 + chunk * 8;
+#pragma unroll 4
+      for (int it = 0; it < TB * 32 / (NW * 64); ++it) {
+        const int row = it * (NW * 64 / 32) + (int)(threadIdx.x >> 5);
+        const int64_t m = m0 + row;
+        if (m >= M || n >= N) continue;
+        uint4 w = *reinterpret_cast<const uint4*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4));
+        if (EPI == ALODLM_EPI_RESIDUAL) {
+          // reference order: x + round_bf16(proj), rounded once more
+          float r[8], o[8];
+          if (n + 8 <= N) {
+            Vec8<bf16_t>::load(R + m * ldr + n, r);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r[e] = n + e < N ? bf16_to_float(R[m * ldr + n + e]) : 0.f;
+          }
+          const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            o[e] = r[e] + bf16_to_float((bf16_t)((e & 1) ? (wv[e >> 1] >> 16) : (wv[e >> 1] & 0xffff)));
+          if (n + 8 <= N) {
+            Vec8<bf16_t>::store(Cb + m * ldc + n, o);
+            continue;
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) Cb[m * ldc + n + e] = float_to_bf16(o[e]);
+        } else {
+          if (n + 8 <= N) {
+            *reinterpret_cast<uint4*>(Cb + m * ldc + n) = w;
+            continue;
+          }
+          const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) Cb[m * ldc + n + e] = (bf16_t)((e & 1) ? (wv[e >> 1] >> 16) : (wv[e >> 1] & 0xffff));
+        }
+      }
+      return;
+    }
+  }
+
+  // Direct epilogue (float outputs, and unaligned bf16 outputs): lane owns row
+  // m = ... + col and columns n .. n+3 (n = 8*jj + 4*half).
+  float* Cf = reinterpret_cast<float*>(C);
   float* P = partial ? partial + (int64_t)blockIdx.y * M * N : nullptr;
   const int64_t ldo = P ? N : ldc;
   const bool vec = (ldo % 4 == 0) && (reinterpret_cast<uintptr_t>(P ? (void*)P : C) % 16 == 0) &&
@@ -286,7 +370,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 // for m/n-contiguous operands, dimensions in whole 16-byte chunks.
 bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int64_t M, int64_t N,
                       int64_t K) {
-  if (M < TB || N < TB || K < KD || K % KD != 0) return false;
+  if (M < TB || N < TB || K < KMIN || K % KMIN != 0) return false;
   if (lda % 8 != 0 || ldb % 8 != 0) return false;
   if (!a_kmajor && M % 8 != 0) return false;
   if (!b_kmajor && N % 8 != 0) return false;
@@ -296,13 +380,13 @@ bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int6
 // Splits of K for ALODLM_EPI_ACCUM products with few output tiles.
 int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
-  const int64_t ksteps = K / KD;
+  const int64_t ksteps = K / KMIN;
   int64_t s = 1;
   while (tiles * s < 512 && ksteps / (s * 2) >= 32) s *= 2;
   return s;
 }
 
-template <bool AK, bool BK, int NW>
+template <bool AK, bool BK, int NW, int KD, int ST>
 static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                       int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N, int64_t K,
                       float alpha, int epi, float* part, int64_t kps, int64_t nsplit,
@@ -310,19 +394,33 @@ static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
   dim3 grid((unsigned)tiles, (unsigned)nsplit);
   if (epi == ALODLM_EPI_STORE)
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, NW><<<grid, NW * 64, 0, st>>>(
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
   else if (epi == ALODLM_EPI_RESIDUAL)
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, NW><<<grid, NW * 64, 0, st>>>(
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
   else
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, NW><<<grid, NW * 64, 0, st>>>(
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
 }
 
-#ifndef GEMM_DL_WAVES
-#define GEMM_DL_WAVES 8
+// Stage shape per operand layout: 32 k x 4 stages, or 64 k x 2 stages
+// (whole 128-byte rows per direct load for k-contiguous operands).
+#ifndef GEMM_DL_KK_DEEP
+#define GEMM_DL_KK_DEEP 0
 #endif
+#ifndef GEMM_DL_KMN_DEEP
+#define GEMM_DL_KMN_DEEP 0
+#endif
+
+template <bool AK, bool BK>
+static void launch_layout(bool deep, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb,
+                          void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
+                          int64_t K, float alpha, int epi, float* part, int64_t kps,
+                          int64_t nsplit, hipStream_t st) {
+  if (deep) launch_dl<AK, BK, 8, 64, 2>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
+  else launch_dl<AK, BK, 8, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
+}
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
 // splits > 1 (ALODLM_EPI_ACCUM only), the caller reduces it.
@@ -331,13 +429,16 @@ void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
                     int64_t* nsplit_out, hipStream_t st) {
   int64_t kps = K;
-  if (splits > 1) kps = (((K + splits - 1) / splits) + KD - 1) / KD * KD;
+  if (splits > 1) kps = (((K + splits - 1) / splits) + KMIN - 1) / KMIN * KMIN;
   const int64_t nsplit = (K + kps - 1) / kps;
   *nsplit_out = nsplit;
   float* p = (epi == ALODLM_EPI_ACCUM && nsplit > 1) ? part : nullptr;
-  constexpr int NW = GEMM_DL_WAVES;
-  if (a_kmajor && b_kmajor) launch_dl<true, true, NW>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (a_kmajor) launch_dl<true, false, NW>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (b_kmajor) launch_dl<false, true, NW>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else launch_dl<false, false, NW>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  // 64-deep stages need every split to hold whole 64-k tiles
+  const bool k64 = kps % 64 == 0;
+  const bool both = a_kmajor && b_kmajor;
+  const bool deep = k64 && (both ? GEMM_DL_KK_DEEP : GEMM_DL_KMN_DEEP);
+  if (both) launch_layout<true, true>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else if (a_kmajor) launch_layout<true, false>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else if (b_kmajor) launch_layout<false, true>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else launch_layout<false, false>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
 }
