@@ -177,8 +177,28 @@ rmsnorm_bwd_scalar_kernel(const T* __restrict__ dy, const T* __restrict__ x,
   for (int64_t c = lane; c < cols; c += 64) partial[(int64_t)blockIdx.x * cols + c] = dw_lds[c];
 }
 
-// out[c - col0] += sum_p partial[p * ld + c] for c in [col0, col0 + ncols), in
-// a fixed order: 64 columns x 4 partial groups per block, combined in LDS.
+// out[c - col0] += sum_p partial[p * ld + col0 + c] for c < ncols, in a fixed
+// order, in two passes: column_split_kernel sums contiguous groups of partial
+// rows into `tmp` ([groups][ncols]); column_reduce_kernel then adds the group
+// sums in order.  Each block covers 64 columns with 4 interleaved row streams
+// combined in LDS.
+__global__ void __launch_bounds__(256)
+column_split_kernel(const float* __restrict__ partial, int64_t nparts, int64_t ld, int64_t col0,
+                    int64_t ncols, int64_t per_group, float* __restrict__ tmp) {
+  __shared__ float sm[4][64];
+  const int cx = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + cx;
+  const int64_t p0 = (int64_t)blockIdx.y * per_group;
+  const int64_t p1 = p0 + per_group < nparts ? p0 + per_group : nparts;
+  float s = 0.f;
+  if (c < ncols)
+    for (int64_t p = p0 + g; p < p1; p += 4) s += partial[p * ld + col0 + c];
+  sm[g][cx] = s;
+  __syncthreads();
+  if (g == 0 && c < ncols)
+    tmp[(int64_t)blockIdx.y * ncols + c] = ((sm[0][cx] + sm[1][cx]) + sm[2][cx]) + sm[3][cx];
+}
+
 __global__ void __launch_bounds__(256)
 column_reduce_kernel(const float* __restrict__ partial, int64_t nparts, int64_t ld, int64_t col0,
                      int64_t ncols, float* __restrict__ out) {
@@ -193,10 +213,23 @@ column_reduce_kernel(const float* __restrict__ partial, int64_t nparts, int64_t 
   if (g == 0 && c < ncols) out[c] += ((sm[0][cx] + sm[1][cx]) + sm[2][cx]) + sm[3][cx];
 }
 
+int64_t column_reduce_groups(int64_t nparts) {
+  const int64_t g = (nparts + 15) / 16;
+  return g < COLUMN_REDUCE_MAX_GROUPS ? g : COLUMN_REDUCE_MAX_GROUPS;
+}
+
 int column_reduce(const float* partial, int64_t nparts, int64_t ld, int64_t col0, int64_t ncols,
-                  float* out, hipStream_t st) {
+                  float* out, float* tmp, hipStream_t st) {
   if (ncols == 0 || nparts == 0) return ALODLM_OK;
-  column_reduce_kernel<<<ceil_div_u(ncols, 64), 256, 0, st>>>(partial, nparts, ld, col0, ncols, out);
+  const int64_t groups = column_reduce_groups(nparts);
+  if (groups > 1) {
+    const int64_t per = (nparts + groups - 1) / groups;
+    column_split_kernel<<<dim3(ceil_div_u(ncols, 64), (unsigned)groups), 256, 0, st>>>(
+        partial, nparts, ld, col0, ncols, per, tmp);
+    column_reduce_kernel<<<ceil_div_u(ncols, 64), 256, 0, st>>>(tmp, groups, ncols, 0, ncols, out);
+  } else {
+    column_reduce_kernel<<<ceil_div_u(ncols, 64), 256, 0, st>>>(partial, nparts, ld, col0, ncols, out);
+  }
   ALODLM_CHECK_LAUNCH("column_reduce");
   return ALODLM_OK;
 }
@@ -218,7 +251,8 @@ extern "C" int alodlm_rmsnorm_fwd(const void* x, const void* w, void* y, float* 
 }
 
 extern "C" int64_t alodlm_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
-  return ((rows + BWD_ROWS_PER_BLOCK - 1) / BWD_ROWS_PER_BLOCK) * cols;
+  // per-block partial rows, then the column reduction's group sums
+  return ((rows + BWD_ROWS_PER_BLOCK - 1) / BWD_ROWS_PER_BLOCK + COLUMN_REDUCE_MAX_GROUPS) * cols;
 }
 
 static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, const void* w,
@@ -252,7 +286,8 @@ static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, 
           cols, skip_exits, skip_depth);
   });
   ALODLM_CHECK_LAUNCH("rmsnorm_bwd");
-  if (dw_accum) return column_reduce(workspace, nparts, cols, 0, cols, dw_accum, st);
+  if (dw_accum)
+    return column_reduce(workspace, nparts, cols, 0, cols, dw_accum, workspace + nparts * cols, st);
   return ALODLM_OK;
 }
 

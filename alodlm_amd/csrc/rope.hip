@@ -10,6 +10,8 @@
 #include "common.h"
 #include "norm.h"
 
+#include <type_traits>
+
 #define ROPE_WAVES 4
 #define ROPE_MAX_T 2  // pairs per lane: dh/2 <= 128
 
@@ -167,6 +169,165 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
   }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 128, bf16: four heads per wavefront pass, 16 lanes per head, lane j
+// owning rotary elements i = 4j..4j+3 and i + 64 (8-byte accesses); sums over
+// a head are 16-lane reductions.  Same arithmetic and rounding points as the
+// kernels above.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ void load4(const bf16_t* p, float* v) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  v[0] = bf16_to_float((bf16_t)(u.x & 0xffff)); v[1] = bf16_to_float((bf16_t)(u.x >> 16));
+  v[2] = bf16_to_float((bf16_t)(u.y & 0xffff)); v[3] = bf16_to_float((bf16_t)(u.y >> 16));
+}
+__device__ __forceinline__ void store4(bf16_t* p, const float* v) {
+  *reinterpret_cast<uint2*>(p) =
+      make_uint2((uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16),
+                 (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16));
+}
+
+__global__ void __launch_bounds__(64 * ROPE_WAVES)
+qknorm_rope128_fwd_kernel(const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ wq,
+                          const bf16_t* __restrict__ wk, const int64_t* __restrict__ positions,
+                          const float* __restrict__ inv_freq, bf16_t* __restrict__ q_out,
+                          bf16_t* __restrict__ k_out, int64_t rows, int nq, int nkv, float eps) {
+  const int lane = threadIdx.x & 63, slot = lane >> 4, j = lane & 15;
+  const int64_t row = (int64_t)blockIdx.x * ROPE_WAVES + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int i0 = 4 * j;
+  const float pos = (float)positions[row];
+  float cs[4], sn[4], wqa[4], wqb[4], wka[4], wkb[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float ang = pos * inv_freq[i0 + e];
+    cs[e] = round_bf16(cosf(ang));
+    sn[e] = round_bf16(sinf(ang));
+  }
+  load4(wq + i0, wqa); load4(wq + i0 + 64, wqb);
+  load4(wk + i0, wka); load4(wk + i0 + 64, wkb);
+  const int heads = nq + nkv;
+  const bf16_t* src = qkv + row * (int64_t)(nq + 2 * nkv) * 128;
+  for (int h0 = 0; h0 < heads; h0 += 4) {
+    const int head = h0 + slot;
+    const bool live = head < heads;
+    const bool is_q = head < nq;
+    float xa[4] = {0.f, 0.f, 0.f, 0.f}, xb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) { load4(src + head * 128 + i0, xa); load4(src + head * 128 + i0 + 64, xb); }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += xa[e] * xa[e] + xb[e] * xb[e];
+    ss = sum16(ss);
+    const float r = 1.0f / sqrtf(ss / 128.f + eps);
+    float oa[4], ob[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = round_bf16((is_q ? wqa[e] : wka[e]) * round_bf16(xa[e] * r));
+      const float b = round_bf16((is_q ? wqb[e] : wkb[e]) * round_bf16(xb[e] * r));
+      oa[e] = round_bf16(a * cs[e]) + round_bf16(-b * sn[e]);
+      ob[e] = round_bf16(b * cs[e]) + round_bf16(a * sn[e]);
+    }
+    if (live) {
+      bf16_t* dst = is_q ? q_out + (row * nq + head) * 128 : k_out + (row * nkv + head - nq) * 128;
+      store4(dst + i0, oa);
+      store4(dst + i0 + 64, ob);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(64 * ROPE_WAVES)
+qknorm_rope128_bwd_kernel(const bf16_t* __restrict__ dq, const bf16_t* __restrict__ dk,
+                          const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ wq,
+                          const bf16_t* __restrict__ wk, const int64_t* __restrict__ positions,
+                          const float* __restrict__ inv_freq, bf16_t* __restrict__ dqkv,
+                          float* __restrict__ partial, int64_t rows, int nq, int nkv, float eps) {
+  __shared__ float lds[ROPE_WAVES * 4][2 * 128];  // [wave*4 + slot][dwq | dwk]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane >> 4, j = lane & 15;
+  const int i0 = 4 * j;
+  const int heads = nq + nkv;
+  const int64_t width = (int64_t)(nq + 2 * nkv) * 128;
+  float wqa[4], wqb[4], wka[4], wkb[4];
+  float gqa[4] = {0.f, 0.f, 0.f, 0.f}, gqb[4] = {0.f, 0.f, 0.f, 0.f};
+  float gka[4] = {0.f, 0.f, 0.f, 0.f}, gkb[4] = {0.f, 0.f, 0.f, 0.f};
+  load4(wq + i0, wqa); load4(wq + i0 + 64, wqb);
+  load4(wk + i0, wka); load4(wk + i0 + 64, wkb);
+  const int64_t r0 = (int64_t)blockIdx.x * ROPE_BWD_ROWS;
+  for (int64_t row = r0 + wave; row < r0 + ROPE_BWD_ROWS && row < rows; row += ROPE_WAVES) {
+    const float pos = (float)positions[row];
+    float cs[4], sn[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ang = pos * inv_freq[i0 + e];
+      cs[e] = round_bf16(cosf(ang));
+      sn[e] = round_bf16(sinf(ang));
+    }
+    for (int h0 = 0; h0 < heads; h0 += 4) {
+      const int head = h0 + slot;
+      const bool live = head < heads;
+      const bool is_q = head < nq;
+      float xa[4] = {0.f, 0.f, 0.f, 0.f}, xb[4] = {0.f, 0.f, 0.f, 0.f};
+      float go[4] = {0.f, 0.f, 0.f, 0.f}, gh[4] = {0.f, 0.f, 0.f, 0.f};
+      if (live) {
+        const bf16_t* x = qkv + row * width + head * 128;
+        const bf16_t* g = is_q ? dq + (row * nq + head) * 128 : dk + (row * nkv + head - nq) * 128;
+        load4(x + i0, xa); load4(x + i0 + 64, xb);
+        load4(g + i0, go); load4(g + i0 + 64, gh);
+      }
+      float ta[4], tb[4], ss = 0.f, s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ta[e] = go[e] * cs[e] + gh[e] * sn[e];   // d/d t[i]
+        tb[e] = gh[e] * cs[e] - go[e] * sn[e];   // d/d t[i + half]
+        ss += xa[e] * xa[e] + xb[e] * xb[e];
+        s += ta[e] * (is_q ? wqa[e] : wka[e]) * xa[e] + tb[e] * (is_q ? wqb[e] : wkb[e]) * xb[e];
+      }
+      ss = sum16(ss);
+      s = sum16(s);
+      const float r = 1.0f / sqrtf(ss / 128.f + eps);
+      const float k = s * r * r * r / 128.f;
+      float oa[4], ob[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float na = round_bf16(xa[e] * r), nb = round_bf16(xb[e] * r);
+        if (is_q) { gqa[e] += ta[e] * na; gqb[e] += tb[e] * nb; }
+        else { gka[e] += ta[e] * na; gkb[e] += tb[e] * nb; }
+        oa[e] = r * ta[e] * (is_q ? wqa[e] : wka[e]) - xa[e] * k;
+        ob[e] = r * tb[e] * (is_q ? wqb[e] : wkb[e]) - xb[e] * k;
+      }
+      if (live) {
+        bf16_t* out = dqkv + row * width + head * 128;
+        store4(out + i0, oa);
+        store4(out + i0 + 64, ob);
+      }
+    }
+  }
+  float* L = lds[wave * 4 + slot];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    L[i0 + e] = gqa[e]; L[i0 + 64 + e] = gqb[e];
+    L[128 + i0 + e] = gka[e]; L[128 + i0 + 64 + e] = gkb[e];
+  }
+  __syncthreads();
+  {
+    const int c = threadIdx.x;  // 256 threads = 2 * 128 columns
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < ROPE_WAVES * 4; ++v) acc += lds[v][c];
+    partial[(int64_t)blockIdx.x * 256 + c] = acc;
+  }
+}
+
+// The head_dim-128 kernels make 8-byte accesses.
+static bool rope128_aligned(const void* a, const void* b, const void* c) {
+  return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+           reinterpret_cast<uintptr_t>(c)) & 7) == 0;
+}
+
 static int check_rope(int64_t rows, int64_t nq, int64_t nkv, int64_t dh) {
   ALODLM_CHECK_ARG(rows >= 0 && nq > 0 && nkv > 0, "qknorm_rope: bad head counts");
   ALODLM_CHECK_ARG(dh > 0 && dh % 2 == 0 && dh <= 128 * ROPE_MAX_T,
@@ -182,6 +343,13 @@ extern "C" int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const voi
   if (rc) return rc;
   if (rows == 0) return ALODLM_OK;
   ALODLM_DISPATCH(dtype, T, {
+    if (std::is_same<T, bf16_t>::value && dh == 128 && rope128_aligned(qkv, q_out, k_out)) {
+      qknorm_rope128_fwd_kernel<<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
+                                  as_stream(stream)>>>(
+          (const bf16_t*)qkv, (const bf16_t*)wq, (const bf16_t*)wk, positions, inv_freq,
+          (bf16_t*)q_out, (bf16_t*)k_out, rows, (int)nq, (int)nkv, eps);
+      break;
+    }
     qknorm_rope_fwd_kernel<T><<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
                                 as_stream(stream)>>>(
         (const T*)qkv, (const T*)wq, (const T*)wk, positions, inv_freq, (T*)q_out, (T*)k_out,
@@ -194,7 +362,8 @@ extern "C" int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const voi
 extern "C" int64_t alodlm_qknorm_rope_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv,
                                                     int64_t dh) {
   (void)nq; (void)nkv;
-  return ((rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS) * 2 * dh;
+  // per-block partial rows [dwq | dwk], then the column reduction's group sums
+  return ((rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS) * 2 * dh + COLUMN_REDUCE_MAX_GROUPS * dh;
 }
 
 extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv,
@@ -208,13 +377,22 @@ extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void
   const int64_t nparts = (rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS;
   hipStream_t st = as_stream(stream);
   ALODLM_DISPATCH(dtype, T, {
+    if (std::is_same<T, bf16_t>::value && dh == 128 && rope128_aligned(dq, dk, qkv) &&
+        rope128_aligned(dqkv, wq, wk)) {
+      qknorm_rope128_bwd_kernel<<<(unsigned)nparts, 64 * ROPE_WAVES, 0, st>>>(
+          (const bf16_t*)dq, (const bf16_t*)dk, (const bf16_t*)qkv, (const bf16_t*)wq,
+          (const bf16_t*)wk, positions, inv_freq, (bf16_t*)dqkv, workspace, rows, (int)nq,
+          (int)nkv, eps);
+      break;
+    }
     qknorm_rope_bwd_kernel<T><<<(unsigned)nparts, 64 * ROPE_WAVES,
                                 ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
         (const T*)dq, (const T*)dk, (const T*)qkv, (const T*)wq, (const T*)wk, positions,
         inv_freq, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps);
   });
   ALODLM_CHECK_LAUNCH("qknorm_rope_bwd");
-  rc = column_reduce(workspace, nparts, 2 * dh, 0, dh, dwq_accum, st);
+  float* tmp = workspace + nparts * 2 * dh;
+  rc = column_reduce(workspace, nparts, 2 * dh, 0, dh, dwq_accum, tmp, st);
   if (rc) return rc;
-  return column_reduce(workspace, nparts, 2 * dh, dh, dh, dwk_accum, st);
+  return column_reduce(workspace, nparts, 2 * dh, dh, dh, dwk_accum, tmp, st);
 }

@@ -379,10 +379,16 @@ class StepEngine:
             R = int(sel_count.item())
             rec["R"], rec["sel_rows"] = R, sel_rows
             if R:
-                xsel = self._empty(R, H)
+                # Rows padded to a multiple of 32 with zeros: their logits and
+                # dL/dlogits are exactly zero, and the LM-head dW product (whose
+                # depth is the row count) runs on whole 32-deep k stages.
+                Rp = -(-R // 32) * 32
+                xsel = self._empty(Rp, H)
+                if Rp > R:
+                    xsel[R:].zero_()
                 call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
-                logits = self._empty(R, V)
-                self._gemm(xsel, H, 1, self.lm_head, H, 1, logits, V, R, V, H)
+                logits = self._empty(Rp, V)
+                self._gemm(xsel, H, 1, self.lm_head, H, 1, logits, V, Rp, V, H)
                 ce = torch.empty(R, dtype=torch.float32, device=self.device)
                 call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
                      ptr(sel_count), R, V, ptr(ce), None, c, st)
@@ -430,8 +436,8 @@ class StepEngine:
                 # d readout = dlogits . W_lm ; dW_lm += dlogits^T . readout
                 self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
                            alpha=grad_scale)
-                self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H, R,
-                           alpha=grad_scale, epi=EPI_ACCUM)
+                self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H,
+                           rec["xsel"].shape[0], alpha=grad_scale, epi=EPI_ACCUM)
                 call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
                      c, st)
                 del dsel
