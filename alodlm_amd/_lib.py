@@ -41,7 +41,7 @@ SIGNATURES = {
     "alodlm_attention_bwd": [P, P, P, I64, P, P, P, P, P, P, I64, P, P, P, I64, P, I64, I64, I64,
                              I64, I64, I32, P],
     "alodlm_swiglu_fwd": [P, P, I64, I64, I32, P],
-    "alodlm_swiglu_bwd": [P, P, P, I64, I64, I32, P],
+    "alodlm_swiglu_bwd": [P, P, P, P, I64, I64, I32, P],
     "alodlm_final_norm_gate": [P, P, P, P, P, I64, P, P, P, I64, I64, F32, I32, P],
     "alodlm_carry_select": [P, P, P, P, P, I64, P, P, I64, I64, I64, F32, I32, P],
     "alodlm_carry_select_bwd": [P, P, P, P, P, I64, P, P, P, P, P, P, I64, I64, I64, I32, P],
@@ -60,6 +60,7 @@ SIGNATURES = {
     "alodlm_adamw": [P, P, P, P, P, P, P, P, P, I64, I64, P, F32, F32, F32, F32, F32, I64, I32, P],
     "alodlm_cast_f32": [P, P, I64, I32, P],
     "alodlm_scale_f32": [P, P, I64, P],
+    "alodlm_transpose": [P, P, I64, I64, I32, P],
 }
 _RESTYPE = {
     "alodlm_last_error": ctypes.c_char_p,

@@ -63,26 +63,57 @@ def attention_mask(length, block_size, device):
     return ((q_block == k_block) & (q_noisy == k_noisy) & (k <= q)) | ((k_block < q_block) & ~k_noisy)
 
 
+_DRAW_STREAMS = {}
+
+
+def _draw_stream(device):
+    """Per-device side stream (default priority) for the masking draws.
+
+    The draws read no device data, so they need not wait for the compute
+    stream: on a stream of their own, the host reads the per-segment mask
+    ratios back without draining the previous step's queued work.  The
+    generator's state advances on the host at launch time, so the values and
+    their order are the same as on the compute stream."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _DRAW_STREAMS.get(index)
+    if stream is None:
+        stream = _DRAW_STREAMS[index] = torch.cuda.Stream(device=torch.device("cuda", index))
+    return stream
+
+
 def draw_masking(labels_host, offsets, block_size, device, generator=None):
     """Draw the masking randomness in the reference's order.
 
     Returns per-block arrays (p, count) on the host and the list of per-block
-    permutations (device tensors, or None where count is zero).
+    permutations (tensors on ``device``, or None where count is zero).  On a
+    GPU the draws are issued on the side stream of ``_draw_stream``; the
+    caller orders its own stream after that one before reading them.
     """
+    device = torch.device(device)
+    if device.type == "cuda":
+        with torch.cuda.stream(_draw_stream(device)):
+            return _draw(labels_host, offsets, block_size, device, generator)
+    return _draw(labels_host, offsets, block_size, device, generator)
+
+
+def _draw(labels_host, offsets, block_size, device, generator):
     probs, counts, perms = [], [], []
     for a, b in zip(offsets, offsets[1:]):
         length = b - a
         nblocks = (length + block_size - 1) // block_size
         u = torch.empty(nblocks, device=device).uniform_(0, 1, generator=generator).clamp_min(1e-8)
-        u_host = u.tolist()
-        seg_labels = labels_host[a:b]
+        # p as the reference reads it (a float32 value widened to float64), the
+        # supervised count n of every block, and round(n * p) rounded half to
+        # even in float64 like Python's round (alodlm/batch.py:50-57)
+        p = u.cpu().numpy().astype(np.float64)
+        valid = (labels_host[a:b] != -100).astype(np.int64)
+        n = np.add.reduceat(valid, np.arange(0, length, block_size))
+        count = np.rint(n * p).astype(np.int64)
+        probs.extend(p.tolist())
+        counts.extend(count.tolist())
         for blk in range(nblocks):
-            left = blk * block_size
-            n = int((seg_labels[left:left + block_size] != -100).sum())
-            count = round(n * u_host[blk])
-            probs.append(u_host[blk])
-            counts.append(count)
-            perms.append(torch.randperm(n, device=device, generator=generator) if count else None)
+            perms.append(torch.randperm(int(n[blk]), device=device, generator=generator)
+                         if count[blk] else None)
     return np.asarray(probs, dtype=np.float32), np.asarray(counts, dtype=np.int32), perms
 
 
@@ -108,22 +139,28 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     if device.type != "cuda":
         raise ValueError("build_batch runs on the GPU; move ids/labels to a CUDA device")
     labels_host = labels.detach().cpu().numpy()
-    if draws is None:
-        draws = draw_masking(labels_host, offsets, block_size, device, generator)
-    probs, counts, perms = draws
     nseg = len(offsets) - 1
     seg_block = [0]
     for a, b in zip(offsets, offsets[1:]):
         seg_block.append(seg_block[-1] + (b - a + block_size - 1) // block_size)
     nblocks = seg_block[-1]
-    perm_offset = np.zeros(nblocks, dtype=np.int64)
-    chunks, total = [], 0
-    for i, perm in enumerate(perms):
-        perm_offset[i] = total
-        if perm is not None:
-            chunks.append(perm.to(device=device, dtype=torch.int64))
-            total += perm.numel()
-    perm_buf = torch.cat(chunks) if chunks else torch.zeros(1, dtype=torch.int64, device=device)
+    side = _draw_stream(device)
+    with torch.cuda.stream(side):
+        if draws is None:
+            draws = _draw(labels_host, offsets, block_size, device, generator)
+        probs, counts, perms = draws
+        perm_offset = np.zeros(nblocks, dtype=np.int64)
+        chunks, total = [], 0
+        for i, perm in enumerate(perms):
+            perm_offset[i] = total
+            if perm is not None:
+                chunks.append(perm.to(device=device, dtype=torch.int64))
+                total += perm.numel()
+        perm_buf = (torch.cat(chunks) if chunks
+                    else torch.zeros(1, dtype=torch.int64, device=device))
+    main = torch.cuda.current_stream(device)
+    main.wait_stream(side)
+    perm_buf.record_stream(main)
     ids = ids.to(torch.int64).contiguous()
     labels = labels.to(torch.int64).contiguous()
     n = 2 * len(ids)

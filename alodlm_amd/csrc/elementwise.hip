@@ -54,14 +54,18 @@ __global__ void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ act,
   else Elem<T>::store(act, i, a[0]);
 }
 
-// dgate = dact * up * silu'(gate), dup = dact * silu(gate)
+// dgate = dact * up * silu'(gate), dup = dact * silu(gate); where act is not
+// null the forward product act = cast(cast(silu(gate)) * up) is written too
+// (the same expression as swiglu_fwd_kernel, so the value is bit-identical),
+// which saves the backward a separate recompute pass over gu.
 template <typename T, int W>
 __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restrict__ gu,
-                                  T* __restrict__ dgu, int64_t rows, int64_t I) {
+                                  T* __restrict__ dgu, T* __restrict__ act, int64_t rows,
+                                  int64_t I) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
   if (i >= rows * I) return;
   const int64_t r = i / I, c = i % I;
-  float g[8], u[8], da[8], dg[8], du[8];
+  float g[8], u[8], da[8], dg[8], du[8], a[8];
   if (W == 8) {
     Vec8<T>::load(gu + r * 2 * I + c, g);
     Vec8<T>::load(gu + r * 2 * I + I + c, u);
@@ -76,13 +80,40 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restric
     const float sg = 1.0f / (1.0f + expf(-g[e]));
     dg[e] = da[e] * u[e] * (sg * (1.0f + g[e] * (1.0f - sg)));
     du[e] = da[e] * Elem<T>::round(g[e] * sg);
+    a[e] = Elem<T>::round(g[e] / (1.0f + expf(-g[e]))) * u[e];
   }
   if (W == 8) {
     Vec8<T>::store(dgu + r * 2 * I + c, dg);
     Vec8<T>::store(dgu + r * 2 * I + I + c, du);
+    if (act) Vec8<T>::store(act + i, a);
   } else {
     Elem<T>::store(dgu, r * 2 * I + c, dg[0]);
     Elem<T>::store(dgu, r * 2 * I + I + c, du[0]);
+    if (act) Elem<T>::store(act, i, a[0]);
+  }
+}
+
+// dst[c][r] = src[r][c] for a rows x cols matrix, through a 64 x 64 LDS tile
+// (row pitch 65 elements, so the column reads of the transposed pass fall in
+// distinct banks).  One workgroup of 256 threads per tile.
+template <typename T>
+__global__ void __launch_bounds__(256)
+transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols) {
+  __shared__ T tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rr = ty + 4 * i;
+    const int64_t r = r0 + rr, c = c0 + tx;
+    if (r < rows && c < cols) tile[rr][tx] = src[r * cols + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int cc = ty + 4 * i;
+    const int64_t c = c0 + cc, r = r0 + tx;
+    if (r < rows && c < cols) dst[c * rows + r] = tile[tx][cc];
   }
 }
 
@@ -137,20 +168,34 @@ extern "C" int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_
   return ALODLM_OK;
 }
 
-extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, int64_t rows,
-                                 int64_t inter, int dtype, void* stream) {
+extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, void* act,
+                                 int64_t rows, int64_t inter, int dtype, void* stream) {
   if (rows == 0) return ALODLM_OK;
   const bool v8 = inter % 8 == 0 && aligned8(gu, dtype) && aligned8(dact, dtype) &&
-                  aligned8(dgu, dtype);
+                  aligned8(dgu, dtype) && (act == nullptr || aligned8(act, dtype));
   ALODLM_DISPATCH(dtype, T, {
     if (v8)
       swiglu_bwd_kernel<T, 8><<<ceil_div_u(rows * inter / 8, 256), 256, 0, as_stream(stream)>>>(
-          (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
+          (const T*)dact, (const T*)gu, (T*)dgu, (T*)act, rows, inter);
     else
       swiglu_bwd_kernel<T, 1><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
-          (const T*)dact, (const T*)gu, (T*)dgu, rows, inter);
+          (const T*)dact, (const T*)gu, (T*)dgu, (T*)act, rows, inter);
   });
   ALODLM_CHECK_LAUNCH("swiglu_bwd");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
+                                void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && cols >= 0, "transpose: negative shape");
+  ALODLM_CHECK_ARG(rows <= 64 * 65535LL, "transpose: too many rows");
+  if (rows == 0 || cols == 0) return ALODLM_OK;
+  ALODLM_CHECK_ARG(src != dst, "transpose: in-place transpose is not supported");
+  dim3 grid(ceil_div_u(cols, 64), ceil_div_u(rows, 64));
+  ALODLM_DISPATCH(dtype, T, {
+    transpose_kernel<T><<<grid, 256, 0, as_stream(stream)>>>((const T*)src, (T*)dst, rows, cols);
+  });
+  ALODLM_CHECK_LAUNCH("transpose");
   return ALODLM_OK;
 }
 

@@ -418,6 +418,12 @@ static void launch_layout(bool deep, const bf16_t* A, int64_t lda, const bf16_t*
                           void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
                           int64_t nsplit, hipStream_t st) {
+#ifdef GEMM_DL_KK_CFG
+  if (AK && BK) {
+    if (GEMM_DL_KK_CFG == 2) { launch_dl<AK, BK, 4, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st); return; }
+    if (GEMM_DL_KK_CFG == 3 && deep) { launch_dl<AK, BK, 4, 64, 2>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st); return; }
+  }
+#endif
   if (deep) launch_dl<AK, BK, 8, 64, 2>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
   else launch_dl<AK, BK, 8, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
 }

@@ -4,7 +4,7 @@
 whole step of alodlm/model.py:130-187 as an explicit schedule of kernel
 launches on the current stream:
 
-forward   embed -> prelude -> for each depth: (re-embed/carry) -> core -> coda
+forward   weight transposes -> embed -> prelude -> for each depth: (re-embed/carry) -> core -> coda
           -> final norm + gate -> exit sampling -> loss-bearing row selection
           -> LM head GEMM -> vocabulary CE (writes dL/dlogits in place)
           -> objective kernel (loss, metrics, dL/dgate)
@@ -135,6 +135,38 @@ class _Layer:
         self.kn = arena.view(buf, pre + "self_attn.k_norm.weight")
 
 
+class _TransposedWeights:
+    """Out-contiguous copies ([in, out]) of every forward product's weight.
+
+    The forward products C = X . W^T then read W^T with out-contiguous rows,
+    the operand layout the GEMM kernel streams fastest (whole 512-byte rows per
+    direct load instead of 64-byte pieces of k-contiguous rows).  The copies
+    are refreshed from the arena at the start of every forward, so they always
+    match the parameters; the backward keeps using the arena itself."""
+
+    def __init__(self, engine):
+        pairs = []   # (source [rows, cols], attribute owner, name)
+        for layer in engine.layers:
+            pairs += [(layer.wqkv, layer, "wqkv_t"), (layer.wo, layer, "wo_t"),
+                      (layer.wgu, layer, "wgu_t"), (layer.wd, layer, "wd_t")]
+        pairs.append((engine.lm_head, engine, "lm_head_t"))
+        total, spans = 0, []
+        for src, _, _ in pairs:
+            spans.append(total)
+            total += (src.numel() + _ALIGN - 1) // _ALIGN * _ALIGN
+        self.buf = torch.empty(total, dtype=engine.dtype, device=engine.device)
+        self.jobs = []
+        for (src, owner, name), off in zip(pairs, spans):
+            rows, cols = src.shape
+            dst = self.buf[off:off + src.numel()].view(cols, rows)
+            setattr(owner, name, dst)
+            self.jobs.append((src, dst, rows, cols))
+
+    def refresh(self, code, stream):
+        for src, dst, rows, cols in self.jobs:
+            call("alodlm_transpose", ptr(src), ptr(dst), rows, cols, code, stream)
+
+
 class StepEngine:
     """Runs the ALoDLM step of one model on its GPU (see the module docstring)."""
 
@@ -162,6 +194,7 @@ class StepEngine:
         self.gate_w = a.view(a.flat, "exit_gate.net.weight")
         self.gate_b = a.view(a.flat, "exit_gate.net.bias")
         self.depth_bias = a.view(a.flat, "exit_gate.depth_bias")
+        self.transposed = _TransposedWeights(self)
         # rotary inverse frequencies exactly as [tf] modeling_qwen3.py:115-117 (float32)
         inv = 1.0 / (d.theta ** (torch.arange(0, d.head_dim, 2, dtype=torch.float32) / d.head_dim))
         self.inv_freq = inv.to(self.device)
@@ -218,7 +251,7 @@ class StepEngine:
         rstd1 = self._empty(N, dtype=torch.float32)
         call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), ptr(rstd1), N, H, d.eps, c, st)
         qkv = self._empty(N, W)
-        self._gemm(h1, H, 1, w.wqkv, H, 1, qkv, W, N, W, H)
+        self._gemm(h1, H, 1, w.wqkv_t, W, 0, qkv, W, N, W, H)
         del h1
         q = self._empty(N, d.heads * d.head_dim)
         k = self._empty(N, d.kv_heads * d.head_dim)
@@ -230,18 +263,18 @@ class StepEngine:
         self._attention_fwd(q, k, v, o, lse, b)
         del q, k
         x1 = self._empty(N, H)
-        self._gemm(o, d.heads * d.head_dim, 1, w.wo, d.heads * d.head_dim, 1, x1, H, N, H,
+        self._gemm(o, d.heads * d.head_dim, 1, w.wo_t, H, 0, x1, H, N, H,
                    d.heads * d.head_dim, epi=EPI_RESIDUAL, R=x, ldr=H)
         h2 = self._empty(N, H)
         rstd2 = self._empty(N, dtype=torch.float32)
         call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), ptr(rstd2), N, H, d.eps, c, st)
         gu = self._empty(N, 2 * I)
-        self._gemm(h2, H, 1, w.wgu, H, 1, gu, 2 * I, N, 2 * I, H)
+        self._gemm(h2, H, 1, w.wgu_t, 2 * I, 0, gu, 2 * I, N, 2 * I, H)
         del h2
         act = self._empty(N, I)
         call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
         y = self._empty(N, H)
-        self._gemm(act, I, 1, w.wd, I, 1, y, H, N, H, I, epi=EPI_RESIDUAL, R=x1, ldr=H)
+        self._gemm(act, I, 1, w.wd_t, H, 0, y, H, N, H, I, epi=EPI_RESIDUAL, R=x1, ldr=H)
         if save is not None:
             save.append((li, x, rstd1, qkv, o, lse, x1, rstd2, gu))
         return y
@@ -252,16 +285,15 @@ class StepEngine:
         w, gw = self.layers[li], self.grad_layers[li]
         H, W, I = d.hidden, d.qkv_width, d.intermediate
         QD = d.heads * d.head_dim
-        # ---- MLP: y = x1 + act . Wd^T
-        act = self._empty(N, I)
-        call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
+        # ---- MLP: y = x1 + act . Wd^T  (the SwiGLU backward also rewrites act)
         dact = self._empty(N, I)
         self._gemm(dy, H, 1, w.wd, I, 0, dact, I, N, I, H)
+        act = self._empty(N, I)
+        dgu = self._empty(N, 2 * I)
+        call("alodlm_swiglu_bwd", ptr(dact), ptr(gu), ptr(dgu), ptr(act), N, I, c, st)
+        del dact
         self._gemm(dy, H, 0, act, I, 0, gw.wd, I, H, I, N, epi=EPI_ACCUM)
         del act
-        dgu = self._empty(N, 2 * I)
-        call("alodlm_swiglu_bwd", ptr(dact), ptr(gu), ptr(dgu), N, I, c, st)
-        del dact
         h2 = self._empty(N, H)
         call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
         dh2 = self._empty(N, H)
@@ -316,6 +348,7 @@ class StepEngine:
         cfg, d = self.cfg, self.dims
         K = cfg.max_depth
         st, c = self._stream(), self.code
+        self.transposed.refresh(c, st)
         ids = ids.to(self.device)
         labels = labels.to(self.device)
         b = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id,
@@ -388,7 +421,7 @@ class StepEngine:
                     xsel[R:].zero_()
                 call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
                 logits = self._empty(Rp, V)
-                self._gemm(xsel, H, 1, self.lm_head, H, 1, logits, V, Rp, V, H)
+                self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
                 ce = torch.empty(R, dtype=torch.float32, device=self.device)
                 call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
                      ptr(sel_count), R, V, ptr(ce), None, c, st)

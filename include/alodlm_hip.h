@@ -159,8 +159,10 @@ int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ld
  * ------------------------------------------------------------------------ */
 int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_t inter, int dtype,
                       void* stream);
-int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, int64_t rows, int64_t inter,
-                      int dtype, void* stream);
+/* act (nullable): also write the forward product, bit-identical to
+ * alodlm_swiglu_fwd's, so the backward needs no separate recompute pass. */
+int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, void* act, int64_t rows,
+                      int64_t inter, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Readout and halting (alodlm/model.py:152-168).
@@ -289,6 +291,14 @@ int alodlm_adamw(void* const* params, float* const* master, float* const* exp_av
 /* Elementwise helpers. */
 int alodlm_cast_f32(const float* src, void* dst, int64_t n, int dtype, void* stream);
 int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream);
+/* dst[c][r] = src[r][c] for a row-major rows x cols matrix (dst and src must
+ * not overlap).  The step keeps transposed copies of the projection and
+ * LM-head weights ([in, out], refreshed at the start of every forward) so
+ * that every forward product reads its weight operand in out-contiguous
+ * rows; it replaces the weight layout the forward products of
+ * alodlm/model.py:52-58,161 read through torch.nn.Linear. */
+int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
+                     void* stream);
 
 #ifdef __cplusplus
 }

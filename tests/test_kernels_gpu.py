@@ -106,6 +106,57 @@ def test_gemm_splitk_accumulates_large_k():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (70, 130), (64, 64), (4096, 2048), (2048, 6144),
+                                       (1000, 33)])
+def test_transpose(dtype, rows, cols):
+    """Weight transposes (exact: a permutation of the elements)."""
+    L = lib()
+    log(f"transpose rows={rows} cols={cols} {dtype}")
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype).to(DEV)
+    y = torch.full((cols, rows), float("nan"), dtype=dtype, device=DEV)
+    L.call("alodlm_transpose", L.ptr(x), L.ptr(y), rows, cols, L.dtype_code(dtype), st())
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), x.cpu().T)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,inter", [(3, 8), (37, 768), (5, 13)])
+def test_swiglu_fwd_bwd(dtype, rows, inter):
+    """SwiGLU against torch float64 ([tf] modeling_qwen3.py:81-83 with the
+    reference's roundings); the product written by the backward is
+    bit-identical to the forward's."""
+    L = lib()
+    log(f"swiglu rows={rows} inter={inter} {dtype}")
+    g = torch.Generator().manual_seed(rows + inter)
+    gu = (2 * torch.randn(rows, 2 * inter, generator=g)).to(dtype)
+    dact = torch.randn(rows, inter, generator=g).to(dtype)
+    gud, dactd = gu.to(DEV), dact.to(DEV)
+    code = L.dtype_code(dtype)
+    act = torch.empty(rows, inter, dtype=dtype, device=DEV)
+    L.call("alodlm_swiglu_fwd", L.ptr(gud), L.ptr(act), rows, inter, code, st())
+    dgu = torch.empty(rows, 2 * inter, dtype=dtype, device=DEV)
+    act2 = torch.empty(rows, inter, dtype=dtype, device=DEV)
+    L.call("alodlm_swiglu_bwd", L.ptr(dactd), L.ptr(gud), L.ptr(dgu), L.ptr(act2), rows, inter,
+           code, st())
+    dgu_noact = torch.empty(rows, 2 * inter, dtype=dtype, device=DEV)
+    L.call("alodlm_swiglu_bwd", L.ptr(dactd), L.ptr(gud), L.ptr(dgu_noact), None, rows, inter,
+           code, st())
+    torch.cuda.synchronize()
+    assert torch.equal(act2.cpu(), act.cpu())
+    assert torch.equal(dgu_noact.cpu(), dgu.cpu())
+    gate = gu[:, :inter].double().requires_grad_(True)
+    up = gu[:, inter:].double().requires_grad_(True)
+    silu = F.silu(gate)
+    ref = silu.to(dtype).double() * up if dtype != torch.float32 else silu * up
+    dg, du = torch.autograd.grad(ref, (gate, up), dact.double())
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(act.cpu().double(), ref.detach(), rtol=tol, atol=tol)
+    torch.testing.assert_close(dgu.cpu().double()[:, :inter], dg, rtol=tol, atol=tol)
+    torch.testing.assert_close(dgu.cpu().double()[:, inter:], du, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(37, 256), (64, 2048), (5, 100)])
 def test_rmsnorm_fwd_bwd(dtype, rows, cols):
     L = lib()
