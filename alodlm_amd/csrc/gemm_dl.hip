@@ -20,9 +20,18 @@
 //    lanes of a read touch 4 rows x 4 chunks = 16 distinct 4-bank groups.
 // Both give the MFMA operand "row i = lane % 32, k = 8*(lane / 32) + 0..7".
 //
-// Waves: NW = 8 (2 x 4, 128x64 each, two waves per SIMD) or NW = 4 (2 x 2,
-// 128x128 each).  v_mfma_f32_32x32x16_bf16 with the operands swapped (B rows
-// as the MFMA's A operand), so each lane owns 4 consecutive output columns.
+// Waves: 4 (2 x 2, 128x128 each, one per SIMD).  v_mfma_f32_32x32x16_bf16
+// with the operands swapped (B rows as the MFMA's A operand), so each lane
+// owns 4 consecutive output columns.  A 128x128 wave tile reads a third less
+// LDS per MFMA than a 128x64 one; with one wave per SIMD the MFMA pipe is kept
+// fed by an explicit per-k-step schedule: each of the 16 MFMAs of a k step is
+// followed by one LDS fragment read of the next k step (first 8) or by the
+// direct loads of a later stage (last 8), so no group of memory instructions
+// ever stalls the MFMA issue.
+//
+// The step is power-bound on MI355X (the chip holds its 1400 W limit by
+// lowering the clock), so the loop is shaped for energy per FLOP as much as
+// for latency: fewer LDS bytes per MFMA and no redundant instructions.
 //
 // Workgroup -> tile order: consecutive workgroups land on different XCDs, so
 // the tile sequence is dealt out in contiguous chunks per XCD, then swept in
@@ -80,6 +89,10 @@ template <int NW, int KD> struct Opnd<true, NW, KD> {
 #pragma unroll
     for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
   }
+  // instruction i (< PER) of this wave's share of a stage
+  __device__ __forceinline__ void issue_one(const char* o, char* stage, int wave, int i) const {
+    dma16(o, off[i], stage + (wave + NW * i) * 1024);
+  }
   // row `row` (0..255) of the tile, k step ks, 8 k values at 8*half
   static __device__ __forceinline__ bf16x8_t frag(const char* stage, int row, int ks, int half, int lane) {
     (void)lane;
@@ -112,6 +125,10 @@ template <int NW, int KD> struct Opnd<false, NW, KD> {
 #pragma unroll
     for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
   }
+  // instruction i (< PER) of this wave's share of a stage
+  __device__ __forceinline__ void issue_one(const char* o, char* stage, int wave, int i) const {
+    dma16(o, off[i], stage + (wave + NW * i) * 1024);
+  }
   // column `row` (0..255) of the tile, k step ks: two transposed reads of
   // k rows 16ks + 8half + {0..3} and {4..7}
   static __device__ __forceinline__ bf16x8_t frag(const char* stage, int row, int ks, int half, int lane) {
@@ -127,29 +144,17 @@ template <int NW, int KD> struct Opnd<false, NW, KD> {
 
 }  // namespace
 
-// Wait until this wave's LDS reads are back and at most N of its direct
-// loads are outstanding, then barrier; nothing is scheduled across it (so the
-// MFMAs written before it are issued before it).
-template <int N> __device__ __forceinline__ void wait_barrier() {
-  static_assert(N == 0 || N == 8 || N == 16, "add the vmcnt value");
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (N == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 template <bool AK, bool BK, int EPI, int NW, int KD, int STAGES>
-__global__ void __launch_bounds__(NW * 64, NW == 8 ? 2 : 1)
+__global__ void __launch_bounds__(NW * 64, 1)
 gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                int64_t N, int64_t K, float alpha, int64_t k_per_split, float* __restrict__ partial) {
-  constexpr int WM = 128, WN = NW == 8 ? 64 : 128;
+  static_assert(NW == 4, "the k-step schedule is written for 4 waves of 128x128");
+  constexpr int WM = 128, WN = 128;
   constexpr int FI = WM / 32, FJ = WN / 32;
   constexpr int WAVES_N = TB / WN;
   constexpr int OPB = TB * KD * 2;   // bytes of one operand's stage
   constexpr int KS = KD / 16;         // k steps per stage
-  constexpr int WAIT = (STAGES - 2) * KD / NW;  // loads of the later stages still in flight
   __shared__ __attribute__((aligned(1024))) char lds[STAGES][2][OPB];
 
   const int tiles_m = (int)((M + TB - 1) / TB), tiles_n = (int)((N + TB - 1) / TB);
@@ -194,46 +199,78 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // Fragment registers: F[0] holds k step 0 of the current tile, F[1] k step 1.
+  // Fragment registers: F[ks & 1] holds k step ks of the current tile.
   bf16x8_t fa[2][FI], fb[2][FJ];
-  auto read = [&](int set, int stage, int ks) {
-    const char* sa = lds[stage][0];
-    const char* sb = lds[stage][1];
-#pragma unroll
-    for (int i = 0; i < FI; ++i) fa[set][i] = Opnd<AK, NW, KD>::frag(sa, wm * WM + i * 32 + col, ks, half, lane);
-#pragma unroll
-    for (int j = 0; j < FJ; ++j) fb[set][j] = Opnd<BK, NW, KD>::frag(sb, wn * WN + j * 32 + col, ks, half, lane);
+  // Direct-load slots: MFMA slots 8..15 of every k step (of the k step after
+  // the barrier too when the ring has 3+ stages: its target stage was freed
+  // one barrier earlier); a stage's PL loads are spread evenly over them.
+  constexpr int PA = Opnd<AK, NW, KD>::PER, PB = Opnd<BK, NW, KD>::PER, PL = PA + PB;
+  constexpr int PRE = (KS - 1) * 8;                     // slots before the barrier
+  constexpr int SLOTS = STAGES >= 3 ? KS * 8 : PRE;
+  static_assert(PL <= SLOTS, "not enough direct-load slots");
+  constexpr int DPRE = (PL * PRE + SLOTS - 1) / SLOTS;   // loads issued before the barrier
+  // loads of this wave that may still be in flight at the barrier of tile tt
+  // (tile tt+1 must have landed): whole later stages plus this tile's early ones
+  constexpr int VM_LOOP = STAGES >= 3 ? (STAGES - 3) * PL + DPRE : 0;
+  constexpr int VM_PRO = (STAGES - 2) * PL;
+  // load d of this wave's share of tile tt
+  auto dma_one = [&](int tt, int d) {
+    const int live = tt < ntiles ? tt : ntiles - 1;
+    const int64_t k0 = kbeg + (int64_t)live * KD;
+    char* st = lds[tt % STAGES][0];
+    if (d < PA) oa.issue_one(oa.origin(A, m0, k0), st, wave, d);
+    else ob.issue_one(ob.origin(B, n0, k0), st + OPB, wave, d - PA);
   };
-  auto mma = [&](int set) {
-#pragma unroll
-    for (int i = 0; i < FI; ++i)
-#pragma unroll
-      for (int j = 0; j < FJ; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
+  // fragment q of a k step, in the order the MFMAs consume them:
+  // A0, B0, B1, B2, B3, A1, A2, A3
+  auto read_one = [&](int set, int stage, int ks, int q) {
+    const bool isa = q == 0 || q >= 5;
+    const int idx = q == 0 ? 0 : (q >= 5 ? q - 4 : q - 1);
+    if (isa) fa[set][idx] = Opnd<AK, NW, KD>::frag(lds[stage][0], wm * WM + idx * 32 + col, ks, half, lane);
+    else fb[set][idx] = Opnd<BK, NW, KD>::frag(lds[stage][1], wn * WN + idx * 32 + col, ks, half, lane);
+  };
+  auto mma_one = [&](int set, int q) {
+    const int i = q >> 2, j = q & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
   };
 
-  // Schedule per tile t (stage t % STAGES visible, F[0] = its k step 0):
-  //   issue tile t + STAGES - 1 (into the stage of tile t - 1, fully read)
-  //   k steps 0 .. KS-2: read the next step's fragments, MFMAs of this step
-  //   wait for tile t + 1 and for the last reads, barrier
-  //   read F[0] = tile t + 1, k step 0;  MFMAs of k step KS - 1
-  // so every barrier has MFMAs on each side of it.
+  // Tile tt: k steps 0 .. KS-2, then the barrier that publishes tile tt+1
+  // (this wave's loads of it are waited for first), then k step KS-1, whose
+  // reads fetch tile tt+1's k step 0.  Every instruction group is fenced with
+  // sched_barrier so the compiler keeps this order.
   if (ntiles > 0) {  // (every split of an eligible product has k tiles)
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) issue(s);
-    wait_barrier<WAIT>();
-    read(0, 0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(VM_PRO) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) read_one(0, 0, 0, q);
     for (int tt = 0; tt < ntiles; ++tt) {
       const int stage = tt % STAGES;
-      issue(tt + STAGES - 1);
+      const int nstage = (tt + 1) % STAGES;
 #pragma unroll
-      for (int ks = 0; ks < KS - 1; ++ks) {
-        read((ks + 1) & 1, stage, ks + 1);
-        mma(ks & 1);
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks == KS - 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(VM_LOOP) : "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          mma_one(ks & 1, q);
+          if (q < 8) {
+            // after the last tile these reads fetch a stage that is never used
+            if (ks + 1 < KS) read_one((ks + 1) & 1, stage, ks + 1, q);
+            else read_one(0, nstage, 0, q);
+          } else {
+            const int slot = ks * 8 + (q - 8);
+#pragma unroll
+            for (int d = 0; d < PL; ++d)
+              if ((d * SLOTS) / PL == slot) dma_one(tt + STAGES - 1, d);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-      wait_barrier<WAIT>();
-      if (tt + 1 < ntiles) read(0, (tt + 1) % STAGES, 0);
-      mma((KS - 1) & 1);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -249,7 +286,24 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
                             (ldr % 8 == 0 && reinterpret_cast<uintptr_t>(R) % 16 == 0));
     if (coalesced) {
       char* tile = lds[0][0];  // 128 KB: the whole stage ring
-      __syncthreads();         // every wave is done with the stages
+      constexpr int ITER = TB * 32 / (NW * 64);
+      const bool interior = m0 + TB <= M && n0 + TB <= N;
+      // residual rows of an interior tile are fetched before the tile is
+      // staged, so their latency overlaps the LDS writes
+      uint4 rres[EPI == ALODLM_EPI_RESIDUAL ? ITER : 1];
+      if constexpr (EPI == ALODLM_EPI_RESIDUAL) {
+        if (interior) {
+          const int64_t nr = n0 + (threadIdx.x & 31) * 8;
+#pragma unroll
+          for (int it = 0; it < ITER; ++it) {
+            const int row = it * (NW * 64 / 32) + (int)(threadIdx.x >> 5);
+            rres[it] = *reinterpret_cast<const uint4*>(R + (m0 + row) * ldr + nr);
+          }
+        }
+      }
+      // every wave is done with the stages (an LDS-only wait: the residual
+      // loads above stay in flight)
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
       for (int i = 0; i < FI; ++i) {
         const int row = wm * WM + i * 32 + col;
@@ -264,9 +318,33 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
                            (uint32_t)float_to_bf16(alpha * a[jj * 4 + 2]) | ((uint32_t)float_to_bf16(alpha * a[jj * 4 + 3]) << 16));
           }
       }
-      __syncthreads();
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       const int chunk = threadIdx.x & 31;
       const int64_t n = n0 + chunk * 8;
+      if (interior) {
+#pragma unroll
+        for (int it = 0; it < ITER; ++it) {
+          const int row = it * (NW * 64 / 32) + (int)(threadIdx.x >> 5);
+          const uint4 w = *reinterpret_cast<const uint4*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4));
+          bf16_t* dst = Cb + (m0 + row) * ldc + n;
+          if constexpr (EPI == ALODLM_EPI_RESIDUAL) {
+            // reference order: x + round_bf16(proj), rounded once more
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+            const uint32_t rv[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
+            uint32_t ov[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo = bf16_to_float((bf16_t)(rv[e] & 0xffff)) + bf16_to_float((bf16_t)(wv[e] & 0xffff));
+              const float hi = bf16_to_float((bf16_t)(rv[e] >> 16)) + bf16_to_float((bf16_t)(wv[e] >> 16));
+              ov[e] = (uint32_t)float_to_bf16(lo) | ((uint32_t)float_to_bf16(hi) << 16);
+            }
+            *reinterpret_cast<uint4*>(dst) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+          } else {
+            *reinterpret_cast<uint4*>(dst) = w;
+          }
+        }
+        return;
+      }
 #pragma unroll 4
       for (int it = 0; it < TB * 32 / (NW * 64); ++it) {
         const int row = it * (NW * 64 / 32) + (int)(threadIdx.x >> 5);
@@ -404,28 +482,14 @@ static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
 }
 
-// Stage shape per operand layout: 32 k x 4 stages, or 64 k x 2 stages
-// (whole 128-byte rows per direct load for k-contiguous operands).
-#ifndef GEMM_DL_KK_DEEP
-#define GEMM_DL_KK_DEEP 0
-#endif
-#ifndef GEMM_DL_KMN_DEEP
-#define GEMM_DL_KMN_DEEP 0
-#endif
-
 template <bool AK, bool BK>
-static void launch_layout(bool deep, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb,
-                          void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
+static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
+                          int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
                           int64_t nsplit, hipStream_t st) {
-#ifdef GEMM_DL_KK_CFG
-  if (AK && BK) {
-    if (GEMM_DL_KK_CFG == 2) { launch_dl<AK, BK, 4, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st); return; }
-    if (GEMM_DL_KK_CFG == 3 && deep) { launch_dl<AK, BK, 4, 64, 2>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st); return; }
-  }
-#endif
-  if (deep) launch_dl<AK, BK, 8, 64, 2>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
-  else launch_dl<AK, BK, 8, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps, nsplit, st);
+  // 4 waves, 32-deep k stages in a ring of 4 (128 KB of LDS)
+  launch_dl<AK, BK, 4, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
+                              nsplit, st);
 }
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
@@ -439,12 +503,8 @@ void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B,
   const int64_t nsplit = (K + kps - 1) / kps;
   *nsplit_out = nsplit;
   float* p = (epi == ALODLM_EPI_ACCUM && nsplit > 1) ? part : nullptr;
-  // 64-deep stages need every split to hold whole 64-k tiles
-  const bool k64 = kps % 64 == 0;
-  const bool both = a_kmajor && b_kmajor;
-  const bool deep = k64 && (both ? GEMM_DL_KK_DEEP : GEMM_DL_KMN_DEEP);
-  if (both) launch_layout<true, true>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (a_kmajor) launch_layout<true, false>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (b_kmajor) launch_layout<false, true>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else launch_layout<false, false>(deep, A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  else launch_layout<false, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
 }
