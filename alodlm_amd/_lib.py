@@ -58,7 +58,7 @@ SIGNATURES = {
     "alodlm_gate_bwd": [P, P, F32, P, P, P, I64, I64, I64, P, I32, P],
     "alodlm_grad_norm": [P, P, P, P, I64, I64, I32, P, P, P],
     "alodlm_adamw": [P, P, P, P, P, P, P, P, P, I64, I64, P, F32, F32, F32, F32, F32, I64, I32, P],
-    "alodlm_cast_f32": [P, P, I64, I32, P],
+    "alodlm_cast_f32": [P, P, P, I64, I32, P],
     "alodlm_scale_f32": [P, P, I64, P],
     "alodlm_transpose": [P, P, I64, I64, I32, P],
 }

@@ -81,6 +81,26 @@ def _draw_stream(device):
     return stream
 
 
+def block_supervised_counts(labels_host, offsets, block_size):
+    """Per segment, the number of supervised labels (!= -100) of every block
+    (the candidate count n of alodlm/batch.py:50-55)."""
+    out = []
+    for a, b in zip(offsets, offsets[1:]):
+        valid = (labels_host[a:b] != -100).astype(np.int64)
+        out.append(np.add.reduceat(valid, np.arange(0, b - a, block_size)))
+    return out
+
+
+def full_block_counts(offsets, block_size):
+    """Per segment, the block widths: the candidate counts when every label
+    is supervised."""
+    out = []
+    for a, b in zip(offsets, offsets[1:]):
+        starts = np.arange(0, b - a, block_size)
+        out.append(np.minimum(block_size, (b - a) - starts).astype(np.int64))
+    return out
+
+
 def draw_masking(labels_host, offsets, block_size, device, generator=None):
     """Draw the masking randomness in the reference's order.
 
@@ -90,24 +110,22 @@ def draw_masking(labels_host, offsets, block_size, device, generator=None):
     caller orders its own stream after that one before reading them.
     """
     device = torch.device(device)
+    counts = block_supervised_counts(labels_host, offsets, block_size)
     if device.type == "cuda":
         with torch.cuda.stream(_draw_stream(device)):
-            return _draw(labels_host, offsets, block_size, device, generator)
-    return _draw(labels_host, offsets, block_size, device, generator)
+            return _draw(counts, offsets, block_size, device, generator)
+    return _draw(counts, offsets, block_size, device, generator)
 
 
-def _draw(labels_host, offsets, block_size, device, generator):
+def _draw(block_counts, offsets, block_size, device, generator):
+    """The draws of alodlm/batch.py:50-60 for given candidate counts n."""
     probs, counts, perms = [], [], []
-    for a, b in zip(offsets, offsets[1:]):
-        length = b - a
-        nblocks = (length + block_size - 1) // block_size
+    for (a, b), n in zip(zip(offsets, offsets[1:]), block_counts):
+        nblocks = (b - a + block_size - 1) // block_size
         u = torch.empty(nblocks, device=device).uniform_(0, 1, generator=generator).clamp_min(1e-8)
-        # p as the reference reads it (a float32 value widened to float64), the
-        # supervised count n of every block, and round(n * p) rounded half to
-        # even in float64 like Python's round (alodlm/batch.py:50-57)
+        # p as the reference reads it (a float32 value widened to float64) and
+        # round(n * p) rounded half to even in float64 like Python's round
         p = u.cpu().numpy().astype(np.float64)
-        valid = (labels_host[a:b] != -100).astype(np.int64)
-        n = np.add.reduceat(valid, np.arange(0, length, block_size))
         count = np.rint(n * p).astype(np.int64)
         probs.extend(p.tolist())
         counts.extend(count.tolist())
@@ -115,6 +133,13 @@ def _draw(labels_host, offsets, block_size, device, generator):
             perms.append(torch.randperm(int(n[blk]), device=device, generator=generator)
                          if count[blk] else None)
     return np.asarray(probs, dtype=np.float32), np.asarray(counts, dtype=np.int32), perms
+
+
+def _generator_of(device, generator):
+    if generator is not None:
+        return generator
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch.cuda.default_generators[index]
 
 
 @torch.no_grad()
@@ -138,16 +163,35 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     device = ids.device
     if device.type != "cuda":
         raise ValueError("build_batch runs on the GPU; move ids/labels to a CUDA device")
-    labels_host = labels.detach().cpu().numpy()
     nseg = len(offsets) - 1
     seg_block = [0]
     for a, b in zip(offsets, offsets[1:]):
         seg_block.append(seg_block[-1] + (b - a + block_size - 1) // block_size)
     nblocks = seg_block[-1]
     side = _draw_stream(device)
+    speculative = None
+    if draws is None:
+        # The draws depend on the labels only through the supervised count of
+        # every block.  Draw first assuming every label is supervised: this
+        # needs no labels on the host, so it overlaps the work still queued
+        # on the compute stream.  If the labels then show an unsupervised
+        # position, the generator is rewound and the draws are made again
+        # with the true counts; either way the consumed random numbers are
+        # exactly the reference's.
+        gen = _generator_of(device, generator)
+        state = gen.get_state()
+        assumed = full_block_counts(offsets, block_size)
+        with torch.cuda.stream(side):
+            speculative = _draw(assumed, offsets, block_size, device, generator)
+    labels_host = labels.detach().cpu().numpy()
     with torch.cuda.stream(side):
         if draws is None:
-            draws = _draw(labels_host, offsets, block_size, device, generator)
+            actual = block_supervised_counts(labels_host, offsets, block_size)
+            if all(np.array_equal(x, y) for x, y in zip(actual, assumed)):
+                draws = speculative
+            else:
+                gen.set_state(state)
+                draws = _draw(actual, offsets, block_size, device, generator)
         probs, counts, perms = draws
         perm_offset = np.zeros(nblocks, dtype=np.int64)
         chunks, total = [], 0

@@ -117,10 +117,12 @@ transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, i
   }
 }
 
+// dst = cast(src * scale[0]) (scale may be null: no scaling)
 template <typename T>
-__global__ void cast_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
+__global__ void cast_kernel(const float* __restrict__ src, const float* __restrict__ scale,
+                            T* __restrict__ dst, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) Elem<T>::store(dst, i, src[i]);
+  if (i < n) Elem<T>::store(dst, i, scale ? src[i] * scale[0] : src[i]);
 }
 
 __global__ void scale_kernel(float* __restrict__ x, const float* __restrict__ s, int64_t n) {
@@ -199,10 +201,11 @@ extern "C" int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_
   return ALODLM_OK;
 }
 
-extern "C" int alodlm_cast_f32(const float* src, void* dst, int64_t n, int dtype, void* stream) {
+extern "C" int alodlm_cast_f32(const float* src, const float* scale, void* dst, int64_t n,
+                               int dtype, void* stream) {
   if (n == 0) return ALODLM_OK;
   ALODLM_DISPATCH(dtype, T, {
-    cast_kernel<T><<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(src, (T*)dst, n);
+    cast_kernel<T><<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(src, scale, (T*)dst, n);
   });
   ALODLM_CHECK_LAUNCH("cast_f32");
   return ALODLM_OK;

@@ -17,6 +17,7 @@ from pathlib import Path
 import torch
 import torch.nn as nn
 
+from . import _lib
 from .config import ModelConfig, local_dir
 from .engine import METRIC_NAMES, StepEngine
 
@@ -61,16 +62,20 @@ class _Step(torch.autograd.Function):
         engine, state = ctx.engine, ctx.state
         if state is None:
             raise RuntimeError("the step was run without gradient tracking")
-        scale = float(grad_loss)
-        grads = engine.backward(state, scale)
+        # The backward is linear in the loss's upstream gradient: it runs for a
+        # unit seed and the seed (a device scalar, never read on the host, so
+        # the host does not wait for the forward here) scales the result.
+        seed = grad_loss.detach().to(device=engine.device, dtype=torch.float32).reshape(1)
+        grads = engine.backward(state, 1.0)
         ctx.state = None
+        stream = _lib.stream_handle(engine.device)
         if engine.dtype == torch.float32:
             flat = grads
+            _lib.call("alodlm_scale_f32", _lib.ptr(flat), _lib.ptr(seed), flat.numel(), stream)
         else:
             flat = torch.empty(engine.arena.total, dtype=engine.dtype, device=engine.device)
-            from . import _lib
-            _lib.call("alodlm_cast_f32", _lib.ptr(grads), _lib.ptr(flat), grads.numel(),
-                      engine.code, _lib.stream_handle(engine.device))
+            _lib.call("alodlm_cast_f32", _lib.ptr(grads), _lib.ptr(seed), _lib.ptr(flat),
+                      grads.numel(), engine.code, stream)
         views = [engine.arena.view(flat, name) for name in engine.arena.names]
         return (None, None, None, *views)
 

@@ -34,7 +34,10 @@ class _Table:
 
     @staticmethod
     def pointers(tensors, device):
-        return torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=device)
+        # staged through pinned memory and copied without blocking, so a step
+        # never waits for the backward still queued on the stream
+        host = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64).pin_memory()
+        return host.to(device, non_blocking=True)
 
 
 class FusedAdamW(torch.optim.Optimizer):

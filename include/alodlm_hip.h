@@ -289,7 +289,12 @@ int alodlm_adamw(void* const* params, float* const* master, float* const* exp_av
                  float eps, int64_t step, int dtype, void* stream);
 
 /* Elementwise helpers. */
-int alodlm_cast_f32(const float* src, void* dst, int64_t n, int dtype, void* stream);
+/* dst = cast(src * scale[0]); scale is a device scalar or null (no scaling).
+ * Casts the float32 gradient arena to the parameter dtype for autograd,
+ * applying the upstream gradient of the loss (torch's loss.backward() seed,
+ * alodlm/train.py:136) without reading it on the host. */
+int alodlm_cast_f32(const float* src, const float* scale, void* dst, int64_t n, int dtype,
+                    void* stream);
 int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream);
 /* dst[c][r] = src[r][c] for a row-major rows x cols matrix (dst and src must
  * not overlap).  The step keeps transposed copies of the projection and

@@ -335,3 +335,4 @@ def test_cosine_schedule_closed_form():
     assert O.cosine_lr_multiplier(2, 4, 100) == 0.5
     assert abs(O.cosine_lr_multiplier(52, 4, 100) - 0.5) < 1e-12
     assert O.cosine_lr_multiplier(100, 4, 100) == 0.0
+

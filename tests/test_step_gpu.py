@@ -103,6 +103,15 @@ def test_micro_step_autograd_path_fills_grads():
     for name, p in model.named_parameters():
         ref = torch.as_tensor(g["grad_" + name])
         torch.testing.assert_close(p.grad.cpu(), ref, rtol=1e-4, atol=1e-6, msg=name)
+    # a non-unit upstream gradient scales every parameter gradient
+    model.zero_grad(set_to_none=True)
+    loss, _ = model(torch.as_tensor(g["in_ids"]).cuda(), labels.cuda(),
+                    torch.as_tensor(g["in_boundaries"]),
+                    exit_uniforms=[u.cuda() for u in uniforms], draws=draws)
+    (loss * -2.5).backward()
+    for name, p in model.named_parameters():
+        ref = -2.5 * torch.as_tensor(g["grad_" + name])
+        torch.testing.assert_close(p.grad.cpu(), ref, rtol=1e-4, atol=3e-6, msg=name)
 
 
 def _tiny_inputs(seed=0):
