@@ -114,6 +114,9 @@ int alodlm_set_error(int code, const char* fmt, ...);
 
 static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Number of blocks of b threads covering a items.  A dispatch holds fewer
+// than 2^32 work-items in each dimension, so every caller's a is bounded by
+// the activation shapes (or the kernel is a grid-stride sweep).
 static inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ----------------------------------------------------------------------------

@@ -117,17 +117,29 @@ transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, i
   }
 }
 
-// dst = cast(src * scale[0]) (scale may be null: no scaling)
+// dst = cast(src * scale[0]) (scale may be null: no scaling).  Grid-stride:
+// these two kernels sweep the whole gradient arena (8.2 G elements at 8B), and
+// one dispatch covers fewer than 2^32 work-items.
 template <typename T>
 __global__ void cast_kernel(const float* __restrict__ src, const float* __restrict__ scale,
                             T* __restrict__ dst, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) Elem<T>::store(dst, i, scale ? src[i] * scale[0] : src[i]);
+  const float k = scale ? scale[0] : 1.0f;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    Elem<T>::store(dst, i, scale ? src[i] * k : src[i]);
 }
 
 __global__ void scale_kernel(float* __restrict__ x, const float* __restrict__ s, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) x[i] *= s[0];
+  const float k = s[0];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] *= k;
+}
+
+// Blocks of 256 for a grid-stride sweep over n elements (at most 8 per CU slot
+// of a 256-CU part, so the grid stays far below the 2^32 work-item limit).
+static unsigned sweep_blocks(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return (unsigned)(b < 16384 ? b : 16384);
 }
 
 extern "C" int alodlm_embed_gather(const void* table, const int64_t* ids, void* out, int64_t rows,
@@ -205,7 +217,7 @@ extern "C" int alodlm_cast_f32(const float* src, const float* scale, void* dst, 
                                int dtype, void* stream) {
   if (n == 0) return ALODLM_OK;
   ALODLM_DISPATCH(dtype, T, {
-    cast_kernel<T><<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(src, scale, (T*)dst, n);
+    cast_kernel<T><<<sweep_blocks(n), 256, 0, as_stream(stream)>>>(src, scale, (T*)dst, n);
   });
   ALODLM_CHECK_LAUNCH("cast_f32");
   return ALODLM_OK;
@@ -213,7 +225,7 @@ extern "C" int alodlm_cast_f32(const float* src, const float* scale, void* dst, 
 
 extern "C" int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream) {
   if (n == 0) return ALODLM_OK;
-  scale_kernel<<<ceil_div_u(n, 256), 256, 0, as_stream(stream)>>>(x, scale, n);
+  scale_kernel<<<sweep_blocks(n), 256, 0, as_stream(stream)>>>(x, scale, n);
   ALODLM_CHECK_LAUNCH("scale_f32");
   return ALODLM_OK;
 }

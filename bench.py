@@ -1,8 +1,13 @@
-"""Benchmark: ALoDLM-1.7B full training step on one MI355X.
+"""Benchmark: ALoDLM full training step on one MI355X.
 
-One step = ALoDLM.forward on one pack of 8 x 2048 synthetic tokens (dual-stream
-N = 32768 rows, recurrent core = layers 0-28 run K = 4 times) + backward +
+One step = ALoDLM.forward on one pack of synthetic tokens + backward +
 global-norm clip + AdamW with float32 masters, all on the HIP kernels.
+
+  --model 1.7b (default)  Qwen3-1.7B shapes, recurrent core = layers 0-28 run
+                          K = 4 times, one pack of 8 x 2048 tokens (dual-stream
+                          N = 32768 rows)
+  --model 8b              Qwen3-8B shapes, prelude 0-10 / core 10-26 / coda
+                          26-36, K = 4, one sequence of 2048 tokens (N = 4096)
 
 Prints one JSON line (metric of BASELINE: train tokens/s) with:
   roofline      the dominant kernel class (by time in the timed region, from
@@ -28,26 +33,41 @@ import torch
 PEAK_BF16 = 2516.6e12   # dense bf16 MFMA FLOP/s of MI355X (256 CU x 4096 FLOP/clk x 2.4 GHz)
 PEAK_HBM = 8.0e12
 ROOT = os.path.dirname(os.path.abspath(__file__))
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_bf16_1p7b_step_traffic.md")
 
 
-def qwen3_1p7b_config():
+MODELS = {
+    # Qwen3-1.7B; the repository's 1.7B topology runs every layer as the core
+    "1.7b": dict(hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
+                 num_attention_heads=16, num_key_value_heads=8, loop=(0, 28),
+                 segments=[2048] * 8, name="ALoDLM-1.7B", qwen="Qwen3-1.7B",
+                 traffic="gemm_bf16_1p7b_step_traffic.md"),
+    # Qwen3-8B; prelude [0, 10), core [10, 26), coda [26, 36)
+    "8b": dict(hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+               num_attention_heads=32, num_key_value_heads=8, loop=(10, 26),
+               segments=[2048], name="ALoDLM-8B", qwen="Qwen3-8B",
+               traffic="gemm_bf16_8b_step_traffic.md"),
+}
+
+
+def qwen3_config(spec):
     from transformers import Qwen3Config
-    return Qwen3Config(hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
-                       num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+    return Qwen3Config(hidden_size=spec["hidden_size"], intermediate_size=spec["intermediate_size"],
+                       num_hidden_layers=spec["num_hidden_layers"],
+                       num_attention_heads=spec["num_attention_heads"],
+                       num_key_value_heads=spec["num_key_value_heads"], head_dim=128,
                        vocab_size=151936, max_position_embeddings=40960, rms_norm_eps=1e-6,
                        rope_parameters={"rope_type": "default", "rope_theta": 1e6},
                        tie_word_embeddings=False, bos_token_id=151643, eos_token_id=151645)
 
 
-def build_model(device, dtype, seed=0):
-    """Random-init Qwen3-1.7B backbone (N(0, 0.02), unit norms) + a fresh gate,
-    topology loop 0-28 (the repo's 1.7B configuration)."""
+def build_model(spec, device, dtype, seed=0):
+    """Random-init Qwen3 backbone (N(0, 0.02), unit norms) + a fresh gate with
+    the configuration's loop topology."""
     from transformers import Qwen3ForCausalLM
     from alodlm_amd.config import ModelConfig
     from alodlm_amd.model import ALoDLM
     with torch.device("meta"):
-        backbone = Qwen3ForCausalLM(qwen3_1p7b_config())
+        backbone = Qwen3ForCausalLM(qwen3_config(spec))
     backbone = backbone.to_empty(device=device).to(dtype)
     g = torch.Generator(device=device).manual_seed(seed)
     with torch.no_grad():
@@ -56,7 +76,8 @@ def build_model(device, dtype, seed=0):
                 p.fill_(1.0)
             else:
                 p.normal_(0.0, 0.02, generator=g)
-    cfg = ModelConfig(loop_start=0, loop_end=28, max_depth=4, mask_token_id=151665,
+    start, end = spec["loop"]
+    cfg = ModelConfig(loop_start=start, loop_end=end, max_depth=4, mask_token_id=151665,
                       block_size=32)
     return ALoDLM(backbone, cfg)
 
@@ -134,24 +155,27 @@ def profiled_traffic(path):
     return None
 
 
-def cpu_baseline(cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
+def cpu_baseline(spec, cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     """Time the CPU oracle (float32, torch eager on this host) on a bounded
-    sample: `layer_reps` decoder-layer fwd+bwd passes over one dual-stream
-    segment and one LM-head readout fwd+bwd over `readout_rows` rows.  Returns
-    (seconds per layer pass, seconds per readout row, threads)."""
+    sample: `layer_reps` decoder-layer fwd+bwd passes of the model's layer
+    shape over one dual-stream segment and one LM-head readout fwd+bwd over
+    `readout_rows` rows.  Returns (seconds per layer pass, seconds per readout
+    row, threads)."""
     from oracle import step as O
     threads = threads or torch.get_num_threads()  # honours OMP_NUM_THREADS
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    d = O.Dims(hidden=2048, heads=16, kv_heads=8, head_dim=128, intermediate=6144,
+    H, I = spec["hidden_size"], spec["intermediate_size"]
+    nq, nkv = spec["num_attention_heads"], spec["num_key_value_heads"]
+    d = O.Dims(hidden=H, heads=nq, kv_heads=nkv, head_dim=128, intermediate=I,
                vocab=151936, layers=1, eps=1e-6, theta=1e6)
     pre = "model.layers.0."
-    shapes = {"self_attn.q_proj.weight": (2048, 2048), "self_attn.k_proj.weight": (1024, 2048),
-              "self_attn.v_proj.weight": (1024, 2048), "self_attn.o_proj.weight": (2048, 2048),
-              "mlp.gate_proj.weight": (6144, 2048), "mlp.up_proj.weight": (6144, 2048),
-              "mlp.down_proj.weight": (2048, 6144)}
+    shapes = {"self_attn.q_proj.weight": (nq * 128, H), "self_attn.k_proj.weight": (nkv * 128, H),
+              "self_attn.v_proj.weight": (nkv * 128, H), "self_attn.o_proj.weight": (H, nq * 128),
+              "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H),
+              "mlp.down_proj.weight": (H, I)}
     p = {pre + k: (torch.randn(*s, generator=g) * 0.02).requires_grad_(True) for k, s in shapes.items()}
-    for k, n in (("input_layernorm.weight", 2048), ("post_attention_layernorm.weight", 2048),
+    for k, n in (("input_layernorm.weight", H), ("post_attention_layernorm.weight", H),
                  ("self_attn.q_norm.weight", 128), ("self_attn.k_norm.weight", 128)):
         p[pre + k] = torch.ones(n).requires_grad_(True)
     L = cfg_seg
@@ -159,15 +183,15 @@ def cpu_baseline(cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     pos = torch.cat((torch.arange(L), torch.arange(L)))
     cos, sin = O.rope_tables(pos, 128, 1e6)
     allowed = torch.as_tensor(O.attention_mask(L, 32))
-    x = torch.randn(rows, 2048, generator=g).requires_grad_(True)
-    dy = torch.randn(rows, 2048, generator=g)
+    x = torch.randn(rows, H, generator=g).requires_grad_(True)
+    dy = torch.randn(rows, H, generator=g)
     t0 = time.perf_counter()
     for _ in range(layer_reps):
         y = O.layer_forward(p, pre, x, cos, sin, allowed, d)
         y.backward(dy)
     t_layer = (time.perf_counter() - t0) / layer_reps
-    W = (torch.randn(151936, 2048, generator=g) * 0.02).requires_grad_(True)
-    X = torch.randn(readout_rows, 2048, generator=g).requires_grad_(True)
+    W = (torch.randn(151936, H, generator=g) * 0.02).requires_grad_(True)
+    X = torch.randn(readout_rows, H, generator=g).requires_grad_(True)
     tgt = torch.randint(0, 151936, (readout_rows,), generator=g)
     t0 = time.perf_counter()
     loss = torch.nn.functional.cross_entropy(X @ W.T, tgt)
@@ -179,6 +203,7 @@ def cpu_baseline(cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--model", choices=sorted(MODELS), default="1.7b")
     parser.add_argument("--steps", type=int, default=5)
     # two warmup steps: the first optimizer step allocates the float32 masters
     # and moments, and the step after it is the first to run under the final
@@ -207,11 +232,12 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     dtype = torch.bfloat16
-    model = build_model(device, dtype)
+    spec = MODELS[args.model]
+    model = build_model(spec, device, dtype)
     engine = model.engine()
     timer = None
     gen = torch.Generator().manual_seed(0)
-    seg_lengths = [2048] * 8
+    seg_lengths = spec["segments"]
     ids = torch.randint(0, 151936, (sum(seg_lengths),), generator=gen).to(device)
     labels = ids.clone()
     bounds = torch.tensor([0] + [sum(seg_lengths[:i + 1]) for i in range(len(seg_lengths))])
@@ -248,13 +274,15 @@ def main():
                                         [sum(r) / len(rows) for r in zip(*rows)])
     step_f = gemm_f + attn_f + head_f
     line = {
-        "metric": "train tokens/s, ALoDLM-1.7B seq2048 on 1 MI355X",
+        "metric": "train tokens/s, ALoDLM-1.7B & 8B seq2048 on 1 MI355X; % bf16 MFMA peak",
         "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 2), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "ALoDLM-1.7B full training step (fwd+bwd+clip+AdamW fp32 master)",
-                   "model": "Qwen3-1.7B random init, untied, loop 0-28, max_depth 4",
-                   "global_batch": 8, "seq_len": 2048, "dual_stream_rows": 2 * tokens,
+        "config": {"workload": f"{spec['name']} full training step (fwd+bwd+clip+AdamW fp32 master)",
+                   "model": (f"{spec['qwen']} random init, untied, loop {spec['loop'][0]}-"
+                             f"{spec['loop'][1]}, max_depth 4"),
+                   "global_batch": len(seg_lengths), "seq_len": 2048,
+                   "dual_stream_rows": 2 * tokens,
                    "parallelism": "none (1 GPU)"},
         "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
         "step_tflop": round(step_f / 1e12, 1),
@@ -272,9 +300,10 @@ def main():
                             "frac": round(achieved / PEAK_BF16, 4),
                             "traffic": None}
         if dom == "gemm_bf16":
+            traffic_profile = os.path.join(ROOT, "profiles", spec["traffic"])
             line["roofline"]["algorithmic_bytes_per_launch"] = timer.gemm_bytes // s["launches"]
-            line["roofline"]["traffic"] = profiled_traffic(TRAFFIC_PROFILE)
-            line["roofline"]["traffic_source"] = os.path.relpath(TRAFFIC_PROFILE, ROOT)
+            line["roofline"]["traffic"] = profiled_traffic(traffic_profile)
+            line["roofline"]["traffic_source"] = os.path.relpath(traffic_profile, ROOT)
         line["kernel_classes"] = {k: {"ms_per_step": round(v["ms"] / args.steps, 1),
                                       "tflops": round(v["flops"] / (v["ms"] / 1000) / 1e12, 1)}
                                   for k, v in summary.items()}
@@ -283,7 +312,7 @@ def main():
         model_apps = cfg.loop_start + cfg.max_depth * (engine.dims.layers - cfg.loop_start)
         del opt, model, engine
         torch.cuda.empty_cache()
-        t_layer, t_row, threads = cpu_baseline()
+        t_layer, t_row, threads = cpu_baseline(spec)
         apps = model_apps
         readout_rows = sum(sum(r) for r in rows) / len(rows)
         t_step = apps * len(seg_lengths) * t_layer + readout_rows * t_row
@@ -291,8 +320,8 @@ def main():
             "value": round(tokens / t_step, 4), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": (f"oracle fp32 eager: 3 decoder-layer fwd+bwd passes on one "
-                       f"4096x2048 dual-stream segment ({t_layer:.2f}s each) + LM head/CE "
-                       f"fwd+bwd on 2048 rows x 151936 ({1000 * t_row:.2f} ms/row); "
+                       f"4096x{spec['hidden_size']} dual-stream segment ({t_layer:.2f}s each) "
+                       f"+ LM head/CE fwd+bwd on 2048 rows x 151936 ({1000 * t_row:.2f} ms/row); "
                        f"step = {apps} layer applications x {len(seg_lengths)} segments "
                        f"+ {readout_rows:.0f} readout rows"),
         }

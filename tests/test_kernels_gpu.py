@@ -388,3 +388,23 @@ def test_objective_kernel_matches_oracle(K, depths):
     assert abs(out[8] - ar.item()) < 1e-6
     torch.testing.assert_close(dgate.cpu().double()[:, mrows], dg, rtol=1e-5, atol=1e-7)
     assert (dgate.cpu()[:, [0, 1, 4, 5, 7]] == 0).all()
+
+
+def test_cast_covers_more_than_2_32_elements():
+    """The float32 -> bf16 gradient cast sweeps arenas beyond 2^32 elements (the
+    8B arena holds 8.2 G); a one-thread-per-element dispatch would cover only
+    n mod 2^32 of them."""
+    L = lib()
+    n = (1 << 32) + 4096 * 3
+    log(f"cast n={n}")
+    src = torch.full((n,), 1.5, dtype=torch.float32, device=DEV)
+    src[-8192:] = 2.5
+    dst = torch.zeros(n, dtype=torch.bfloat16, device=DEV)
+    seed = torch.tensor([2.0], dtype=torch.float32, device=DEV)
+    L.call("alodlm_cast_f32", L.ptr(src), L.ptr(seed), L.ptr(dst), n, 1, st())
+    torch.cuda.synchronize()
+    assert float(dst[0]) == 3.0
+    assert torch.equal(dst[(1 << 32) - 8:(1 << 32) + 8].float().cpu(), torch.full((16,), 3.0))
+    assert torch.equal(dst[-8192:].float().cpu(), torch.full((8192,), 5.0))
+    del src, dst
+    torch.cuda.empty_cache()
