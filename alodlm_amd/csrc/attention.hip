@@ -252,7 +252,7 @@ int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
                      float* lse, int64_t N, int nq, int nkv, int B, float scale, hipStream_t st);
 int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
-                     const float* lse, const float* delta, const bf16_t* dout,
+                     const float* lse, const bf16_t* o, float* delta, const bf16_t* dout,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
                      bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
                      float scale, hipStream_t st);
@@ -296,7 +296,14 @@ extern "C" int alodlm_attention_fwd(const void* q, const void* k, const void* v,
   return ALODLM_OK;
 }
 
-extern "C" int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq) { return rows * nq; }
+int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles);
+
+extern "C" int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv,
+                                                  int64_t dh, int64_t n_tiles) {
+  // delta [nq][rows]; the head_dim-128 kernels may also keep dK/dV partials
+  if (dh == 128 && nq > 0 && nkv > 0) return fa128_bwd_workspace(rows, (int)nq, (int)nkv, n_tiles);
+  return rows * nq;
+}
 
 extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
                                     const void* o, const float* lse, const void* dout,
@@ -311,19 +318,24 @@ extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v,
   const float scale = 1.0f / sqrtf((float)dh);
   hipStream_t st = as_stream(stream);
   float* delta = workspace;
+  const bool mfma = use_mfma(dtype, dh, tiles, ldv, {q, k, v, o, dout, dq, dk, dv}) && lddv % 8 == 0;
+  if (mfma && dh == 128) {
+    // the head_dim-128 dQ kernel computes delta itself
+    if (n_tiles == 0) return ALODLM_OK;
+    ALODLM_CHECK_ARG(n_tiles <= 65535, "attention: too many 128-row tiles (%lld)", (long long)n_tiles);
+    return fa128_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse,
+                            (const bf16_t*)o, delta, (const bf16_t*)dout, bounds, tiles, n_tiles,
+                            (bf16_t*)dq, (bf16_t*)dk, (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv,
+                            (int)block_size, scale, st);
+  }
   ALODLM_DISPATCH(dtype, T, {
     attn_delta_kernel<T><<<ceil_div_u(rows * nq, 4), 256, 0, st>>>((const T*)o, (const T*)dout,
                                                                    delta, rows, nq, dh);
   });
   ALODLM_CHECK_LAUNCH("attention_delta");
-  if (use_mfma(dtype, dh, tiles, ldv, {q, k, v, o, dout, dq, dk, dv}) && lddv % 8 == 0) {
+  if (mfma) {  // head_dim 64
     if (n_tiles == 0) return ALODLM_OK;
     ALODLM_CHECK_ARG(n_tiles <= 65535, "attention: too many 128-row tiles (%lld)", (long long)n_tiles);
-    if (dh == 128)
-      return fa128_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse,
-                              delta, (const bf16_t*)dout, bounds, tiles, n_tiles, (bf16_t*)dq,
-                              (bf16_t*)dk, (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv,
-                              (int)block_size, scale, st);
     return fa_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse, delta,
                          (const bf16_t*)dout, bounds, tiles, n_tiles, (bf16_t*)dq, (bf16_t*)dk,
                          (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv, (int)dh, (int)block_size,

@@ -235,14 +235,17 @@ fa128_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 }
 
 // ---------------------------------------------------------------------------
-// dQ = scale * dS K,  dS = P * (dP - delta),  dP = dO V^T
+// dQ = scale * dS K,  dS = P * (dP - delta),  dP = dO V^T, with
+// delta[h, r] = sum_e dO[r, h, e] * O[r, h, e] computed here from the dO
+// fragments each lane already holds and written out for the dK/dV pass.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256, 2)
 fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                 const bf16_t* __restrict__ v, int64_t ldv, const float* __restrict__ lse,
-                const float* __restrict__ delta, const bf16_t* __restrict__ dout,
-                const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
-                bf16_t* __restrict__ dq, int64_t N, int nq, int nkv, int B, float scale) {
+                const bf16_t* __restrict__ o, float* __restrict__ delta,
+                const bf16_t* __restrict__ dout, const int64_t* __restrict__ bounds,
+                const int32_t* __restrict__ tiles, bf16_t* __restrict__ dq, int64_t N, int nq,
+                int nkv, int B, float scale) {
   __shared__ __attribute__((aligned(1024))) char lds[2][2][KT * ROWB];  // [stage][K | V]
   const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -265,7 +268,19 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     }
   }
   const float lse2 = T.valid ? lse[(int64_t)h * N + base + T.qi] * FA_LOG2E : 0.f;
-  const float delta_q = T.valid ? delta[(int64_t)h * N + base + T.qi] : 0.f;
+  // delta of this lane's query: its 64 head_dim values, then the other half's
+  float delta_q = 0.f;
+  if (T.valid) {
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+      const bf16x8_t of = load_frag(o + (base + T.qi) * ldq + h * HD + kk * 16 + half * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        delta_q += bf16_to_float((bf16_t)df[kk][e]) * bf16_to_float((bf16_t)of[e]);
+    }
+  }
+  delta_q += __shfl_xor(delta_q, 32, 64);
+  if (T.valid && half == 0) delta[(int64_t)h * N + base + T.qi] = delta_q;
   f32x16_t acc[HD / 32];
 #pragma unroll
   for (int i = 0; i < HD / 32; ++i) acc[i] = zero16();
@@ -352,13 +367,19 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                   const float* __restrict__ delta, const bf16_t* __restrict__ dout,
                   const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
                   int n_tiles, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv,
-                  int64_t N, int nq, int nkv, int B, float scale) {
+                  float* __restrict__ partial, int64_t N, int nq, int nkv, int B, float scale) {
   __shared__ __attribute__((aligned(1024))) char lds[2][2][QT * ROWB];  // [stage][Q | dO]
   __shared__ __attribute__((aligned(1024))) char lds_v[128 * ROWB];     // V of the key tile
   __shared__ __attribute__((aligned(16))) float lds_ld[2][2 * QT];      // [stage][lse | delta]
   const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hk = blockIdx.x, group = nq / nkv;
+  // One workgroup per (kv head, key tile) walking the group's query heads, or,
+  // with `partial`, one per (query head, key tile) writing float32 partials
+  // that fa128_dkdv_reduce_kernel sums over the group.
+  const int group = nq / nkv;
+  const int hk = partial ? (int)blockIdx.x / group : (int)blockIdx.x;
+  const int h_first = partial ? (int)blockIdx.x : hk * group;
+  const int h_end = partial ? h_first + 1 : (hk + 1) * group;
   const int t = n_tiles - 1 - (int)blockIdx.y;
   const int seg = tiles[2 * t], start = tiles[2 * t + 1];
   const int64_t base = bounds[seg];
@@ -404,7 +425,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       dma4_v(src, lds_addr(lds_ld[stg]));
     }
   };
-  int r = 0, q0 = 0, h = hk * group;
+  int r = 0, q0 = 0, h = h_first;
   bool more = range_first(R, r, q0);
   __builtin_amdgcn_s_waitcnt(0);
   if (more) issue(0, h, r, q0);
@@ -417,7 +438,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     const bool full = k1 - start == 128 && cur_q0 >= (r ? last.lo1 : last.lo0) &&
                       cur_q0 + QT <= (r ? first.hi1 : first.hi0);
     more = range_next(R, QT, r, q0);
-    if (!more && h + 1 < (hk + 1) * group) {
+    if (!more && h + 1 < h_end) {
       ++h;
       more = range_first(R, r, q0);
     }
@@ -461,7 +482,23 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     }
     stg ^= 1;
   }
-  if (k_valid) {
+  if (k_valid && partial) {
+    // [2][group][N][nkv * HD]: dK partials, then dV partials
+    const int64_t plane = (int64_t)group * N * nkv * HD;
+    float* prow = partial + ((int64_t)(h_first % group) * N + base + ki) * (nkv * HD) + hk * HD;
+#pragma unroll
+    for (int db = 0; db < HD / 32; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = db * 32 + j * 8 + half * 4;
+        *reinterpret_cast<float4*>(prow + d) =
+            make_float4(dkacc[db][j * 4] * scale, dkacc[db][j * 4 + 1] * scale,
+                        dkacc[db][j * 4 + 2] * scale, dkacc[db][j * 4 + 3] * scale);
+        *reinterpret_cast<float4*>(prow + plane + d) =
+            make_float4(dvacc[db][j * 4], dvacc[db][j * 4 + 1], dvacc[db][j * 4 + 2],
+                        dvacc[db][j * 4 + 3]);
+      }
+  } else if (k_valid) {
     bf16_t* krow = dk + (base + ki) * ldk + hk * HD;
     bf16_t* vrow = dv + (base + ki) * lddv + hk * HD;
 #pragma unroll
@@ -479,9 +516,45 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   }
 }
 
+// dK / dV of every key from the group's float32 partials, summed in head
+// order (deterministic).  8 consecutive head_dim values per thread.
+__global__ void __launch_bounds__(256)
+fa128_dkdv_reduce_kernel(const float* __restrict__ partial, int group, int64_t N, int nkv,
+                         bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv) {
+  const int64_t width = (int64_t)nkv * HD;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= 2 * N * width) return;
+  const int which = i >= N * width;  // 0: dK, 1: dV
+  const int64_t e = which ? i - N * width : i;
+  const int64_t row = e / width, c = e % width;
+  const float* src = partial + (int64_t)which * group * N * width + e;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < group; ++g) {
+    const float4 a = *reinterpret_cast<const float4*>(src + (int64_t)g * N * width);
+    const float4 b = *reinterpret_cast<const float4*>(src + (int64_t)g * N * width + 4);
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+  bf16_t* dst = which ? dv + row * lddv + c : dk + row * width + c;
+  Vec8<bf16_t>::store(dst, acc);
+}
+
 // ---------------------------------------------------------------------------
 // Launchers (head_dim 128)
 // ---------------------------------------------------------------------------
+
+// The dK/dV pass splits its work by query head when (kv head, key tile)
+// workgroups would not fill the chip four times over: a single long sequence
+// has few key tiles and the first ones see most of the queries.
+static bool dkdv_head_split(int64_t n_tiles, int nq, int nkv) {
+  return nq > nkv && (int64_t)nkv * n_tiles < 1024;
+}
+
+int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles) {
+  // delta [nq][N], then (head split) the float32 dK/dV partials [2][group][N][nkv*128]
+  const int64_t delta = N * nq;
+  return dkdv_head_split(n_tiles, nq, nkv) ? delta + 2 * N * (int64_t)nq * HD : delta;
+}
 int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
                      float* lse, int64_t N, int nq, int nkv, int B, float scale, hipStream_t st) {
@@ -492,15 +565,25 @@ int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
 }
 
 int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
-                     const float* lse, const float* delta, const bf16_t* dout,
+                     const float* lse, const bf16_t* o, float* delta, const bf16_t* dout,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
                      bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
                      float scale, hipStream_t st) {
+  // the dQ pass writes delta, which the dK/dV pass reads (stream order)
   fa128_dq_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
-      q, k, v, ldv, lse, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale);
-  fa128_dkdv_kernel<<<dim3((unsigned)nkv, (unsigned)n_tiles), 256, 0, st>>>(
-      q, k, v, ldv, lse, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, N, nq, nkv, B,
-      scale);
+      q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale);
+  if (dkdv_head_split(n_tiles, nq, nkv)) {
+    float* partial = delta + N * nq;
+    fa128_dkdv_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
+        q, k, v, ldv, lse, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, partial, N, nq,
+        nkv, B, scale);
+    fa128_dkdv_reduce_kernel<<<ceil_div_u(2 * N * nkv * HD / 8, 256), 256, 0, st>>>(
+        partial, nq / nkv, N, nkv, dk, dv, lddv);
+  } else {
+    fa128_dkdv_kernel<<<dim3((unsigned)nkv, (unsigned)n_tiles), 256, 0, st>>>(
+        q, k, v, ldv, lse, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, nullptr, N,
+        nq, nkv, B, scale);
+  }
   ALODLM_CHECK_LAUNCH("attention_bwd_fa128");
   return ALODLM_OK;
 }

@@ -223,7 +223,8 @@ class StepEngine:
 
     def _attention_bwd(self, q, k, v, o, lse, do, dq, dk, dv, b):
         d, N = self.dims, q.shape[0]
-        ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads))
+        ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads, d.kv_heads,
+                                   d.head_dim, b.tiles.shape[0]))
         call("alodlm_attention_bwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(o), ptr(lse),
              ptr(do), ptr(b.boundaries), ptr(b.row_segment), ptr(b.tiles), b.tiles.shape[0],
              ptr(dq), ptr(dk), ptr(dv), d.qkv_width, ptr(ws), N, d.heads, d.kv_heads,

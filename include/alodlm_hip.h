@@ -138,14 +138,17 @@ int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t
  * bf16 and head_dim 64/128 the MFMA flash kernels run, otherwise (or with
  * tiles == NULL) the reference kernels.
  * bwd: dq [rows, nq*dh], dk [rows, nkv*dh], dv (stride lddv) from do.
- * `workspace` holds alodlm_attention_bwd_workspace(rows, nq) floats.
+ * `workspace` holds alodlm_attention_bwd_workspace(rows, nq, nkv, dh, n_tiles)
+ * floats (delta per head and row; for head_dim 128 with few key tiles per kv
+ * head, float32 dK/dV partials per query head as well).
  * ------------------------------------------------------------------------ */
 int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const int64_t* bounds, const int32_t* row_segment,
                          const int32_t* tiles, int64_t n_tiles, void* o, float* lse,
                          int64_t rows, int64_t nq, int64_t nkv, int64_t dh, int64_t block_size,
                          int dtype, void* stream);
-int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq);
+int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
+                                       int64_t n_tiles);
 int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const void* o, const float* lse, const void* dout,
                          const int64_t* bounds, const int32_t* row_segment,

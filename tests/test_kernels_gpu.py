@@ -258,7 +258,8 @@ def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block, path):
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dqkv = torch.zeros(N, W, dtype=dtype, device=DEV)
-    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq), dtype=torch.float32,
+    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0]),
+                     dtype=torch.float32,
                      device=DEV)
     dout_d = dout.to(DEV)
     L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
@@ -408,3 +409,65 @@ def test_cast_covers_more_than_2_32_elements():
     assert torch.equal(dst[-8192:].float().cpu(), torch.full((8192,), 5.0))
     del src, dst
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("seg_len,n_seg", [(1024, 8), (2048, 1)])
+def test_attention_fa128_large_packs_against_torch_fp32(seg_len, n_seg):
+    """head_dim-128 attention at the 1.7B head layout (16 q / 8 kv heads) on
+    long packs: 8 x 1024 tokens keeps one dK/dV workgroup per (kv head, key
+    tile); 1 x 2048 splits the dK/dV work by query head and reduces the float32
+    partials.  Reference: torch float32 autograd per segment under the
+    dual-stream mask (alodlm/batch.py:23-31), on the GPU."""
+    from alodlm_amd.batch import attention_mask, attention_tiles
+    L = lib()
+    nq, nkv, dh, block = 16, 8, 128, 32
+    log(f"attention fa128 large pack seg_len={seg_len} n_seg={n_seg}")
+    bounds = [i * seg_len for i in range(n_seg + 1)]
+    N = 2 * bounds[-1]
+    tiles = torch.tensor(attention_tiles(bounds), dtype=torch.int32).view(-1, 2).to(DEV)
+    packed = torch.tensor([2 * b for b in bounds], dtype=torch.int64, device=DEV)
+    seg = torch.repeat_interleave(torch.arange(n_seg, dtype=torch.int32), 2 * seg_len).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(seg_len + n_seg)
+    W = (nq + 2 * nkv) * dh
+    qkv = torch.randn(N, W, device=DEV, generator=g).to(torch.bfloat16)
+    q = qkv[:, :nq * dh].contiguous()
+    k = qkv[:, nq * dh:(nq + nkv) * dh].contiguous()
+    v = qkv[:, (nq + nkv) * dh:]
+    dout = torch.randn(N, nq * dh, device=DEV, generator=g).to(torch.bfloat16)
+    o = torch.empty(N, nq * dh, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(nq, N, dtype=torch.float32, device=DEV)
+    L.call("alodlm_attention_fwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(packed), L.ptr(seg),
+           L.ptr(tiles), tiles.shape[0], L.ptr(o), L.ptr(lse), N, nq, nkv, dh, block, 1, st())
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dqkv = torch.zeros(N, W, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0]),
+                     dtype=torch.float32, device=DEV)
+    L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
+           L.ptr(dout), L.ptr(packed), L.ptr(seg), L.ptr(tiles), tiles.shape[0], L.ptr(dq),
+           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block, 1,
+           st())
+    torch.cuda.synchronize()
+    dv = dqkv[:, (nq + nkv) * dh:]
+    mask = attention_mask(seg_len, block, DEV)
+    errs = {}
+    for s in range(n_seg):
+        rows = slice(2 * bounds[s], 2 * bounds[s + 1])
+        qs = q[rows].float().view(-1, nq, dh).transpose(0, 1).contiguous().requires_grad_(True)
+        ks = k[rows].float().view(-1, nkv, dh).transpose(0, 1).contiguous().requires_grad_(True)
+        vs = v[rows].float().reshape(-1, nkv, dh).transpose(0, 1).contiguous().requires_grad_(True)
+        kr = ks.repeat_interleave(nq // nkv, 0)
+        vr = vs.repeat_interleave(nq // nkv, 0)
+        sc = torch.matmul(qs, kr.transpose(1, 2).contiguous()) * dh ** -0.5
+        p = torch.softmax(sc.masked_fill(~mask, float("-inf")), -1)
+        ref = torch.matmul(p, vr)
+        go = dout[rows].float().view(-1, nq, dh).transpose(0, 1).contiguous()
+        gq, gk, gv = torch.autograd.grad(ref, (qs, ks, vs), go)
+        pairs = {"o": (o[rows], ref.detach().transpose(0, 1).reshape(-1, nq * dh)),
+                 "dq": (dq[rows], gq.transpose(0, 1).reshape(-1, nq * dh)),
+                 "dk": (dk[rows], gk.transpose(0, 1).reshape(-1, nkv * dh)),
+                 "dv": (dv[rows], gv.transpose(0, 1).reshape(-1, nkv * dh))}
+        for name, (got, want) in pairs.items():
+            e = ((got.float() - want).abs().max() / want.abs().max()).item()
+            errs[name] = max(errs.get(name, 0.0), e)
+    assert all(e <= 2e-2 for e in errs.values()), errs
