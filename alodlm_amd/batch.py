@@ -142,14 +142,22 @@ def _generator_of(device, generator):
     return torch.cuda.default_generators[index]
 
 
+def _to_device(array, device):
+    """Host array -> device tensor through pinned memory, without blocking:
+    a copy from pageable memory would wait for all work queued on the stream."""
+    return torch.from_numpy(np.ascontiguousarray(array)).pin_memory().to(device, non_blocking=True)
+
+
 @torch.no_grad()
 def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdpa",
-                generator=None, draws=None):
+                generator=None, draws=None, labels_host=None):
     """Dual-stream batch of one pack (alodlm/batch.py:34-85) on the GPU.
 
     ``backend`` is accepted for API compatibility; the attention kernels read the
     mask from the boundaries whatever its value.  ``draws`` (p, counts, perms)
-    may be supplied to replay known randomness.
+    may be supplied to replay known randomness.  ``labels_host``, a host copy
+    of ``labels``, saves reading them back from the device (which waits for
+    the work queued before this call).
     """
     if ids.ndim != 1 or ids.shape != labels.shape or ids.numel() == 0:
         raise ValueError("Expected nonempty flat input and label tensors")
@@ -183,7 +191,8 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
         assumed = full_block_counts(offsets, block_size)
         with torch.cuda.stream(side):
             speculative = _draw(assumed, offsets, block_size, device, generator)
-    labels_host = labels.detach().cpu().numpy()
+    if labels_host is None:
+        labels_host = labels.detach().cpu().numpy()
     with torch.cuda.stream(side):
         if draws is None:
             actual = block_supervised_counts(labels_host, offsets, block_size)
@@ -208,10 +217,11 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     ids = ids.to(torch.int64).contiguous()
     labels = labels.to(torch.int64).contiguous()
     n = 2 * len(ids)
-    to_dev = lambda a: torch.from_numpy(a).to(device, non_blocking=False)
-    seg_t = torch.tensor(offsets, dtype=torch.int64, device=device)
-    seg_block_t = torch.tensor(seg_block, dtype=torch.int32, device=device)
-    p_t, c_t, po_t = to_dev(probs), to_dev(counts), to_dev(perm_offset)
+    seg_t = _to_device(np.asarray(offsets, dtype=np.int64), device)
+    seg_block_t = _to_device(np.asarray(seg_block, dtype=np.int32), device)
+    p_t = _to_device(probs, device)
+    c_t = _to_device(counts, device)
+    po_t = _to_device(perm_offset, device)
     out = {
         "ids": torch.empty(n, dtype=torch.int64, device=device),
         "original": torch.empty(n, dtype=torch.int64, device=device),
@@ -238,7 +248,7 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     else:
         mask = plan_to_device(sparse_plan([2 * v for v in offsets], block_size, backend), device)
     pairs = sum(allowed_pairs(b - a, block_size) for a, b in zip(offsets, offsets[1:]))
-    tiles = torch.tensor(attention_tiles(offsets), dtype=torch.int32, device=device).view(-1, 2)
+    tiles = _to_device(np.asarray(attention_tiles(offsets), dtype=np.int32), device).view(-1, 2)
     return Batch(out["ids"], out["original"], out["positions"], out["masked"], out["prob"],
                  out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count, pairs,
                  tiles)

@@ -350,10 +350,14 @@ class StepEngine:
         K = cfg.max_depth
         st, c = self._stream(), self.code
         self.transposed.refresh(c, st)
-        ids = ids.to(self.device)
-        labels = labels.to(self.device)
+        # host inputs (a pack from the data loader): the labels are read on the
+        # host and the copies to the device do not block
+        labels_host = labels.numpy() if labels.device.type == "cpu" else None
+        pin = lambda t: t.pin_memory() if t.device.type == "cpu" and not t.is_pinned() else t
+        ids = pin(ids).to(self.device, non_blocking=True)
+        labels = pin(labels).to(self.device, non_blocking=True)
         b = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id,
-                        generator=generator, draws=draws)
+                        generator=generator, draws=draws, labels_host=labels_host)
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         S = b.boundaries.numel() - 1
         saves = [] if need_grad else None

@@ -117,6 +117,10 @@ class ALoDLM(nn.Module):
         path = Path(directory)
         path.mkdir(parents=True, exist_ok=True)
         state = state_dict if state_dict is not None else self.state_dict()
+        # Parameters are views of one device arena: each tensor is copied to
+        # host memory of its own, so that neither safetensors nor torch.save
+        # sees (or writes) the shared storage.
+        state = {k: v.detach().to("cpu", copy=True) for k, v in state.items()}
         backbone = {k[len("backbone."):]: v for k, v in state.items() if k.startswith("backbone.")}
         gate = {k[len("exit_gate."):]: v for k, v in state.items() if k.startswith("exit_gate.")}
         self.backbone.config._name_or_path = ""

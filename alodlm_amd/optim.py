@@ -55,6 +55,7 @@ class FusedAdamW(torch.optim.Optimizer):
         self.max_grad_norm = max_grad_norm
         self.last_grad_norm = None
         self._tables = None
+        self._norm_ready = False
 
     def _params(self):
         return [p for g in self.param_groups for p in g["params"]]
@@ -96,12 +97,50 @@ class FusedAdamW(torch.optim.Optimizer):
         self._partial = torch.empty(self._all.n_chunks, dtype=torch.float32, device=device)
         self._norm = torch.zeros(1, dtype=torch.float32, device=device)
 
+    def zero_grad(self, set_to_none=True):
+        self._norm_ready = False
+        super().zero_grad(set_to_none)
+
     def load_state_dict(self, state_dict):
-        super().load_state_dict(state_dict)
+        """Restore a ``state_dict()`` of this optimizer.
+
+        The float32 masters and moments are restored as float32 whatever the
+        parameter dtype (``torch.optim.Optimizer.load_state_dict`` would cast
+        them to it).  Float32 parameters take their master's values and share
+        its storage again.
+        """
+        saved_groups = state_dict["param_groups"]
+        if len(saved_groups) != len(self.param_groups):
+            raise ValueError("loaded state dict has a different number of parameter groups")
+        for group, saved in zip(self.param_groups, saved_groups):
+            if len(group["params"]) != len(saved["params"]):
+                raise ValueError("loaded state dict contains a parameter group that doesn't "
+                                 "match the size of optimizer's group")
+        self.state.clear()
+        for group, saved in zip(self.param_groups, saved_groups):
+            for key, value in saved.items():
+                if key != "params":
+                    group[key] = value
+            for p, index in zip(group["params"], saved["params"]):
+                entry = state_dict["state"].get(index)
+                if not entry:
+                    continue
+                f32 = lambda t: t.to(device=p.device, dtype=torch.float32).clone()
+                master = f32(entry["master"])
+                if p.dtype == torch.float32:
+                    p.data.copy_(master)
+                    master = p.detach()
+                self.state[p] = {"step": int(entry["step"]), "master": master,
+                                 "exp_avg": f32(entry["exp_avg"]),
+                                 "exp_avg_sq": f32(entry["exp_avg_sq"])}
         self._tables = None
+        self._norm_ready = False
 
     def grad_norm(self):
-        """Global L2 norm of all gradients into a device scalar (no host sync)."""
+        """Global L2 norm of all gradients into a device scalar (no host sync).
+
+        The next ``step()`` clips with this norm instead of computing it again,
+        so the gradients must not change in between."""
         if self._tables is None:
             self._prepare()
         params = self._params()
@@ -115,6 +154,7 @@ class FusedAdamW(torch.optim.Optimizer):
                   self._all.n_chunks, CHUNK, self._code, _lib.ptr(self._partial),
                   _lib.ptr(self._norm), _lib.stream_handle(self._device))
         self.last_grad_norm = self._norm[0]
+        self._norm_ready = True
         return self._norm[0], grads
 
     @torch.no_grad()
@@ -124,8 +164,10 @@ class FusedAdamW(torch.optim.Optimizer):
             self._prepare()
         norm_ptr = None
         if self.max_grad_norm is not None:
-            self.grad_norm()
+            if not self._norm_ready:
+                self.grad_norm()
             norm_ptr = _lib.ptr(self._norm)
+        self._norm_ready = False
         for group, table in zip(self.param_groups, self._tables):
             if table is None:
                 continue

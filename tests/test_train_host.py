@@ -1,0 +1,189 @@
+"""Host side of the training loop (alodlm/train.py) without a GPU: horizon,
+schedule, run identity, pack order, checkpoint pruning and the training-state
+round trip, against a recorded run of the reference on the workflow fixture."""
+
+import json
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from tests.golden import HERE as GOLDEN
+
+# the schedule is stepped without optimizer steps here
+pytestmark = pytest.mark.filterwarnings("ignore:Detected call of `lr_scheduler.step")
+
+RUN = json.loads((GOLDEN / "workflow" / "train.json").read_text())
+FIXTURE = GOLDEN / "workflow" / "fixture"
+
+
+def fixture_config(tmp_path, **overrides):
+    from alodlm_amd.config import ModelConfig, TrainConfig
+    values = dict(RUN["config"])
+    values.update(model_dir=str(FIXTURE / "base"), train_file=str(tmp_path / "training.jsonl"),
+                  output_dir=str(tmp_path / "run"), cache_file=str(tmp_path / "packed.pt"))
+    values.update(overrides)
+    values["model"] = ModelConfig(**values["model"])
+    return TrainConfig(**values)
+
+
+def test_horizon():
+    """steps = ceil(packs / gas) per epoch, times epochs, capped by max_steps
+    (alodlm/train.py:50-54); the fixture run has 5 packs, 2 epochs, cap 4."""
+    from alodlm_amd.train import training_horizon
+    assert training_horizon(5, 1, 2, 4) == RUN["run"]["header"]["training_steps"] == 4
+    assert training_horizon(5, 1, 2, 0) == 10
+    assert training_horizon(5, 2, 2, 0) == 6
+    assert training_horizon(7, 3, 1, 0) == 3
+    assert training_horizon(7, 3, 1, 2) == 2
+
+
+def test_schedule_matches_reference_run(tmp_path):
+    """The learning rate logged after each step equals the reference's."""
+    from alodlm_amd.optim import FusedAdamW
+    from alodlm_amd.train import cosine_schedule
+    cfg = fixture_config(tmp_path)
+    p = torch.nn.Parameter(torch.zeros(4))
+    opt = FusedAdamW([{"params": [p], "weight_decay": 0.0}], lr=cfg.learning_rate)
+    sched = cosine_schedule(opt, 4, cfg.warmup_ratio)
+    assert opt.param_groups[0]["lr"] == cfg.learning_rate
+    for record in RUN["run"]["metrics"]:
+        sched.step()
+        assert sched.get_last_lr()[0] == pytest.approx(record["learning_rate"], rel=1e-12, abs=1e-18)
+    # warmup: int(20 * 0.25) = 5 steps from 0
+    opt2 = FusedAdamW([{"params": [p], "weight_decay": 0.0}], lr=1.0)
+    sched2 = cosine_schedule(opt2, 20, 0.25)
+    lrs = [opt2.param_groups[0]["lr"]]
+    for _ in range(20):
+        sched2.step()
+        lrs.append(opt2.param_groups[0]["lr"])
+    assert lrs[:6] == pytest.approx([0.0, 0.2, 0.4, 0.6, 0.8, 1.0])
+    assert lrs[20] == pytest.approx(0.0, abs=1e-12)
+
+
+def test_identity_matches_reference(tmp_path):
+    """The resume identity equals the one the reference wrote."""
+    from alodlm_amd.train import run_identity
+    want = RUN["run"]["checkpoints"]["checkpoint-2"]["trainer_state"]["identity"]
+    got = run_identity(fixture_config(tmp_path), want["cache_identity"], 4)
+    assert got == want
+    other = run_identity(fixture_config(tmp_path, learning_rate=2e-5), want["cache_identity"], 4)
+    assert other != want
+    # paths do not enter the identity
+    moved = run_identity(fixture_config(tmp_path, output_dir="/elsewhere", resume="x"),
+                         want["cache_identity"], 4)
+    assert moved == want
+
+
+def test_pack_order_matches_reference():
+    """From the CPU generator state the reference recorded at the start of
+    the epoch, the loader yields the reference's packs in its order, and the
+    resumed loader (2 packs skipped) continues with the same order."""
+    from alodlm_amd.train import pack_loader
+
+    class Indices(torch.utils.data.Dataset):
+        def __len__(self):
+            return 5
+
+        def __getitem__(self, i):
+            return {"index": i}
+
+    epoch_rng = RUN["run"]["checkpoints"]["checkpoint-2"]["trainer_state"]["epoch_rng"]
+    assert epoch_rng["sampler"] is None
+    state = torch.tensor(epoch_rng["cpu"], dtype=torch.uint8)
+    saved = torch.get_rng_state()
+    try:
+        torch.set_rng_state(state)
+        order = [item["index"] for item in pack_loader(Indices())]
+        assert order[:4] == RUN["run"]["consumed"][:4]
+        torch.set_rng_state(state)
+        resumed = [item["index"] for item in pack_loader(Indices(), skip=2)]
+        assert resumed == order[2:]
+        assert resumed[:2] == RUN["resumed"]["consumed"][:2]
+    finally:
+        torch.set_rng_state(saved)
+
+
+def test_prune_checkpoints(tmp_path):
+    """Only completed checkpoint-<n> directories count; the newest are kept."""
+    from alodlm_amd.train import completed_checkpoints, prune_checkpoints
+    for n in (2, 10, 4, 6):
+        d = tmp_path / f"checkpoint-{n}"
+        d.mkdir()
+        (d / "trainer_state.json").write_text("{}")
+    (tmp_path / "checkpoint-8").mkdir()  # incomplete
+    (tmp_path / "checkpoint-x").mkdir()
+    (tmp_path / "checkpoint-12").symlink_to(tmp_path / "checkpoint-10")
+    assert [p.name for p in completed_checkpoints(tmp_path)] == [
+        "checkpoint-2", "checkpoint-4", "checkpoint-6", "checkpoint-10"]
+    prune_checkpoints(tmp_path, 2)
+    assert sorted(p.name for p in tmp_path.iterdir()) == [
+        "checkpoint-10", "checkpoint-12", "checkpoint-6", "checkpoint-8", "checkpoint-x"]
+
+
+def test_training_state_round_trip(tmp_path):
+    """Optimizer masters and moments stay float32 for bf16 parameters, step
+    counts, schedule and every generator are restored."""
+    from alodlm_amd.optim import FusedAdamW
+    from alodlm_amd.train import cosine_schedule, load_training_state, save_training_state
+
+    def make():
+        model = torch.nn.Module()
+        model.a = torch.nn.Parameter(torch.randn(3, 5).to(torch.bfloat16))
+        model.bias = torch.nn.Parameter(torch.randn(7).to(torch.bfloat16))
+        opt = FusedAdamW([{"params": [model.a], "weight_decay": 0.01},
+                          {"params": [model.bias], "weight_decay": 0.0}], lr=1e-3)
+        return model, opt, cosine_schedule(opt, 10, 0.2)
+
+    model, opt, sched = make()
+    for p in (model.a, model.bias):
+        opt.state[p] = {"step": 3, "master": torch.randn(p.shape, dtype=torch.float64).float(),
+                        "exp_avg": torch.randn(p.shape), "exp_avg_sq": torch.rand(p.shape)}
+    for _ in range(3):
+        sched.step()
+    random.seed(5)
+    np.random.seed(6)
+    torch.manual_seed(7)
+    save_training_state(tmp_path / "state", model, opt, sched)
+    expect = (random.random(), np.random.rand(), torch.rand(1).item())
+    model2, opt2, sched2 = make()
+    load_training_state(tmp_path / "state", model2, opt2, sched2)
+    for p, q in ((model.a, model2.a), (model.bias, model2.bias)):
+        for key in ("master", "exp_avg", "exp_avg_sq"):
+            assert opt2.state[q][key].dtype == torch.float32
+            assert torch.equal(opt2.state[q][key], opt.state[p][key])
+        assert opt2.state[q]["step"] == 3
+    assert opt2.param_groups[0]["lr"] == opt.param_groups[0]["lr"]
+    assert opt2.param_groups[1]["weight_decay"] == 0.0
+    assert opt2.param_groups[0]["betas"] == (0.9, 0.999)
+    sched.step()
+    sched2.step()
+    assert sched2.get_last_lr() == sched.get_last_lr()
+    assert (random.random(), np.random.rand(), torch.rand(1).item()) == expect
+    files = sorted(p.name for p in (tmp_path / "state").iterdir())
+    assert files == ["optimizer-00000.safetensors", "optimizer.json", "random_states.json",
+                     "scheduler.json"]
+
+
+def test_train_needs_gpu(tmp_path):
+    from alodlm_amd.train import train
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="GPU"):
+        train(fixture_config(tmp_path))
+
+
+def test_config_errors(tmp_path):
+    """TrainConfig.load rejects what the reference rejects (alodlm/config.py:82-102)."""
+    import yaml
+    from alodlm_amd.config import TrainConfig
+    base = dict(RUN["config"], model_dir="m", train_file="t", output_dir="o", cache_file="c")
+    path = tmp_path / "c.yaml"
+    path.write_text(yaml.safe_dump(base))
+    assert TrainConfig.load(path).max_steps == 4
+    for change in ({"bogus": 1}, {"warmup_ratio": 1.0}, {"precision": "fp16"},
+                   {"learning_rate": 0.0}, {"save_steps": 0}, {"max_steps": -1}):
+        path.write_text(yaml.safe_dump(dict(base, **change)))
+        with pytest.raises(ValueError):
+            TrainConfig.load(path)
