@@ -451,7 +451,12 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       sacc = mfma(row_frag(qt, col, kk * 2 + half), kf[kk], sacc);
       pacc = mfma(row_frag(dt, col, kk * 2 + half), row_frag(lds_v, wave * 32 + col, kk * 2 + half), pacc);
     }
-    // S[q, key]: lane owns the key column; element e is query row 8(e/4) + 4*half + e%4
+    // S[q, key]: lane owns the key column; element e is query row 8(e/4) + 4*half + e%4.
+    // Query qq is allowed iff (unsigned)(qq - qlo) < qhi - qlo; for a tile every
+    // key sees whole the bound is set so that the test always passes (one add,
+    // compare and select per element, no second copy of the loop body).
+    const int q_off = full ? 0 : cur_q0 + half * 4 - qlo;
+    const unsigned q_width = full ? 0xffffffffu : (unsigned)(qhi - qlo);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int qo = j * 8 + half * 4;
@@ -462,10 +467,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       for (int i = 0; i < 4; ++i) {
         const int e = j * 4 + i;
         float p = fast_exp2(fmaf(sacc[e], c, -lsv[i] * FA_LOG2E));
-        if (!full) {
-          const int qq = cur_q0 + qo + i;
-          if (qq < qlo || qq >= qhi) p = 0.f;
-        }
+        if ((unsigned)(q_off + j * 8 + i) >= q_width) p = 0.f;
         sacc[e] = p;
         pacc[e] = p * (pacc[e] - dlv[i]);
       }

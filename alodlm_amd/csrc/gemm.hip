@@ -208,7 +208,7 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __rest
     }
 }
 
-// C[m, n] += sum_s partial[s, m, n]
+// C[m, n] += sum_s partial[s, m, n] (partials summed in split order, then added)
 __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int64_t splits, int64_t M,
                                      int64_t N, float* __restrict__ C, int64_t ldc) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -216,6 +216,40 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int64_t 
   float s = 0.f;
   for (int64_t p = 0; p < splits; ++p) s += partial[p * M * N + i];
   C[(i / N) * ldc + (i % N)] += s;
+}
+
+// The same sum, 4 consecutive columns per thread (N, ldc multiples of 4, both
+// buffers 16-byte aligned): grid.x covers a row's N/4 column groups, grid.y
+// strides over rows, so no 64-bit division is needed.
+__global__ void splitk_reduce4_kernel(const float* __restrict__ partial, int64_t splits,
+                                      int64_t M, int64_t N, float* __restrict__ C, int64_t ldc) {
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (n >= N) return;
+  const int64_t plane = M * N;
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+    const float* src = partial + m * N + n;
+    float4 s = *reinterpret_cast<const float4*>(src);
+    for (int64_t p = 1; p < splits; ++p) {
+      const float4 t = *reinterpret_cast<const float4*>(src + p * plane);
+      s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+    }
+    float4* dst = reinterpret_cast<float4*>(C + m * ldc + n);
+    float4 c = *dst;
+    c.x += s.x; c.y += s.y; c.z += s.z; c.w += s.w;
+    *dst = c;
+  }
+}
+
+static void splitk_reduce(const float* partial, int64_t splits, int64_t M, int64_t N, float* C,
+                          int64_t ldc, hipStream_t st) {
+  const bool vec = N % 4 == 0 && ldc % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(partial) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
+  if (vec) {
+    const dim3 grid(ceil_div_u(N / 4, 256), (unsigned)(M < 65535 ? M : 65535));
+    splitk_reduce4_kernel<<<grid, 256, 0, st>>>(partial, splits, M, N, C, ldc);
+  } else {
+    splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(partial, splits, M, N, C, ldc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -344,8 +378,7 @@ static void launch_mfma(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t l
   else
     gemm_bf16_kernel<AK, BK, ALODLM_EPI_ACCUM><<<grid, GM_THREADS, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
-  if (part)
-    splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(part, nsplit, M, N, (float*)C, ldc);
+  if (part) splitk_reduce(part, nsplit, M, N, (float*)C, ldc, st);
 }
 
 extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb,
@@ -369,8 +402,7 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
                    (const bf16_t*)R, ldr, M, N, K, alpha, epilogue, workspace, splits, &nsplit, st);
     ALODLM_CHECK_LAUNCH("gemm_bf16_dl");
     if (epilogue == ALODLM_EPI_ACCUM && nsplit > 1) {
-      splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(workspace, nsplit, M, N,
-                                                                   (float*)C, ldc);
+      splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st);
       ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
     }
     return ALODLM_OK;
@@ -387,8 +419,7 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
                     (const bf16_t*)R, ldr, M, N, K, alpha, epilogue, workspace, splits, &nsplit, st);
     ALODLM_CHECK_LAUNCH("gemm_bf16_256");
     if (epilogue == ALODLM_EPI_ACCUM && nsplit > 1) {
-      splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(workspace, nsplit, M, N,
-                                                                   (float*)C, ldc);
+      splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st);
       ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
     }
     return ALODLM_OK;

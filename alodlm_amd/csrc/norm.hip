@@ -59,6 +59,51 @@ rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restri
   }
 }
 
+// The same for rows of at most 512*NCH columns (a multiple of 8): the row is
+// read once into registers, the weight once per wavefront, and each wavefront
+// strides over rows.  Same arithmetic and summation order as above.
+template <typename T, int NCH>
+__global__ void __launch_bounds__(64 * NORM_WAVES)
+rmsnorm_fwd_vec_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
+                       float* __restrict__ rstd, int64_t rows, int64_t cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  float wv[NCH][8];
+#pragma unroll
+  for (int t = 0; t < NCH; ++t) {
+    const int64_t c = (int64_t)lane * 8 + 512 * t;
+    if (c < cols) Vec8<T>::load(w + c, wv[t]);
+  }
+  const int64_t stride = (int64_t)gridDim.x * NORM_WAVES;
+  for (int64_t row = (int64_t)blockIdx.x * NORM_WAVES + (threadIdx.x >> 6); row < rows;
+       row += stride) {
+    const T* xr = x + row * cols;
+    float v[NCH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      const int64_t c = (int64_t)lane * 8 + 512 * t;
+      if (c < cols) {
+        Vec8<T>::load(xr + c, v[t]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[t][i] * v[t][i];
+      }
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+    if (lane == 0 && rstd) rstd[row] = r;
+    T* yr = y + row * cols;
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      const int64_t c = (int64_t)lane * 8 + 512 * t;
+      if (c < cols) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[t][i] = wv[t][i] * Elem<T>::round(v[t][i] * r);
+        Vec8<T>::store(yr + c, v[t]);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Backward.  dx = dres + r*(dy*w) - x*r^3*mean((dy*w)*x); the weight gradient
 // sum dy*cast(x*r) is kept per lane in registers (NCH 8-wide chunks per lane,
@@ -138,6 +183,97 @@ rmsnorm_bwd_vec_kernel(const T* __restrict__ dy, const T* __restrict__ x,
 #pragma unroll
     for (int v = 0; v < NORM_WAVES; ++v) s += lds[v * cols + c];
     partial[(int64_t)blockIdx.x * cols + c] = s;
+  }
+}
+
+// bf16 rows kept packed in registers: element i of an 8-wide chunk.
+__device__ __forceinline__ float bf16_elem(const uint4& u, int i) {
+  const uint32_t w = i < 2 ? u.x : i < 4 ? u.y : i < 6 ? u.z : u.w;
+  return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
+// The bf16 backward with dy, x and w held as packed bf16 (4 registers per
+// 8-wide chunk instead of 8), which keeps several wavefronts per SIMD at
+// hidden 4096.  Same arithmetic as rmsnorm_bwd_vec_kernel.
+template <int NCH>
+__global__ void __launch_bounds__(64 * NORM_WAVES)
+rmsnorm_bwd_bf16_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
+                        const float* __restrict__ rstd, const bf16_t* __restrict__ w,
+                        const bf16_t* dres, bf16_t* dx, float* __restrict__ partial, int64_t rows,
+                        int64_t cols, const int32_t* __restrict__ skip_exits, int64_t skip_depth) {
+  extern __shared__ float lds[];  // [NORM_WAVES][cols]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float acc[NCH][8];
+  uint4 wr[NCH];
+#pragma unroll
+  for (int t = 0; t < NCH; ++t) {
+    const int64_t c = (int64_t)lane * 8 + 512 * t;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[t][i] = 0.f;
+    if (c < cols) wr[t] = *reinterpret_cast<const uint4*>(w + c);
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * BWD_ROWS_PER_BLOCK;
+  for (int64_t row = r0 + wave; row < r0 + BWD_ROWS_PER_BLOCK && row < rows; row += NORM_WAVES) {
+    const bool skip = skip_exits && skip_exits[row] <= skip_depth;
+    const float r = rstd[row];
+    uint4 ar[NCH], br[NCH];
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      const int64_t c = (int64_t)lane * 8 + 512 * t;
+      if (c < cols && !skip) {
+        ar[t] = *reinterpret_cast<const uint4*>(dy + row * cols + c);
+        br[t] = *reinterpret_cast<const uint4*>(x + row * cols + c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float a = bf16_elem(ar[t], i), b = bf16_elem(br[t], i);
+          s += a * bf16_elem(wr[t], i) * b;
+          acc[t][i] += a * round_bf16(b * r);
+        }
+      }
+    }
+    s = wave_sum(s);
+    const float k = s * r * r * r / (float)cols;
+    // the second pass unpacks the packed rows again instead of keeping the
+    // first pass's floats alive (the empty asm hides the values' origin)
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      asm volatile("" : "+v"(ar[t].x), "+v"(ar[t].y), "+v"(ar[t].z), "+v"(ar[t].w));
+      asm volatile("" : "+v"(br[t].x), "+v"(br[t].y), "+v"(br[t].z), "+v"(br[t].w));
+      asm volatile("" : "+v"(wr[t].x), "+v"(wr[t].y), "+v"(wr[t].z), "+v"(wr[t].w));
+    }
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      const int64_t c = (int64_t)lane * 8 + 512 * t;
+      if (c >= cols) continue;
+      float o[8];
+      if (dres) Vec8<bf16_t>::load(dres + row * cols + c, o);
+      else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = 0.f;
+      }
+      if (!skip) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          o[i] += r * bf16_elem(ar[t], i) * bf16_elem(wr[t], i) - bf16_elem(br[t], i) * k;
+      }
+      Vec8<bf16_t>::store(dx + row * cols + c, o);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NCH; ++t) {
+    const int64_t c = (int64_t)lane * 8 + 512 * t;
+    if (c < cols) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lds[wave * cols + c + i] = acc[t][i];
+    }
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < cols; c += 64 * NORM_WAVES) {
+    float sum = 0.f;
+#pragma unroll
+    for (int v = 0; v < NORM_WAVES; ++v) sum += lds[v * cols + c];
+    partial[(int64_t)blockIdx.x * cols + c] = sum;
   }
 }
 
@@ -241,9 +377,18 @@ extern "C" int alodlm_rmsnorm_fwd(const void* x, const void* w, void* y, float* 
   const bool v8 = cols % 8 == 0 && aligned8(x, dtype) && aligned8(y, dtype) && aligned8(w, dtype);
   ALODLM_DISPATCH(dtype, T, {
     dim3 grid(ceil_div_u(rows, NORM_WAVES));
-    if (v8) rmsnorm_fwd_kernel<T, true><<<grid, 64 * NORM_WAVES, 0, as_stream(stream)>>>(
+    // register-resident rows: about 4 rows per wavefront, at most 8192 blocks
+    dim3 vgrid(ceil_div_u(rows, 4 * NORM_WAVES) < 8192 ? ceil_div_u(rows, 4 * NORM_WAVES) : 8192);
+    hipStream_t st = as_stream(stream);
+    if (v8 && cols <= 2048)
+      rmsnorm_fwd_vec_kernel<T, 4><<<vgrid, 64 * NORM_WAVES, 0, st>>>(
+          (const T*)x, (const T*)w, (T*)y, rstd, rows, cols, eps);
+    else if (v8 && cols <= 4096)
+      rmsnorm_fwd_vec_kernel<T, 8><<<vgrid, 64 * NORM_WAVES, 0, st>>>(
+          (const T*)x, (const T*)w, (T*)y, rstd, rows, cols, eps);
+    else if (v8) rmsnorm_fwd_kernel<T, true><<<grid, 64 * NORM_WAVES, 0, st>>>(
         (const T*)x, (const T*)w, (T*)y, rstd, rows, cols, eps);
-    else rmsnorm_fwd_kernel<T, false><<<grid, 64 * NORM_WAVES, 0, as_stream(stream)>>>(
+    else rmsnorm_fwd_kernel<T, false><<<grid, 64 * NORM_WAVES, 0, st>>>(
         (const T*)x, (const T*)w, (T*)y, rstd, rows, cols, eps);
   });
   ALODLM_CHECK_LAUNCH("rmsnorm_fwd");
@@ -266,6 +411,22 @@ static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, 
                   aligned8(dx, dtype) && aligned8(w, dtype) && (!dres || aligned8(dres, dtype));
   const int64_t nparts = (rows + BWD_ROWS_PER_BLOCK - 1) / BWD_ROWS_PER_BLOCK;
   const int64_t nch = (cols + 511) / 512;
+  const size_t lds_bytes = (size_t)NORM_WAVES * cols * sizeof(float);
+  if (dtype == ALODLM_BF16 && v8 && nch <= 8 && lds_bytes <= 128 * 1024) {
+    const bf16_t *dyb = (const bf16_t*)dy, *xb = (const bf16_t*)x, *wb = (const bf16_t*)w;
+    if (nch <= 4)
+      rmsnorm_bwd_bf16_kernel<4><<<(unsigned)nparts, 64 * NORM_WAVES, lds_bytes, st>>>(
+          dyb, xb, rstd, wb, (const bf16_t*)dres, (bf16_t*)dx, workspace, rows, cols, skip_exits,
+          skip_depth);
+    else
+      rmsnorm_bwd_bf16_kernel<8><<<(unsigned)nparts, 64 * NORM_WAVES, lds_bytes, st>>>(
+          dyb, xb, rstd, wb, (const bf16_t*)dres, (bf16_t*)dx, workspace, rows, cols, skip_exits,
+          skip_depth);
+    ALODLM_CHECK_LAUNCH("rmsnorm_bwd");
+    if (dw_accum)
+      return column_reduce(workspace, nparts, cols, 0, cols, dw_accum, workspace + nparts * cols, st);
+    return ALODLM_OK;
+  }
   ALODLM_DISPATCH(dtype, T, {
     const size_t lds = (size_t)NORM_WAVES * cols * sizeof(float);
     if (v8 && nch <= 1)

@@ -157,7 +157,8 @@ def test_swiglu_fwd_bwd(dtype, rows, inter):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,cols", [(37, 256), (64, 2048), (5, 100)])
+@pytest.mark.parametrize("rows,cols", [(37, 256), (64, 2048), (5, 100), (129, 4096), (1000, 2048),
+                                       (140000, 64)])
 def test_rmsnorm_fwd_bwd(dtype, rows, cols):
     L = lib()
     log(f"rmsnorm rows={rows} cols={cols} {dtype}")
