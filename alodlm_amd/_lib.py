@@ -52,6 +52,7 @@ SIGNATURES = {
     "alodlm_scatter_rows": [P, P, I64, P, I64, I64, I32, P],
     "alodlm_cross_entropy": [P, P, P, P, I64, I64, P, P, I32, P],
     "alodlm_scatter_ce": [P, P, P, I64, P, I64, P],
+    "alodlm_decode_readout": [P, I64, I64, P, P, I32, P],
     "alodlm_objective_workspace": [I64, I64, I64],
     "alodlm_objective": [P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P],
     "alodlm_gate_bwd_workspace": [I64, I64],

@@ -398,6 +398,75 @@ extern "C" int alodlm_cross_entropy(void* logits, const int32_t* target, const f
   return ALODLM_OK;
 }
 
+// Decode readout (alodlm/inference.py:115-118): per row of logits, the index
+// of the largest logit (the first one among equal maxima, like torch.argmax)
+// and the entropy -sum p log p = lse - sum p * x of the softmax, in float32.
+// The logits are left unchanged.  One 256-thread block per row.
+template <typename T>
+__global__ void __launch_bounds__(256)
+decode_readout_kernel(const T* __restrict__ logits, int64_t V, int64_t* __restrict__ argmax,
+                      float* __restrict__ entropy) {
+  __shared__ float sm[4], ss[4], st[4], bv[4];
+  __shared__ int64_t bi[4];
+  const T* lr = logits + (int64_t)blockIdx.x * V;
+  float m = -INFINITY, s = 0.f, t = 0.f, best = -INFINITY;
+  int64_t best_i = V;
+  for (int64_t c = threadIdx.x; c < V; c += 256) {
+    const float x = Elem<T>::load(lr, c);
+    if (x > best) { best = x; best_i = c; }  // a thread's indices increase
+    if (x > m) {
+      const float scale = expf(m - x);
+      s = s * scale + 1.f;
+      t = t * scale + x;
+      m = x;
+    } else {
+      const float e = expf(x - m);
+      s += e;
+      t += e * x;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // argmax across the wavefront: larger value, or equal value and smaller index
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off, 64);
+    const int64_t oi = __shfl_xor(best_i, off, 64);
+    if (ov > best || (ov == best && oi < best_i)) { best = ov; best_i = oi; }
+  }
+  const float M = wave_max(m);
+  const float scale = (m == -INFINITY) ? 0.f : expf(m - M);
+  const float S = wave_sum(s * scale), Tt = wave_sum(t * scale);
+  if (lane == 0) { sm[wave] = M; ss[wave] = S; st[wave] = Tt; bv[wave] = best; bi[wave] = best_i; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float gm = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+    float gs = 0.f, gt = 0.f, gv = bv[0];
+    int64_t gi = bi[0];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = (sm[w] == -INFINITY) ? 0.f : expf(sm[w] - gm);
+      gs += ss[w] * f;
+      gt += st[w] * f;
+      if (bv[w] > gv || (bv[w] == gv && bi[w] < gi)) { gv = bv[w]; gi = bi[w]; }
+    }
+    argmax[blockIdx.x] = gi;
+    entropy[blockIdx.x] = gm + logf(gs) - gt / gs;
+  }
+}
+
+extern "C" int alodlm_decode_readout(const void* logits, int64_t rows, int64_t vocab,
+                                     int64_t* argmax, float* entropy, int dtype, void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && vocab > 0, "decode_readout: bad shape");
+  ALODLM_CHECK_ARG(rows <= 0x7fffffff, "decode_readout: too many rows");
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    decode_readout_kernel<T><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+        (const T*)logits, vocab, argmax, entropy);
+  });
+  ALODLM_CHECK_LAUNCH("decode_readout");
+  return ALODLM_OK;
+}
+
 extern "C" int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n_rows,
                                  int64_t max_rows, float* ce_full, int64_t rows, void* stream) {
   (void)rows;

@@ -235,6 +235,12 @@ int alodlm_scatter_rows(const void* src, const int32_t* sel_rows, int64_t n_sel,
 int alodlm_cross_entropy(void* logits, const int32_t* target, const float* coef,
                          const int32_t* n_rows, int64_t max_rows, int64_t vocab, float* ce,
                          float* entropy, int dtype, void* stream);
+/* Decode readout (alodlm/inference.py:115-118: logits.argmax(-1) and the
+ * entropy -(exp(logp) * logp).sum(-1) of log_softmax(logits.float())):
+ * logits [rows, V] (dtype, unchanged) -> argmax[rows] (int64; the first index
+ * among equal maxima) and entropy[rows] (float). */
+int alodlm_decode_readout(const void* logits, int64_t rows, int64_t vocab, int64_t* argmax,
+                          float* entropy, int dtype, void* stream);
 /* Scatter ce of the selected rows into ce_full[depth, rows]. */
 int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n_rows,
                       int64_t max_rows, float* ce_full, int64_t rows, void* stream);

@@ -1,0 +1,265 @@
+"""Cached adaptive decoding on the HIP kernels (alodlm/inference.py;
+tests/test_inference.py): the reference's generations on the workflow
+fixture's model (fresh and trained gate), the decode attention layout on both
+attention paths, cache consistency and the reference's behavioural tests."""
+
+import json
+import math
+import sys
+
+import pytest
+import torch
+
+from tests.golden import HERE as GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+FIXTURE = GOLDEN / "workflow" / "fixture"
+DECODE = json.loads((GOLDEN / "decode" / "decode.json").read_text())
+RUN = json.loads((GOLDEN / "workflow" / "train.json").read_text())
+
+
+def log(msg):
+    print(f"[decode] {msg}", file=sys.stderr, flush=True)
+
+
+def tokenizer():
+    from alodlm_amd.data import load_tokenizer
+    return load_tokenizer(FIXTURE / "base")
+
+
+def base_model(dtype=torch.float32, **changes):
+    from transformers import AutoModelForCausalLM
+    from alodlm_amd.config import ModelConfig
+    from alodlm_amd.model import ALoDLM
+    backbone = AutoModelForCausalLM.from_pretrained(str(FIXTURE / "base"), dtype=dtype)
+    fields = dict(RUN["config"]["model"])
+    fields["gate_init_pi"] = tuple(fields["gate_init_pi"])
+    fields.update(changes)
+    return ALoDLM(backbone, ModelConfig(**fields)).to(DEV)
+
+
+def trained_model():
+    from alodlm_amd.model import ALoDLM
+    return ALoDLM.from_pretrained(GOLDEN / "decode" / "trained").to(DEV)
+
+
+@pytest.mark.parametrize("which", ["base", "trained"])
+def test_generation_matches_reference(which):
+    """Token ids, exit depths, step/pass counts and stop reason equal the
+    reference decoder's; first-pass halt probabilities to 1e-6."""
+    from alodlm_amd.inference import DecodeConfig, Decoder
+    model = base_model() if which == "base" else trained_model()
+    decoder = Decoder(model, tokenizer())
+    for case, want in zip(DECODE["cases"], DECODE[which]["runs"]):
+        log(f"{which} {case['config']}")
+        got = decoder.generate(case["prompt"], DecodeConfig(**case["config"]))
+        for key in ("token_ids", "exit_depths", "outer_steps", "recurrent_passes",
+                    "loop_token_passes", "stop_reason", "generated_tokens", "prompt_tokens"):
+            assert got[key] == want[key], (which, case, key)
+        assert got["first_pass_halt_probabilities"] == pytest.approx(
+            want["first_pass_halt_probabilities"], abs=1e-6)
+        assert got["wall_seconds"] >= got["prefill_seconds"] > 0
+
+
+@pytest.mark.parametrize("which", ["base", "trained"])
+def test_prefill_cache_matches_reference(which):
+    from alodlm_amd.inference import DecodeConfig, Decoder, PrefixCache
+    model = base_model() if which == "base" else trained_model()
+    decoder = Decoder(model, tokenizer())
+    cache = PrefixCache(model.config)
+    empty = torch.empty(0, dtype=torch.long, device=DEV)
+    with torch.inference_mode():
+        window = decoder._window(torch.tensor([4, 7, 9, 12, 5], device=DEV),
+                                 torch.arange(5, device=DEV), cache, empty, DecodeConfig(), empty)[0]
+        cache.append(window, torch.arange(5, device=DEV))
+    want = DECODE[which]["prefill_kv"]
+    assert sorted(f"{a},{b}" for a, b in cache.values) == sorted(want)
+    for key, (k, v) in cache.values.items():
+        ref = want[f"{key[0]},{key[1]}"]
+        torch.testing.assert_close(k.flatten().cpu(), torch.tensor(ref[0]), atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(v.flatten().cpu(), torch.tensor(ref[1]), atol=1e-5, rtol=1e-5)
+
+
+LAYOUT_CASES = [
+    # (dtype, head_dim, tiled layout, prefix rows, window rows)
+    (torch.bfloat16, 128, True, 0, 16),
+    (torch.bfloat16, 128, True, 5, 16),
+    (torch.bfloat16, 128, True, 127, 1),
+    (torch.bfloat16, 128, True, 128, 16),
+    (torch.bfloat16, 128, True, 300, 200),
+    (torch.bfloat16, 64, True, 300, 16),
+    (torch.bfloat16, 64, True, 0, 150),
+    (torch.float32, 8, False, 0, 7),
+    (torch.float32, 8, False, 37, 5),
+    (torch.bfloat16, 8, False, 130, 16),
+    (torch.float32, 64, False, 129, 3),
+]
+
+
+@pytest.mark.parametrize("dtype,dh,tiled,prefix,window", LAYOUT_CASES)
+def test_window_attention_layout(dtype, dh, tiled, prefix, window):
+    """The attention kernels on the decode layout equal softmax attention of
+    each window row over every prefix key and the window keys up to itself
+    (alodlm/inference.py:77-79), against torch float32."""
+    from alodlm_amd import _lib
+    from alodlm_amd.inference import _WindowLayout
+    _lib.load()
+    log(f"layout {dtype} dh={dh} tiled={tiled} P={prefix} W={window}")
+    nq, nkv = 4, 2
+    g = torch.Generator().manual_seed(prefix * 7 + window)
+    q = torch.randn(window, nq * dh, generator=g).to(dtype)
+    kc = torch.randn(prefix + window, nkv * dh, generator=g).to(dtype)
+    vc = torch.randn(prefix + window, nkv * dh, generator=g).to(dtype)
+    lay = _WindowLayout(prefix, window, tiled, DEV)
+    q_all = torch.zeros(lay.q_rows, nq * dh, dtype=dtype, device=DEV)
+    q_all[lay.q_off:] = q.to(DEV)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    o_all = torch.empty_like(q_all)
+    lse = torch.empty(nq, lay.q_rows, dtype=torch.float32, device=DEV)
+    shift = lay.base * nkv * dh * kd.element_size()
+    _lib.call("alodlm_attention_fwd", _lib.ptr(q_all), _lib.ptr(kd) + shift, _lib.ptr(vd) + shift,
+              nkv * dh, _lib.ptr(lay.bounds), _lib.ptr(lay.row_segment), _lib.ptr(lay.tiles),
+              0 if lay.tiles is None else lay.tiles.shape[0], _lib.ptr(o_all), _lib.ptr(lse),
+              lay.q_rows, nq, nkv, dh, 4, _lib.dtype_code(dtype), _lib.stream_handle(DEV))
+    torch.cuda.synchronize()
+    qf = q.float().view(window, nq, dh)
+    kf = kc.float().view(-1, nkv, dh).repeat_interleave(nq // nkv, 1)
+    vf = vc.float().view(-1, nkv, dh).repeat_interleave(nq // nkv, 1)
+    s = torch.einsum("qhd,khd->hqk", qf, kf) / math.sqrt(dh)
+    allowed = torch.arange(prefix + window)[None, :] <= prefix + torch.arange(window)[:, None]
+    s = s.masked_fill(~allowed, float("-inf"))
+    ref = torch.einsum("hqk,khd->qhd", s.softmax(-1), vf).reshape(window, nq * dh)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(o_all[lay.q_off:].float().cpu(), ref, atol=tol, rtol=tol)
+
+
+def test_generation_is_request_independent_and_respects_budget():
+    """tests/test_inference.py:31-42."""
+    from alodlm_amd.inference import DecodeConfig, Decoder
+    decoder = Decoder(base_model(), tokenizer())
+    cfg = DecodeConfig(q=.5, tau=.1, max_new_tokens=8, window_size=4)
+    first = decoder.generate([4, 7, 9], cfg)
+    decoder.generate([4, 7, 10, 11], DecodeConfig(q=.9, max_new_tokens=7, mode="left1"))
+    second = decoder.generate([4, 7, 9], cfg)
+    assert first["token_ids"] == second["token_ids"]
+    assert first["exit_depths"] == second["exit_depths"]
+    assert first["generated_tokens"] <= 8
+    assert len(first["exit_depths"]) == len(first["token_ids"])
+
+
+def test_q_controls_executed_recurrence():
+    """tests/test_inference.py:44-49."""
+    from alodlm_amd.inference import DecodeConfig, Decoder
+    decoder = Decoder(base_model(), tokenizer())
+    shallow = decoder.generate([4, 7, 9], DecodeConfig(q=0, tau=0, max_new_tokens=6, window_size=4))
+    deep = decoder.generate([4, 7, 9], DecodeConfig(q=1, tau=0, max_new_tokens=6, window_size=4))
+    assert shallow["recurrent_passes"] == shallow["outer_steps"]
+    assert deep["recurrent_passes"] == 4 * deep["outer_steps"]
+
+
+def _cache_matches_fresh_prefill(model, prompt, cfg, atol, rtol):
+    """With one recurrent pass the cache after decoding holds the K/V a fresh
+    prefill of the same tokens computes (tests/test_inference.py:51-84)."""
+    from alodlm_amd.inference import Decoder, PrefixCache
+    decoder = Decoder(model, tokenizer())
+    caches = []
+    inner = decoder._window
+
+    def recording(ids, positions, cache, mask_rows, config, logical):
+        caches.append(cache)
+        return inner(ids, positions, cache, mask_rows, config, logical)
+
+    decoder._window = recording
+    out = decoder.generate(prompt, cfg)
+    decoder._window = inner
+    cache = caches[-1]
+    tokens = torch.tensor(list(prompt) + out["token_ids"], device=DEV)[:cache.length]
+    fresh = PrefixCache(model.config)
+    empty = torch.empty(0, dtype=torch.long, device=DEV)
+    with torch.inference_mode():
+        window = decoder._window(tokens, torch.arange(len(tokens), device=DEV), fresh, empty, cfg,
+                                 empty)[0]
+        fresh.append(window, torch.arange(len(tokens), device=DEV))
+    assert sorted(fresh.values) == sorted(cache.values)
+    for key in cache.values:
+        for actual, expected in zip(cache.values[key], fresh.values[key]):
+            torch.testing.assert_close(actual.float(), expected.float(), atol=atol, rtol=rtol)
+    return out
+
+
+def test_prefix_cache_matches_observed_token_forward():
+    from alodlm_amd.inference import DecodeConfig
+    model = base_model()
+    model.config.max_depth = 1  # after construction, as tests/test_inference.py:55 does
+    out = _cache_matches_fresh_prefill(
+        model, [4, 7, 9], DecodeConfig(q=0, mode="left1", max_new_tokens=8, window_size=4),
+        1e-6, 1e-5)
+    assert out["generated_tokens"] == 8
+
+
+def test_bf16_head_dim_128_cache_matches_fresh_prefill():
+    """The MFMA attention layout inside a real decode: a bf16 model with
+    head_dim 128, a 150-token prompt (prefix rows past one 128-row tile)."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    from alodlm_amd.config import ModelConfig
+    from alodlm_amd.inference import DecodeConfig
+    from alodlm_amd.model import ALoDLM
+    torch.manual_seed(0)
+    backbone = Qwen3ForCausalLM(Qwen3Config(
+        hidden_size=256, intermediate_size=512, num_hidden_layers=3, num_attention_heads=2,
+        num_key_value_heads=1, head_dim=128, vocab_size=64, max_position_embeddings=512,
+        bos_token_id=1, eos_token_id=2, pad_token_id=0, tie_word_embeddings=False)).to(torch.bfloat16)
+    model = ALoDLM(backbone, ModelConfig(loop_start=1, loop_end=2, mask_token_id=3,
+                                         block_size=4)).to(DEV)
+    model.config.max_depth = 1
+    prompt = [5 + (i * 7) % 50 for i in range(150)]
+    out = _cache_matches_fresh_prefill(
+        model, prompt, DecodeConfig(q=0, mode="left1", max_new_tokens=20, window_size=8),
+        3e-2, 3e-2)
+    assert out["generated_tokens"] == 20
+
+
+def test_invalid_decode_config_and_context_fail():
+    """tests/test_inference.py:115-122."""
+    from alodlm_amd.inference import DecodeConfig, Decoder
+    decoder = Decoder(base_model(), tokenizer())
+    for cfg in (DecodeConfig(q=1.1), DecodeConfig(tau=float("nan")), DecodeConfig(window_size=0)):
+        with pytest.raises(ValueError):
+            decoder.generate([4, 7], cfg)
+    with pytest.raises(ValueError):
+        decoder.generate([4] * 100, DecodeConfig(max_new_tokens=40))
+    with pytest.raises(ValueError):
+        decoder.generate([], DecodeConfig())
+    with pytest.raises(ValueError):
+        decoder.generate([4, 64], DecodeConfig(max_new_tokens=4))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,vocab", [(7, 1000), (3, 64), (2, 151936)])
+def test_decode_readout(dtype, rows, vocab):
+    """argmax (first of equal maxima, as torch.argmax) and the entropy of
+    log_softmax(logits.float()) (alodlm/inference.py:115-118); the logits are
+    left unchanged."""
+    from alodlm_amd import _lib
+    _lib.load()
+    g = torch.Generator().manual_seed(rows * vocab)
+    logits = (3 * torch.randn(rows, vocab, generator=g)).to(dtype)
+    logits[0, vocab // 3] = logits[0, 2 * vocab // 3] = logits[0].max() + 1  # tie: first wins
+    if rows > 2:
+        logits[2] = 0.5  # all equal: index 0, entropy log(V)
+    dev = logits.to(DEV)
+    before = dev.clone()
+    idx = torch.empty(rows, dtype=torch.int64, device=DEV)
+    ent = torch.empty(rows, dtype=torch.float32, device=DEV)
+    _lib.call("alodlm_decode_readout", _lib.ptr(dev), rows, vocab, _lib.ptr(idx), _lib.ptr(ent),
+              _lib.dtype_code(dtype), _lib.stream_handle(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(dev, before)
+    assert idx.cpu().tolist() == logits.float().argmax(-1).tolist()
+    logp = logits.double().log_softmax(-1)
+    ref = -(logp.exp() * logp).sum(-1)
+    torch.testing.assert_close(ent.cpu().double(), ref, atol=1e-4, rtol=1e-5)
+    if rows > 2:
+        assert abs(float(ent[2]) - math.log(vocab)) < 1e-4
