@@ -24,7 +24,26 @@ grad_sumsq_kernel(const void* const* __restrict__ grads, const int32_t* __restri
   const int64_t beg = chunk_start[c];
   const int64_t end = beg + chunk_size < numels[t] ? beg + chunk_size : numels[t];
   float s = 0.f;
-  for (int64_t i = beg + threadIdx.x; i < end; i += OPT_THREADS) {
+  int64_t i = beg;
+  if ((reinterpret_cast<uintptr_t>(g + beg) & 15) == 0) {
+    // 16-byte pieces while whole ones remain (the test is uniform per block)
+    const int64_t vec_end = beg + (end - beg) / (16 / sizeof(T)) * (16 / sizeof(T));
+    if constexpr (sizeof(T) == 2) {
+      for (int64_t j = beg + threadIdx.x * 8; j < vec_end; j += OPT_THREADS * 8) {
+        float v[8];
+        Vec8<T>::load(g + j, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e] * v[e];
+      }
+    } else {
+      for (int64_t j = beg + threadIdx.x * 4; j < vec_end; j += OPT_THREADS * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(g + j);
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+    }
+    i = vec_end;
+  }
+  for (i += threadIdx.x; i < end; i += OPT_THREADS) {
     const float v = Elem<T>::load(g, i);
     s += v * v;
   }

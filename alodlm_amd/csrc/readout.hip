@@ -261,24 +261,38 @@ __global__ void scatter_ce_kernel(const float* __restrict__ ce, const int32_t* _
 }
 
 // partial[blk, 0:H] = sum_r dgate[r]*readout[r]; partial[blk, H] = sum_r dgate[r]
-template <typename T>
-__global__ void __launch_bounds__(64)
+// over the block's kGateBwdRows rows.  grid.y walks row blocks, grid.x column
+// chunks of 8 * 256; each thread keeps 8 column sums in registers and reads
+// 16-byte row pieces (rows whose dgate is 0, the unmasked ones, are skipped:
+// the test is uniform across the block).
+template <typename T, bool V8>
+__global__ void __launch_bounds__(256)
 gate_bwd_kernel(const float* __restrict__ dgate, const T* __restrict__ readout,
                 float* __restrict__ partial, int64_t rows, int64_t H, int64_t rows_per_block) {
-  extern __shared__ float acc[];
-  const int lane = threadIdx.x;
-  for (int64_t c = lane; c <= H; c += 64) acc[c] = 0.f;
-  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  constexpr int W = V8 ? 8 : 1;
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * W;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
   const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float gsum = 0.f;
   for (int64_t r = r0; r < r1; ++r) {
     const float g = dgate[r];
     if (g == 0.f) continue;
     gsum += g;
-    for (int64_t c = lane; c < H; c += 64) acc[c] += g * Elem<T>::load(readout + r * H, c);
+    if (c < H) {
+      float v[8];
+      if (V8) Vec8<T>::load(readout + r * H + c, v);
+      else v[0] = Elem<T>::load(readout, r * H + c);
+#pragma unroll
+      for (int e = 0; e < W; ++e) acc[e] += g * v[e];
+    }
   }
-  for (int64_t c = lane; c < H; c += 64) partial[(int64_t)blockIdx.x * (H + 1) + c] = acc[c];
-  if (lane == 0) partial[(int64_t)blockIdx.x * (H + 1) + H] = gsum;
+  float* out = partial + (int64_t)blockIdx.y * (H + 1);
+  if (c < H) {
+#pragma unroll
+    for (int e = 0; e < W; ++e) out[c + e] = acc[e];
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) out[H] = gsum;
 }
 
 __global__ void gate_bwd_reduce_kernel(const float* __restrict__ partial, int64_t nparts, int64_t H,
@@ -293,7 +307,7 @@ __global__ void gate_bwd_reduce_kernel(const float* __restrict__ partial, int64_
   else { gb[0] += s; gdb[0] += s; }
 }
 
-static const int64_t kGateBwdRows = 256;
+static const int64_t kGateBwdRows = 64;
 
 extern "C" int alodlm_final_norm_gate(const void* x, const void* wf, const void* gate_w,
                                       const void* gate_b, const void* depth_bias, int64_t depth,
@@ -486,12 +500,17 @@ extern "C" int alodlm_gate_bwd(const float* dgate, const void* readout, float sc
                                int64_t rows, int64_t hidden, float* workspace, int dtype,
                                void* stream) {
   ALODLM_CHECK_ARG(rows > 0 && hidden > 0, "gate_bwd: bad shape");
-  ALODLM_CHECK_ARG((hidden + 1) * 4 <= 64 * 1024, "gate_bwd: hidden too large");
   const int64_t nparts = (rows + kGateBwdRows - 1) / kGateBwdRows;
+  ALODLM_CHECK_ARG(nparts <= 65535, "gate_bwd: too many rows");
   hipStream_t st = as_stream(stream);
+  const bool v8 = hidden % 8 == 0 && aligned8(readout, dtype);
   ALODLM_DISPATCH(dtype, T, {
-    gate_bwd_kernel<T><<<(unsigned)nparts, 64, (hidden + 1) * sizeof(float), st>>>(
-        dgate, (const T*)readout, workspace, rows, hidden, kGateBwdRows);
+    if (v8)
+      gate_bwd_kernel<T, true><<<dim3(ceil_div_u(hidden, 8 * 256), (unsigned)nparts), 256, 0, st>>>(
+          dgate, (const T*)readout, workspace, rows, hidden, kGateBwdRows);
+    else
+      gate_bwd_kernel<T, false><<<dim3(ceil_div_u(hidden, 256), (unsigned)nparts), 256, 0, st>>>(
+          dgate, (const T*)readout, workspace, rows, hidden, kGateBwdRows);
   });
   ALODLM_CHECK_LAUNCH("gate_bwd");
   gate_bwd_reduce_kernel<<<ceil_div_u(hidden + 1, 256), 256, 0, st>>>(

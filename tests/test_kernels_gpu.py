@@ -107,7 +107,7 @@ def test_gemm_splitk_accumulates_large_k():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (70, 130), (64, 64), (4096, 2048), (2048, 6144),
-                                       (1000, 33)])
+                                       (1000, 33), (72, 136), (8, 4096)])
 def test_transpose(dtype, rows, cols):
     """Weight transposes (exact: a permutation of the elements)."""
     L = lib()
@@ -472,3 +472,71 @@ def test_attention_fa128_large_packs_against_torch_fp32(seg_len, n_seg):
             e = ((got.float() - want).abs().max() / want.abs().max()).item()
             errs[name] = max(errs.get(name, 0.0), e)
     assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,offset,scaled", [(1003, 0, True), (1003, 1, False), (64, 0, False),
+                                             (100000, 0, True)])
+def test_cast_tail_and_alignment(dtype, n, offset, scaled):
+    """float32 -> dtype cast, with and without the device scale, over lengths
+    that leave a tail after the 8-wide pieces and over unaligned buffers."""
+    L = lib()
+    log(f"cast n={n} offset={offset} scaled={scaled} {dtype}")
+    g = torch.Generator().manual_seed(n + offset)
+    src_all = torch.randn(n + offset, generator=g).to(DEV)
+    dst_all = torch.zeros(n + offset, dtype=dtype, device=DEV)
+    src, dst = src_all[offset:], dst_all[offset:]
+    seed = torch.tensor([-0.75], dtype=torch.float32, device=DEV) if scaled else None
+    L.call("alodlm_cast_f32", L.ptr(src), L.ptr(seed), L.ptr(dst), n, L.dtype_code(dtype), st())
+    torch.cuda.synchronize()
+    want = (src * -0.75 if scaled else src).to(dtype)
+    assert torch.equal(dst.cpu(), want.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_grad_norm_chunks(dtype):
+    """Global L2 norm over a tensor list whose sizes leave ragged chunk tails
+    (torch.nn.utils.clip_grad_norm_'s total norm)."""
+    from alodlm_amd.optim import CHUNK, _Table
+    L = lib()
+    g = torch.Generator().manual_seed(3)
+    sizes = [1, 7, CHUNK + 3, 2 * CHUNK, 200001]
+    tensors = [torch.randn(s, generator=g).to(dtype).to(DEV) for s in sizes]
+    table = _Table(tensors, DEV)
+    ptrs = _Table.pointers(tensors, DEV)
+    partial = torch.empty(table.n_chunks, dtype=torch.float32, device=DEV)
+    total = torch.empty(1, dtype=torch.float32, device=DEV)
+    L.call("alodlm_grad_norm", L.ptr(ptrs), L.ptr(table.chunk_tensor), L.ptr(table.chunk_start),
+           L.ptr(table.numels), table.n_chunks, CHUNK, L.dtype_code(dtype), L.ptr(partial),
+           L.ptr(total), st())
+    torch.cuda.synchronize()
+    want = torch.cat([t.double().cpu() for t in tensors]).norm().item()
+    assert abs(float(total) - want) <= 1e-5 * want
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,hidden", [(100, 32), (5000, 256), (4096, 4096), (300, 100)])
+def test_gate_bwd(dtype, rows, hidden):
+    """Gate head backward: gw += scale * sum_r dgate[r] * readout[r],
+    gb and depth_bias[depth] += scale * sum_r dgate[r] (alodlm/model.py:22-38);
+    rows with dgate 0 contribute nothing."""
+    L = lib()
+    log(f"gate_bwd rows={rows} hidden={hidden} {dtype}")
+    g = torch.Generator().manual_seed(rows + hidden)
+    dgate = torch.randn(rows, generator=g)
+    dgate[torch.rand(rows, generator=g) < 0.5] = 0.0
+    readout = torch.randn(rows, hidden, generator=g).to(dtype)
+    gw = torch.full((hidden,), 0.5, device=DEV)
+    gb = torch.full((1,), 0.25, device=DEV)
+    gdb = torch.zeros(4, device=DEV)
+    ws = torch.empty(L.query("alodlm_gate_bwd_workspace", rows, hidden), dtype=torch.float32,
+                     device=DEV)
+    dg, ro = dgate.to(DEV), readout.to(DEV)
+    L.call("alodlm_gate_bwd", L.ptr(dg), L.ptr(ro), 0.5, L.ptr(gw), L.ptr(gb), L.ptr(gdb), 2,
+           rows, hidden, L.ptr(ws), L.dtype_code(dtype), st())
+    torch.cuda.synchronize()
+    want_w = 0.5 + 0.5 * (dgate.double()[:, None] * readout.double()).sum(0)
+    want_b = 0.5 * dgate.double().sum()
+    torch.testing.assert_close(gw.cpu().double(), want_w, atol=1e-4, rtol=1e-5)
+    assert abs(float(gb) - (0.25 + want_b)) < 1e-4
+    assert abs(float(gdb[2]) - want_b) < 1e-4 and float(gdb[0]) == 0.0
