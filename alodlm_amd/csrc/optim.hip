@@ -82,14 +82,60 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   float* v = exp_avg_sq[t];
   const T* g = reinterpret_cast<const T*>(grads[t]);
   const bool separate = reinterpret_cast<void*>(w) != reinterpret_cast<void*>(p);
-  for (int64_t i = beg + threadIdx.x; i < end; i += OPT_THREADS) {
-    const float gi = Elem<T>::load(g, i) * clip;
-    float wi = w[i] * decay;
-    float mi = m[i];
+  auto update = [&](float gi, float& wi, float& mi, float& vi) {
+    gi *= clip;
+    wi *= decay;
     mi = mi + (1.0f - beta1) * (gi - mi);
-    float vi = v[i] * beta2 + (1.0f - beta2) * gi * gi;
+    vi = vi * beta2 + (1.0f - beta2) * gi * gi;
     const float denom = sqrtf(vi) / bc2_sqrt + eps;
     wi = wi - step_size * (mi / denom);
+  };
+  int64_t i = beg;
+  // float32 state 16-byte aligned; 4 gradient / parameter elements are 16
+  // bytes (float) or 8 bytes (bf16)
+  constexpr uintptr_t half = sizeof(T) == 2 ? 2 : 1;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(w + beg) | reinterpret_cast<uintptr_t>(m + beg) |
+                          reinterpret_cast<uintptr_t>(v + beg) |
+                          reinterpret_cast<uintptr_t>(g + beg) * half |
+                          (separate ? reinterpret_cast<uintptr_t>(p + beg) * half : 0);
+  if ((align & 15) == 0) {
+    // 4 elements per thread and step: 16-byte float32 state, 4 * sizeof(T)
+    // bytes of gradient and parameter (the same arithmetic per element)
+    const int64_t vec_end = beg + (end - beg) / 4 * 4;
+    for (int64_t j = beg + threadIdx.x * 4; j < vec_end; j += OPT_THREADS * 4) {
+      float4 w4 = *reinterpret_cast<const float4*>(w + j);
+      float4 m4 = *reinterpret_cast<const float4*>(m + j);
+      float4 v4 = *reinterpret_cast<const float4*>(v + j);
+      float gv[4], wv[4] = {w4.x, w4.y, w4.z, w4.w}, mv[4] = {m4.x, m4.y, m4.z, m4.w},
+                   vv[4] = {v4.x, v4.y, v4.z, v4.w};
+      if constexpr (sizeof(T) == 2) {
+        const uint2 gr = *reinterpret_cast<const uint2*>(g + j);
+        gv[0] = bf16_to_float((bf16_t)(gr.x & 0xffff)); gv[1] = bf16_to_float((bf16_t)(gr.x >> 16));
+        gv[2] = bf16_to_float((bf16_t)(gr.y & 0xffff)); gv[3] = bf16_to_float((bf16_t)(gr.y >> 16));
+      } else {
+        const float4 g4 = *reinterpret_cast<const float4*>(g + j);
+        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) update(gv[e], wv[e], mv[e], vv[e]);
+      *reinterpret_cast<float4*>(m + j) = make_float4(mv[0], mv[1], mv[2], mv[3]);
+      *reinterpret_cast<float4*>(v + j) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      *reinterpret_cast<float4*>(w + j) = make_float4(wv[0], wv[1], wv[2], wv[3]);
+      if (separate) {
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<uint2*>(p + j) =
+              make_uint2((uint32_t)float_to_bf16(wv[0]) | ((uint32_t)float_to_bf16(wv[1]) << 16),
+                         (uint32_t)float_to_bf16(wv[2]) | ((uint32_t)float_to_bf16(wv[3]) << 16));
+        } else {
+          *reinterpret_cast<float4*>(p + j) = make_float4(wv[0], wv[1], wv[2], wv[3]);
+        }
+      }
+    }
+    i = vec_end;
+  }
+  for (i += threadIdx.x; i < end; i += OPT_THREADS) {
+    float wi = w[i], mi = m[i], vi = v[i];
+    update(Elem<T>::load(g, i), wi, mi, vi);
     m[i] = mi;
     v[i] = vi;
     w[i] = wi;
