@@ -11,3 +11,13 @@
 // `partial`.
 int column_reduce(const float* partial, int64_t nparts, int64_t ld, int64_t col0, int64_t ncols,
                   float* out, float* tmp, hipStream_t st);
+
+// Rows per block of the backward kernels that write one partial row of
+// weight-gradient sums per block: 32 for large row counts, fewer (a multiple
+// of 4, at least 4) so that about 512 blocks keep every CU busy when rows are
+// few (the 8B step's 4096-row packs).
+static inline int64_t bwd_rows_per_block(int64_t rows) {
+  int64_t r = (rows + 511) / 512;
+  r = (r + 3) / 4 * 4;
+  return r < 4 ? 4 : (r > 32 ? 32 : r);
+}

@@ -112,14 +112,14 @@ rmsnorm_fwd_vec_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __re
 // dy = 0 (their output was replaced by a re-embedded token,
 // alodlm/model.py:153-154): dx = dres.
 // ---------------------------------------------------------------------------
-#define BWD_ROWS_PER_BLOCK 32
 
 template <typename T, int NCH>
 __global__ void __launch_bounds__(64 * NORM_WAVES)
 rmsnorm_bwd_vec_kernel(const T* __restrict__ dy, const T* __restrict__ x,
                        const float* __restrict__ rstd, const T* __restrict__ w, const T* dres,
                        T* dx, float* __restrict__ partial, int64_t rows, int64_t cols,
-                       const int32_t* __restrict__ skip_exits, int64_t skip_depth) {
+                       const int32_t* __restrict__ skip_exits, int64_t skip_depth,
+                       int64_t rows_per_block) {
   extern __shared__ float lds[];  // [NORM_WAVES][cols]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc[NCH][8];
@@ -131,8 +131,8 @@ rmsnorm_bwd_vec_kernel(const T* __restrict__ dy, const T* __restrict__ x,
     for (int i = 0; i < 8; ++i) acc[t][i] = 0.f;
     if (c < cols) Vec8<T>::load(w + c, wv[t]);
   }
-  const int64_t r0 = (int64_t)blockIdx.x * BWD_ROWS_PER_BLOCK;
-  for (int64_t row = r0 + wave; row < r0 + BWD_ROWS_PER_BLOCK && row < rows; row += NORM_WAVES) {
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += NORM_WAVES) {
     const bool skip = skip_exits && skip_exits[row] <= skip_depth;
     const float r = rstd[row];
     float a[NCH][8], b[NCH][8];
@@ -200,7 +200,8 @@ __global__ void __launch_bounds__(64 * NORM_WAVES)
 rmsnorm_bwd_bf16_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
                         const float* __restrict__ rstd, const bf16_t* __restrict__ w,
                         const bf16_t* dres, bf16_t* dx, float* __restrict__ partial, int64_t rows,
-                        int64_t cols, const int32_t* __restrict__ skip_exits, int64_t skip_depth) {
+                        int64_t cols, const int32_t* __restrict__ skip_exits, int64_t skip_depth,
+                        int64_t rows_per_block) {
   extern __shared__ float lds[];  // [NORM_WAVES][cols]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc[NCH][8];
@@ -212,8 +213,8 @@ rmsnorm_bwd_bf16_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict_
     for (int i = 0; i < 8; ++i) acc[t][i] = 0.f;
     if (c < cols) wr[t] = *reinterpret_cast<const uint4*>(w + c);
   }
-  const int64_t r0 = (int64_t)blockIdx.x * BWD_ROWS_PER_BLOCK;
-  for (int64_t row = r0 + wave; row < r0 + BWD_ROWS_PER_BLOCK && row < rows; row += NORM_WAVES) {
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += NORM_WAVES) {
     const bool skip = skip_exits && skip_exits[row] <= skip_depth;
     const float r = rstd[row];
     uint4 ar[NCH], br[NCH];
@@ -283,12 +284,13 @@ __global__ void __launch_bounds__(64)
 rmsnorm_bwd_scalar_kernel(const T* __restrict__ dy, const T* __restrict__ x,
                           const float* __restrict__ rstd, const T* __restrict__ w, const T* dres,
                           T* dx, float* __restrict__ partial, int64_t rows, int64_t cols,
-                          const int32_t* __restrict__ skip_exits, int64_t skip_depth) {
+                          const int32_t* __restrict__ skip_exits, int64_t skip_depth,
+                          int64_t rows_per_block) {
   extern __shared__ float dw_lds[];
   const int lane = threadIdx.x;
   for (int64_t c = lane; c < cols; c += 64) dw_lds[c] = 0.f;
-  const int64_t r0 = (int64_t)blockIdx.x * BWD_ROWS_PER_BLOCK;
-  const int64_t r1 = r0 + BWD_ROWS_PER_BLOCK < rows ? r0 + BWD_ROWS_PER_BLOCK : rows;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
   for (int64_t row = r0; row < r1; ++row) {
     const bool skip = skip_exits && skip_exits[row] <= skip_depth;
     const float r = rstd[row];
@@ -377,8 +379,12 @@ extern "C" int alodlm_rmsnorm_fwd(const void* x, const void* w, void* y, float* 
   const bool v8 = cols % 8 == 0 && aligned8(x, dtype) && aligned8(y, dtype) && aligned8(w, dtype);
   ALODLM_DISPATCH(dtype, T, {
     dim3 grid(ceil_div_u(rows, NORM_WAVES));
-    // register-resident rows: about 4 rows per wavefront, at most 8192 blocks
-    dim3 vgrid(ceil_div_u(rows, 4 * NORM_WAVES) < 8192 ? ceil_div_u(rows, 4 * NORM_WAVES) : 8192);
+    // register-resident rows: up to 4 rows per wavefront (the weight is read
+    // once per wavefront), but at least 2048 blocks while there are rows for
+    // them (one row per wavefront on small packs), at most 8192
+    const int64_t one_row = ceil_div_u(rows, NORM_WAVES), four_rows = ceil_div_u(rows, 4 * NORM_WAVES);
+    int64_t nblk = four_rows > 2048 ? four_rows : (one_row < 2048 ? one_row : 2048);
+    dim3 vgrid((unsigned)(nblk < 8192 ? nblk : 8192));
     hipStream_t st = as_stream(stream);
     if (v8 && cols <= 2048)
       rmsnorm_fwd_vec_kernel<T, 4><<<vgrid, 64 * NORM_WAVES, 0, st>>>(
@@ -397,7 +403,8 @@ extern "C" int alodlm_rmsnorm_fwd(const void* x, const void* w, void* y, float* 
 
 extern "C" int64_t alodlm_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
   // per-block partial rows, then the column reduction's group sums
-  return ((rows + BWD_ROWS_PER_BLOCK - 1) / BWD_ROWS_PER_BLOCK + COLUMN_REDUCE_MAX_GROUPS) * cols;
+  const int64_t rpb = bwd_rows_per_block(rows);
+  return ((rows + rpb - 1) / rpb + COLUMN_REDUCE_MAX_GROUPS) * cols;
 }
 
 static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, const void* w,
@@ -409,7 +416,8 @@ static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, 
   if (rows == 0) return ALODLM_OK;
   const bool v8 = cols % 8 == 0 && aligned8(x, dtype) && aligned8(dy, dtype) &&
                   aligned8(dx, dtype) && aligned8(w, dtype) && (!dres || aligned8(dres, dtype));
-  const int64_t nparts = (rows + BWD_ROWS_PER_BLOCK - 1) / BWD_ROWS_PER_BLOCK;
+  const int64_t rpb = bwd_rows_per_block(rows);
+  const int64_t nparts = (rows + rpb - 1) / rpb;
   const int64_t nch = (cols + 511) / 512;
   const size_t lds_bytes = (size_t)NORM_WAVES * cols * sizeof(float);
   if (dtype == ALODLM_BF16 && v8 && nch <= 8 && lds_bytes <= 128 * 1024) {
@@ -417,11 +425,11 @@ static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, 
     if (nch <= 4)
       rmsnorm_bwd_bf16_kernel<4><<<(unsigned)nparts, 64 * NORM_WAVES, lds_bytes, st>>>(
           dyb, xb, rstd, wb, (const bf16_t*)dres, (bf16_t*)dx, workspace, rows, cols, skip_exits,
-          skip_depth);
+          skip_depth, rpb);
     else
       rmsnorm_bwd_bf16_kernel<8><<<(unsigned)nparts, 64 * NORM_WAVES, lds_bytes, st>>>(
           dyb, xb, rstd, wb, (const bf16_t*)dres, (bf16_t*)dx, workspace, rows, cols, skip_exits,
-          skip_depth);
+          skip_depth, rpb);
     ALODLM_CHECK_LAUNCH("rmsnorm_bwd");
     if (dw_accum)
       return column_reduce(workspace, nparts, cols, 0, cols, dw_accum, workspace + nparts * cols, st);
@@ -432,19 +440,19 @@ static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, 
     if (v8 && nch <= 1)
       rmsnorm_bwd_vec_kernel<T, 1><<<(unsigned)nparts, 64 * NORM_WAVES, lds, st>>>(
           (const T*)dy, (const T*)x, rstd, (const T*)w, (const T*)dres, (T*)dx, workspace, rows,
-          cols, skip_exits, skip_depth);
+          cols, skip_exits, skip_depth, rpb);
     else if (v8 && nch <= 4)
       rmsnorm_bwd_vec_kernel<T, 4><<<(unsigned)nparts, 64 * NORM_WAVES, lds, st>>>(
           (const T*)dy, (const T*)x, rstd, (const T*)w, (const T*)dres, (T*)dx, workspace, rows,
-          cols, skip_exits, skip_depth);
+          cols, skip_exits, skip_depth, rpb);
     else if (v8 && nch <= 8 && lds <= 128 * 1024)
       rmsnorm_bwd_vec_kernel<T, 8><<<(unsigned)nparts, 64 * NORM_WAVES, lds, st>>>(
           (const T*)dy, (const T*)x, rstd, (const T*)w, (const T*)dres, (T*)dx, workspace, rows,
-          cols, skip_exits, skip_depth);
+          cols, skip_exits, skip_depth, rpb);
     else
       rmsnorm_bwd_scalar_kernel<T><<<(unsigned)nparts, 64, cols * sizeof(float), st>>>(
           (const T*)dy, (const T*)x, rstd, (const T*)w, (const T*)dres, (T*)dx, workspace, rows,
-          cols, skip_exits, skip_depth);
+          cols, skip_exits, skip_depth, rpb);
   });
   ALODLM_CHECK_LAUNCH("rmsnorm_bwd");
   if (dw_accum)

@@ -74,7 +74,6 @@ qknorm_rope_fwd_kernel(const T* __restrict__ qkv, const T* __restrict__ wq, cons
 // Backward: dt = rotary^T d(out), then the RMSNorm backward over dh.  Per-lane
 // norm-weight partials stay in registers; the block writes one partial row
 // [q grads (dh) | k grads (dh)].
-#define ROPE_BWD_ROWS 32
 
 template <typename T>
 __global__ void __launch_bounds__(64 * ROPE_WAVES)
@@ -82,7 +81,7 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
                        const T* __restrict__ wq, const T* __restrict__ wk,
                        const int64_t* __restrict__ positions, const float* __restrict__ inv_freq,
                        T* __restrict__ dqkv, float* __restrict__ partial, int64_t rows, int nq,
-                       int nkv, int dh, float eps) {
+                       int nkv, int dh, float eps, int64_t rows_per_block) {
   extern __shared__ float lds[];  // [ROPE_WAVES][2*dh]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = dh / 2;
@@ -99,8 +98,8 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
       wka[t] = Elem<T>::load(wk, i); wkb[t] = Elem<T>::load(wk, i + half);
     }
   }
-  const int64_t r0 = (int64_t)blockIdx.x * ROPE_BWD_ROWS;
-  for (int64_t row = r0 + wave; row < r0 + ROPE_BWD_ROWS && row < rows; row += ROPE_WAVES) {
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += ROPE_WAVES) {
     const float pos = (float)positions[row];
     float cs[ROPE_MAX_T], sn[ROPE_MAX_T];
 #pragma unroll
@@ -245,7 +244,8 @@ qknorm_rope128_bwd_kernel(const bf16_t* __restrict__ dq, const bf16_t* __restric
                           const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ wq,
                           const bf16_t* __restrict__ wk, const int64_t* __restrict__ positions,
                           const float* __restrict__ inv_freq, bf16_t* __restrict__ dqkv,
-                          float* __restrict__ partial, int64_t rows, int nq, int nkv, float eps) {
+                          float* __restrict__ partial, int64_t rows, int nq, int nkv, float eps,
+                          int64_t rows_per_block) {
   __shared__ float lds[ROPE_WAVES * 4][2 * 128];  // [wave*4 + slot][dwq | dwk]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane >> 4, j = lane & 15;
   const int i0 = 4 * j;
@@ -256,8 +256,8 @@ qknorm_rope128_bwd_kernel(const bf16_t* __restrict__ dq, const bf16_t* __restric
   float gka[4] = {0.f, 0.f, 0.f, 0.f}, gkb[4] = {0.f, 0.f, 0.f, 0.f};
   load4(wq + i0, wqa); load4(wq + i0 + 64, wqb);
   load4(wk + i0, wka); load4(wk + i0 + 64, wkb);
-  const int64_t r0 = (int64_t)blockIdx.x * ROPE_BWD_ROWS;
-  for (int64_t row = r0 + wave; row < r0 + ROPE_BWD_ROWS && row < rows; row += ROPE_WAVES) {
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += ROPE_WAVES) {
     const float pos = (float)positions[row];
     float cs[4], sn[4];
 #pragma unroll
@@ -363,7 +363,8 @@ extern "C" int64_t alodlm_qknorm_rope_bwd_workspace(int64_t rows, int64_t nq, in
                                                     int64_t dh) {
   (void)nq; (void)nkv;
   // per-block partial rows [dwq | dwk], then the column reduction's group sums
-  return ((rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS) * 2 * dh + COLUMN_REDUCE_MAX_GROUPS * dh;
+  const int64_t rpb = bwd_rows_per_block(rows);
+  return ((rows + rpb - 1) / rpb) * 2 * dh + COLUMN_REDUCE_MAX_GROUPS * dh;
 }
 
 extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv,
@@ -374,7 +375,8 @@ extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void
   int rc = check_rope(rows, nq, nkv, dh);
   if (rc) return rc;
   if (rows == 0) return ALODLM_OK;
-  const int64_t nparts = (rows + ROPE_BWD_ROWS - 1) / ROPE_BWD_ROWS;
+  const int64_t rpb = bwd_rows_per_block(rows);
+  const int64_t nparts = (rows + rpb - 1) / rpb;
   hipStream_t st = as_stream(stream);
   ALODLM_DISPATCH(dtype, T, {
     if (std::is_same<T, bf16_t>::value && dh == 128 && rope128_aligned(dq, dk, qkv) &&
@@ -382,13 +384,13 @@ extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void
       qknorm_rope128_bwd_kernel<<<(unsigned)nparts, 64 * ROPE_WAVES, 0, st>>>(
           (const bf16_t*)dq, (const bf16_t*)dk, (const bf16_t*)qkv, (const bf16_t*)wq,
           (const bf16_t*)wk, positions, inv_freq, (bf16_t*)dqkv, workspace, rows, (int)nq,
-          (int)nkv, eps);
+          (int)nkv, eps, rpb);
       break;
     }
     qknorm_rope_bwd_kernel<T><<<(unsigned)nparts, 64 * ROPE_WAVES,
                                 ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
         (const T*)dq, (const T*)dk, (const T*)qkv, (const T*)wq, (const T*)wk, positions,
-        inv_freq, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps);
+        inv_freq, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps, rpb);
   });
   ALODLM_CHECK_LAUNCH("qknorm_rope_bwd");
   float* tmp = workspace + nparts * 2 * dh;
