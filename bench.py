@@ -278,9 +278,9 @@ def main():
         "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 2), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": f"{spec['name']} full training step (fwd+bwd+clip+AdamW fp32 master)",
-                   "model": (f"{spec['qwen']} random init, untied, loop {spec['loop'][0]}-"
-                             f"{spec['loop'][1]}, max_depth 4"),
+        "config": {"workload": (f"{spec['name']} full training step (fwd+bwd+clip+AdamW fp32 "
+                                f"master): {spec['qwen']} shapes, random init, untied, loop "
+                                f"{spec['loop'][0]}-{spec['loop'][1]}, max_depth 4"),
                    "global_batch": len(seg_lengths), "seq_len": 2048,
                    "dual_stream_rows": 2 * tokens,
                    "parallelism": "none (1 GPU)"},
