@@ -17,8 +17,9 @@ inputs and outputs are stored, under ``tests/golden/workflow/``:
   seed 5).
 * ``train.json``: an ``alodlm.train.train`` run of the fixture configuration
   (fp32, 2 epochs capped at 4 steps, save every 2, log every step, seed 17)
-  and of its resumption from ``checkpoint-2``: the printed header, the pack
-  index each step consumed, every ``metrics.jsonl`` record, each
+  and of its resumption from ``checkpoint-2``, plus a run with gradient
+  accumulation over 2 packs and no step cap (2 epochs): the printed header,
+  the pack index each step consumed, every ``metrics.jsonl`` record, each
   checkpoint's ``trainer_state.json`` and file names.
 """
 
@@ -112,8 +113,10 @@ def main():
         PackedDataset.__getitem__ = recording_getitem
         result = {"config": {k: v for k, v in config.items()
                              if k not in ("model_dir", "train_file", "output_dir", "cache_file")}}
-        for name, resume in (("run", None), ("resumed", "run/checkpoint-2")):
-            cfg = dict(config, output_dir=str(root / name))
+        for name, resume, extra in (("run", None, {}), ("resumed", "run/checkpoint-2", {}),
+                                    ("accumulated", None,
+                                     {"gradient_accumulation_steps": 2, "max_steps": 0})):
+            cfg = dict(config, output_dir=str(root / name), **extra)
             if resume:
                 cfg["resume"] = str(root / resume)
             yaml_path = root / f"{name}.yaml"

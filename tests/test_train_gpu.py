@@ -148,3 +148,31 @@ def test_bf16_resume_is_exact_and_prunes(tmp_path):
     run_train(write_config(tmp_path, "pruned", precision="bf16", save_steps=1, max_steps=3,
                            save_total_limit=1))
     assert sorted(p.name for p in (tmp_path / "pruned").glob("checkpoint-*")) == ["checkpoint-3"]
+
+
+def test_gradient_accumulation_follows_reference_loop(tmp_path):
+    """Accumulation over 2 packs, 2 epochs of 5 packs (alodlm/train.py:50-54,
+    134-150): the horizon, the sync at the end of each epoch's loader (the odd
+    last pack steps alone), learning rates, and each checkpoint's step, epoch
+    and next batch equal the reference's.  The second epoch's order is not
+    compared: on the CPU the reference's masking draws advance the CPU
+    generator, on a GPU they use the device's."""
+    ref = RUN["accumulated"]
+    shutil.copy(FIXTURE / "training.jsonl", tmp_path / "training.jsonl")
+    consumed = []
+    print("[train] accumulation run", file=sys.stderr, flush=True)
+    steps = run_train(write_config(tmp_path, "acc", gradient_accumulation_steps=2, max_steps=0),
+                      consumed)
+    assert steps == ref["steps"] == 6
+    assert consumed[:5] == ref["consumed"][:5]
+    assert len(consumed) == 10
+    records = [json.loads(l) for l in (tmp_path / "acc" / "metrics.jsonl").read_text().splitlines()]
+    assert [r["step"] for r in records] == [r["step"] for r in ref["metrics"]]
+    for got, want in zip(records, ref["metrics"]):
+        assert got["learning_rate"] == pytest.approx(want["learning_rate"], rel=1e-12, abs=1e-18)
+    for name, want in ref["checkpoints"].items():
+        state = json.loads((tmp_path / "acc" / name / "trainer_state.json").read_text())
+        for key in ("step", "epoch", "next_batch", "identity"):
+            assert state[key] == want["trainer_state"][key], (name, key)
+    first = json.loads((tmp_path / "acc" / "checkpoint-2" / "trainer_state.json").read_text())
+    assert first["epoch_rng"] == ref["checkpoints"]["checkpoint-2"]["trainer_state"]["epoch_rng"]
