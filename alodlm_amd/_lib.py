@@ -24,6 +24,7 @@ EPI_STORE, EPI_RESIDUAL, EPI_ACCUM = 0, 1, 2
 # name -> argument types (every entry point returns int unless listed in _RESTYPE)
 SIGNATURES = {
     "alodlm_abi_version": [],
+    "alodlm_device_info": [I32, P, P],
     "alodlm_last_error": [],
     "alodlm_batch_build": [P, P, P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P],
     "alodlm_embed_gather": [P, P, P, I64, I64, I64, I32, P],

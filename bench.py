@@ -134,6 +134,18 @@ class KernelTimer:
         return out
 
 
+def device_info():
+    """Compute units and peak engine clock of cuda:0 as the HIP runtime reports
+    them, and the dense bf16 MFMA peak they imply (4096 FLOP per CU and clock);
+    the published 2516.6 TFLOP/s is what the roofline fractions use."""
+    import ctypes
+    from alodlm_amd import _lib
+    cus, khz = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.call("alodlm_device_info", 0, ctypes.addressof(cus), ctypes.addressof(khz))
+    return {"compute_units": cus.value, "max_clock_mhz": round(khz.value / 1000.0, 1),
+            "peak_bf16_tflops_from_clock": round(cus.value * 4096 * khz.value * 1e3 / 1e12, 1)}
+
+
 def gemm_bytes(A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=0, R=None, ldr=0):
     """Algorithmic HBM bytes of one GEMM launch: A and B read once (bf16), C
     written once (bf16 store), plus R read (residual) or the float32 C read and
@@ -284,6 +296,7 @@ def main():
                    "global_batch": len(seg_lengths), "seq_len": 2048,
                    "dual_stream_rows": 2 * tokens,
                    "parallelism": "none (1 GPU)"},
+        "device": device_info(),
         "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
         "step_tflop": round(step_f / 1e12, 1),
     }

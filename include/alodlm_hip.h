@@ -35,6 +35,10 @@ enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
 /* Library identity and errors. */
 int alodlm_abi_version(void);
 const char* alodlm_last_error(void);
+/* Compute units and peak engine clock (kHz) of a device, for the peak
+ * figures measurements are quoted against.  No counterpart in the reference
+ * (its benchmarks read them from the vendor tools). */
+int alodlm_device_info(int device, int64_t* compute_units, int64_t* max_clock_khz);
 
 /* ---------------------------------------------------------------------------
  * Dual-stream batch (alodlm/batch.py:34-85, build_batch).
