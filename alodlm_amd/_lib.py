@@ -15,6 +15,7 @@ ABI_VERSION = 1
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
+U64 = ctypes.c_uint64
 I32 = ctypes.c_int
 F32 = ctypes.c_float
 
@@ -26,6 +27,7 @@ SIGNATURES = {
     "alodlm_abi_version": [],
     "alodlm_device_info": [I32, P, P],
     "alodlm_last_error": [],
+    "alodlm_mask_draws": [U64, U64, P, I64, P, I64, I64, P, P, P, P, P, P, P, P],
     "alodlm_batch_build": [P, P, P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P],
     "alodlm_embed_gather": [P, P, P, I64, I64, I64, I32, P],
     "alodlm_embed_scatter_add": [P, P, P, I64, P, I64, I64, I64, I32, P],

@@ -1,16 +1,20 @@
 """Dual-stream masking (drop-in for alodlm/batch.py).
 
-``build_batch`` keeps the reference's random-number consumption exactly
+``build_batch`` keeps the reference's random numbers exactly
 (alodlm/batch.py:50-60: per segment one ``uniform_`` of ceil(L/B) floats, then
 one ``randperm`` per block whose masked count round(n*p) is nonzero, all from
-the default generator of the ids' device) and hands the draws to the HIP
-kernel ``alodlm_batch_build``, which writes every dual-stream row.  Masks and
-orders are therefore bit-identical to the reference's for the same generator
-state.  The attention mask is never materialised on the GPU: the attention
+the default generator of the ids' device).  The HIP entry point
+``alodlm_mask_draws`` evaluates that whole sequence from the generator's
+(seed, offset) in two launches, the generator is advanced past it, and
+``alodlm_batch_build`` writes every dual-stream row.  Masks and orders are
+therefore bit-identical to the reference's for the same generator state.  The attention mask is never materialised on the GPU: the attention
 kernels enumerate the closed-form mask from the segment boundaries.
 """
 
 from dataclasses import dataclass
+import ctypes
+import functools
+import math
 
 import numpy as np
 import torch
@@ -70,10 +74,8 @@ def _draw_stream(device):
     """Per-device side stream (default priority) for the masking draws.
 
     The draws read no device data, so they need not wait for the compute
-    stream: on a stream of their own, the host reads the per-segment mask
-    ratios back without draining the previous step's queued work.  The
-    generator's state advances on the host at launch time, so the values and
-    their order are the same as on the compute stream."""
+    stream: on a stream of their own, the host reads the generator's end
+    offset back without draining the previous step's queued work."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     stream = _DRAW_STREAMS.get(index)
     if stream is None:
@@ -91,48 +93,81 @@ def block_supervised_counts(labels_host, offsets, block_size):
     return out
 
 
-def full_block_counts(offsets, block_size):
-    """Per segment, the block widths: the candidate counts when every label
-    is supervised."""
-    out = []
-    for a, b in zip(offsets, offsets[1:]):
-        starts = np.arange(0, b - a, block_size)
-        out.append(np.minimum(block_size, (b - a) - starts).astype(np.int64))
-    return out
+_LOG_THRESHOLD_12 = math.log(0.9) * 12
+# torch's uniform_ gives element i the first draw of Philox subsequence i while
+# its grid (256-thread blocks, at most 8 per compute unit) covers every
+# element: 256 * 8 * 256 on a 256-CU device.
+MAX_SEGMENT_BLOCKS = 1 << 19
 
 
-def draw_masking(labels_host, offsets, block_size, device, generator=None):
-    """Draw the masking randomness in the reference's order.
-
-    Returns per-block arrays (p, count) on the host and the list of per-block
-    permutations (tensors on ``device``, or None where count is zero).  On a
-    GPU the draws are issued on the side stream of ``_draw_stream``; the
-    caller orders its own stream after that one before reading them.
-    """
-    device = torch.device(device)
-    counts = block_supervised_counts(labels_host, offsets, block_size)
-    if device.type == "cuda":
-        with torch.cuda.stream(_draw_stream(device)):
-            return _draw(counts, offsets, block_size, device, generator)
-    return _draw(counts, offsets, block_size, device, generator)
+@functools.lru_cache(maxsize=None)
+def key_bits(block_size):
+    """Key width torch.randperm(n) sorts on, for n = 0..block_size: the fewest
+    bits that keep the chance of any duplicate key under 10 % (the randperm
+    note of ATen/native/cuda/Randperm.cuh), evaluated in double precision as
+    torch's host code does."""
+    bits = [0]
+    for n in range(1, block_size + 1):
+        nd = float(n)
+        bits.append(min(64, math.ceil(math.log2(nd - (6 * nd * nd + 1) / _LOG_THRESHOLD_12))))
+    return np.asarray(bits, dtype=np.int32)
 
 
-def _draw(block_counts, offsets, block_size, device, generator):
-    """The draws of alodlm/batch.py:50-60 for given candidate counts n."""
-    probs, counts, perms = [], [], []
-    for (a, b), n in zip(zip(offsets, offsets[1:]), block_counts):
-        nblocks = (b - a + block_size - 1) // block_size
-        u = torch.empty(nblocks, device=device).uniform_(0, 1, generator=generator).clamp_min(1e-8)
-        # p as the reference reads it (a float32 value widened to float64) and
-        # round(n * p) rounded half to even in float64 like Python's round
-        p = u.cpu().numpy().astype(np.float64)
-        count = np.rint(n * p).astype(np.int64)
-        probs.extend(p.tolist())
-        counts.extend(count.tolist())
-        for blk in range(nblocks):
-            perms.append(torch.randperm(int(n[blk]), device=device, generator=generator)
-                         if count[blk] else None)
-    return np.asarray(probs, dtype=np.float32), np.asarray(counts, dtype=np.int32), perms
+def _device_draws(block_n, seg_block, block_size, device, generator):
+    """The draws of alodlm/batch.py:50-60 from the generator's current state,
+    by ``alodlm_mask_draws`` on the side stream; the generator is then
+    advanced past every random number the reference's calls would consume.
+
+    Returns device tensors (p, count, perm_offset, perms) for batch_build."""
+    if max(b - a for a, b in zip(seg_block, seg_block[1:])) > MAX_SEGMENT_BLOCKS:
+        raise ValueError(f"a segment of more than {MAX_SEGMENT_BLOCKS} masking blocks is "
+                         "not supported")
+    gen = _generator_of(device, generator)
+    seed, offset = gen.initial_seed(), gen.get_offset()
+    nblocks = len(block_n)
+    side = _draw_stream(device)
+    with torch.cuda.stream(side):
+        n_t = _to_device(block_n.astype(np.int32), device)
+        sb_t = _to_device(np.asarray(seg_block, dtype=np.int32), device)
+        bits_t = _to_device(key_bits(block_size), device)
+        p_t = torch.empty(nblocks, dtype=torch.float32, device=device)
+        c_t = torch.empty(nblocks, dtype=torch.int32, device=device)
+        bo_t = torch.empty(nblocks, dtype=torch.int64, device=device)
+        po_t = torch.empty(nblocks, dtype=torch.int64, device=device)
+        perms = torch.empty(nblocks * block_size, dtype=torch.int64, device=device)
+        end_t = torch.empty(1, dtype=torch.int64, device=device)
+        _lib.call("alodlm_mask_draws", ctypes.c_uint64(seed), ctypes.c_uint64(offset),
+                  _lib.ptr(sb_t), len(seg_block) - 1, _lib.ptr(n_t), nblocks, block_size,
+                  _lib.ptr(bits_t), _lib.ptr(p_t), _lib.ptr(c_t), _lib.ptr(bo_t), _lib.ptr(po_t),
+                  _lib.ptr(perms), _lib.ptr(end_t), _lib.stream_handle(device))
+        end_host = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        end_host.copy_(end_t, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(side)
+    done.synchronize()
+    gen.set_offset(int(end_host[0]))
+    main = torch.cuda.current_stream(device)
+    main.wait_stream(side)
+    for t in (p_t, c_t, po_t, perms):
+        t.record_stream(main)
+    return p_t, c_t, po_t, perms
+
+
+def _replayed_draws(draws, device):
+    """Device tensors of given (p, count, perms) per block."""
+    probs, counts, perms = draws
+    perm_offset = np.zeros(len(perms), dtype=np.int64)
+    chunks, total = [], 0
+    for i, perm in enumerate(perms):
+        perm_offset[i] = total
+        if perm is not None:
+            chunks.append(perm.to(device=device, dtype=torch.int64))
+            total += perm.numel()
+    perm_buf = (torch.cat(chunks) if chunks
+                else torch.zeros(1, dtype=torch.int64, device=device))
+    return (_to_device(np.asarray(probs, dtype=np.float32), device),
+            _to_device(np.asarray(counts, dtype=np.int32), device),
+            _to_device(perm_offset, device), perm_buf)
 
 
 def _generator_of(device, generator):
@@ -176,52 +211,19 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     for a, b in zip(offsets, offsets[1:]):
         seg_block.append(seg_block[-1] + (b - a + block_size - 1) // block_size)
     nblocks = seg_block[-1]
-    side = _draw_stream(device)
-    speculative = None
-    if draws is None:
-        # The draws depend on the labels only through the supervised count of
-        # every block.  Draw first assuming every label is supervised: this
-        # needs no labels on the host, so it overlaps the work still queued
-        # on the compute stream.  If the labels then show an unsupervised
-        # position, the generator is rewound and the draws are made again
-        # with the true counts; either way the consumed random numbers are
-        # exactly the reference's.
-        gen = _generator_of(device, generator)
-        state = gen.get_state()
-        assumed = full_block_counts(offsets, block_size)
-        with torch.cuda.stream(side):
-            speculative = _draw(assumed, offsets, block_size, device, generator)
     if labels_host is None:
         labels_host = labels.detach().cpu().numpy()
-    with torch.cuda.stream(side):
-        if draws is None:
-            actual = block_supervised_counts(labels_host, offsets, block_size)
-            if all(np.array_equal(x, y) for x, y in zip(actual, assumed)):
-                draws = speculative
-            else:
-                gen.set_state(state)
-                draws = _draw(actual, offsets, block_size, device, generator)
-        probs, counts, perms = draws
-        perm_offset = np.zeros(nblocks, dtype=np.int64)
-        chunks, total = [], 0
-        for i, perm in enumerate(perms):
-            perm_offset[i] = total
-            if perm is not None:
-                chunks.append(perm.to(device=device, dtype=torch.int64))
-                total += perm.numel()
-        perm_buf = (torch.cat(chunks) if chunks
-                    else torch.zeros(1, dtype=torch.int64, device=device))
-    main = torch.cuda.current_stream(device)
-    main.wait_stream(side)
-    perm_buf.record_stream(main)
+    if draws is None:
+        block_n = np.concatenate(block_supervised_counts(labels_host, offsets, block_size))
+        p_t, c_t, po_t, perm_buf = _device_draws(block_n, seg_block, block_size, device,
+                                                 generator)
+    else:
+        p_t, c_t, po_t, perm_buf = _replayed_draws(draws, device)
     ids = ids.to(torch.int64).contiguous()
     labels = labels.to(torch.int64).contiguous()
     n = 2 * len(ids)
     seg_t = _to_device(np.asarray(offsets, dtype=np.int64), device)
     seg_block_t = _to_device(np.asarray(seg_block, dtype=np.int32), device)
-    p_t = _to_device(probs, device)
-    c_t = _to_device(counts, device)
-    po_t = _to_device(perm_offset, device)
     out = {
         "ids": torch.empty(n, dtype=torch.int64, device=device),
         "original": torch.empty(n, dtype=torch.int64, device=device),

@@ -41,8 +41,28 @@ const char* alodlm_last_error(void);
 int alodlm_device_info(int device, int64_t* compute_units, int64_t* max_clock_khz);
 
 /* ---------------------------------------------------------------------------
+ * Masking draws (alodlm/batch.py:50-60): the values of the reference's
+ * per-segment `uniform_(0, 1).clamp_min(1e-8)` and per-masked-block
+ * `randperm(n_cand)` calls on a Philox device generator whose state on entry
+ * is (seed, offset), evaluated in two launches.  block_n[b] is block b's
+ * candidate count (labels != -100, 0..block_size); segment s owns blocks
+ * [seg_block[s], seg_block[s+1]).  key_bits[n] (n = 0..block_size) is the
+ * randperm sort-key width.  Writes block_p, block_count = round(n * p),
+ * block_offset (the generator offset of each block's randperm), perm_offset
+ * = b * block_size, perms (n_blocks * block_size int64; block b's randperm
+ * at perm_offset[b] when block_count[b] > 0) and *offset_out, the generator
+ * offset after every draw.  Replaces the per-block torch calls of
+ * alodlm/batch.py:50-60; the output feeds alodlm_batch_build.
+ * ------------------------------------------------------------------------ */
+int alodlm_mask_draws(uint64_t seed, uint64_t offset, const int32_t* seg_block,
+                      int64_t n_segments, const int32_t* block_n, int64_t n_blocks,
+                      int64_t block_size, const int32_t* key_bits, float* block_p,
+                      int32_t* block_count, uint64_t* block_offset, int64_t* perm_offset,
+                      int64_t* perms, uint64_t* offset_out, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Dual-stream batch (alodlm/batch.py:34-85, build_batch).
- * Given the host-drawn randomness (per-block mask probability `block_p`,
+ * Given the masking draws (per-block mask probability `block_p`,
  * per-block masked count `block_count` = round(n_candidates * p) and the
  * concatenated randperm draws `perms` with per-block offsets `perm_offset`),
  * writes the clean+noisy rows of every segment.  Segment s covers tokens

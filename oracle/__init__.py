@@ -25,6 +25,8 @@ Pinning (each function is checked by tests/test_oracle.py):
   * gate init: the uniform-mass known answer (test_gate.py:18-30).
   * AdamW / cosine schedule / clip: closed form of the first step and
     torch.optim.AdamW.
+  * masking draws on a Philox device generator (draws.py): the Random123
+    known-answer vectors, and torch's own device draws on a GPU.
 """
 
 from .step import *  # noqa: F401,F403

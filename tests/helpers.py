@@ -50,10 +50,30 @@ def make_model(dims, objective, params, device="cuda", dtype=torch.float32):
     return model.to(device)
 
 
+def draw_masking(labels_host, offsets, block_size, device, generator=None):
+    """The masking draws made the way alodlm/batch.py:50-60 makes them: per
+    segment one ``uniform_`` of the block ratios, then one ``randperm`` per
+    block whose masked count round(n * p) is nonzero.  Returns per-block
+    (p, count) host arrays and the permutations (None where count is 0)."""
+    from alodlm_amd.batch import block_supervised_counts
+    probs, counts, perms = [], [], []
+    for (a, b), n in zip(zip(offsets, offsets[1:]),
+                         block_supervised_counts(labels_host, offsets, block_size)):
+        nblocks = (b - a + block_size - 1) // block_size
+        u = torch.empty(nblocks, device=device).uniform_(0, 1, generator=generator).clamp_min(1e-8)
+        p = u.cpu().numpy().astype(np.float64)
+        count = np.array([round(int(k) * float(v)) for k, v in zip(n, p)], dtype=np.int64)
+        probs.extend(p.tolist())
+        counts.extend(count.tolist())
+        for blk in range(nblocks):
+            perms.append(torch.randperm(int(n[blk]), device=device, generator=generator)
+                         if count[blk] else None)
+    return np.asarray(probs, dtype=np.float32), np.asarray(counts, dtype=np.int32), perms
+
+
 def cpu_draws(labels, boundaries, block_size, seed, max_depth):
     """Masking draws and exit uniforms consumed from the CPU default generator
     in the reference's order (alodlm/batch.py:50-60, alodlm/model.py:166)."""
-    from alodlm_amd.batch import draw_masking
     torch.manual_seed(seed)
     labels_host = torch.as_tensor(labels).numpy()
     offsets = [int(v) for v in boundaries]

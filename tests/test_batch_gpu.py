@@ -1,12 +1,13 @@
-"""Batch building on the GPU generator: the speculative masking draws consume
-exactly the random numbers of the reference's order (alodlm/batch.py:50-60),
-whether or not every label is supervised."""
+"""Batch building on the GPU generator: the masking draws consume exactly the
+random numbers of the reference's order (alodlm/batch.py:50-60), whether or
+not every label is supervised, and give the same rows as those draws made by
+torch's own calls."""
 
 import numpy as np
 import pytest
 import torch
 
-from tests.helpers import log
+from tests.helpers import draw_masking, log
 
 pytestmark = pytest.mark.gpu
 
@@ -23,8 +24,7 @@ def _batch(labels, bounds, seed, draws=None):
 
 @pytest.mark.parametrize("unsupervised", [False, True])
 @pytest.mark.parametrize("bounds", [[0, 2048, 4096], [0, 100, 101, 333]])
-def test_speculative_draws_match_direct_draws(unsupervised, bounds):
-    from alodlm_amd.batch import draw_masking
+def test_device_draws_match_direct_draws(unsupervised, bounds):
     log(f"batch draws bounds={bounds} unsupervised={unsupervised}")
     g = torch.Generator().manual_seed(len(bounds))
     labels = torch.randint(0, 1000, (bounds[-1],), generator=g)
