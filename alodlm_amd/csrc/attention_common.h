@@ -34,7 +34,7 @@ __device__ __forceinline__ bf16x8_t load_split_frag(const bf16_t* p) {
 }
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)float_to_bf16(a) | ((uint32_t)float_to_bf16(b) << 16);
+  return pack_bf16x2(a, b);
 }
 
 // Elements [off, off + 8) of an accumulator as one bf16 MFMA operand.

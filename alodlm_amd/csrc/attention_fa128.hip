@@ -280,7 +280,10 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     }
   }
   delta_q += __shfl_xor(delta_q, 32, 64);
-  if (T.valid && half == 0) delta[(int64_t)h * N + base + T.qi] = delta_q;
+  if (T.valid && half == 0) {
+    delta[(int64_t)h * N + base + T.qi] = delta_q;
+    delta[(int64_t)(nq + h) * N + base + T.qi] = lse2;  // lse * log2(e) for the dK/dV pass
+  }
   f32x16_t acc[HD / 32];
 #pragma unroll
   for (int i = 0; i < HD / 32; ++i) acc[i] = zero16();
@@ -359,18 +362,19 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 }
 
 // ---------------------------------------------------------------------------
-// dV = P^T dO,  dK = scale * dS^T Q
+// dV = P^T dO,  dK = scale * dS^T Q.  lse2[h, r] = lse[h, r] * log2(e), as the
+// dQ pass writes it next to delta.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256, 2)
 fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
-                  const bf16_t* __restrict__ v, int64_t ldv, const float* __restrict__ lse,
+                  const bf16_t* __restrict__ v, int64_t ldv, const float* __restrict__ lse2,
                   const float* __restrict__ delta, const bf16_t* __restrict__ dout,
                   const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
                   int n_tiles, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv,
                   float* __restrict__ partial, int64_t N, int nq, int nkv, int B, float scale) {
   __shared__ __attribute__((aligned(1024))) char lds[2][2][QT * ROWB];  // [stage][Q | dO]
   __shared__ __attribute__((aligned(1024))) char lds_v[128 * ROWB];     // V of the key tile
-  __shared__ __attribute__((aligned(16))) float lds_ld[2][2 * QT];      // [stage][lse | delta]
+  __shared__ __attribute__((aligned(16))) float lds_ld[2][2 * QT];      // [stage][lse2 | delta]
   const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // One workgroup per (kv head, key tile) walking the group's query heads, or,
@@ -418,10 +422,10 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       dload4(lds[stg][0], r0, q + hh * HD, ldq, base + qq, gmax, lane);
       dload4(lds[stg][1], r0, dout + hh * HD, ldq, base + qq, gmax, lane);
     }
-    if (wave == 0) {  // lse (lanes 0-31) and delta (lanes 32-63) of the tile's rows
+    if (wave == 0) {  // lse2 (lanes 0-31) and delta (lanes 32-63) of the tile's rows
       int64_t row = base + qq + col;
       row = row < gmax ? row : gmax;
-      const float* src = (half ? delta : lse) + (int64_t)hh * N + row;
+      const float* src = (half ? delta : lse2) + (int64_t)hh * N + row;
       dma4_v(src, lds_addr(lds_ld[stg]));
     }
   };
@@ -466,7 +470,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int e = j * 4 + i;
-        float p = fast_exp2(fmaf(sacc[e], c, -lsv[i] * FA_LOG2E));
+        float p = fast_exp2(fmaf(sacc[e], c, -lsv[i]));
         if ((unsigned)(q_off + j * 8 + i) >= q_width) p = 0.f;
         sacc[e] = p;
         pacc[e] = p * (pacc[e] - dlv[i]);
@@ -553,8 +557,9 @@ static bool dkdv_head_split(int64_t n_tiles, int nq, int nkv) {
 }
 
 int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles) {
-  // delta [nq][N], then (head split) the float32 dK/dV partials [2][group][N][nkv*128]
-  const int64_t delta = N * nq;
+  // delta [nq][N], lse * log2(e) [nq][N], then (head split) the float32 dK/dV
+  // partials [2][group][N][nkv*128]
+  const int64_t delta = 2 * N * nq;
   return dkdv_head_split(n_tiles, nq, nkv) ? delta + 2 * N * (int64_t)nq * HD : delta;
 }
 int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
@@ -571,19 +576,21 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
                      bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
                      float scale, hipStream_t st) {
-  // the dQ pass writes delta, which the dK/dV pass reads (stream order)
+  // the dQ pass writes delta and lse * log2(e), which the dK/dV pass reads
+  // (stream order)
   fa128_dq_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
       q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale);
+  const float* lse2 = delta + N * nq;
   if (dkdv_head_split(n_tiles, nq, nkv)) {
-    float* partial = delta + N * nq;
+    float* partial = delta + 2 * N * nq;
     fa128_dkdv_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
-        q, k, v, ldv, lse, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, partial, N, nq,
-        nkv, B, scale);
+        q, k, v, ldv, lse2, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, partial, N,
+        nq, nkv, B, scale);
     fa128_dkdv_reduce_kernel<<<ceil_div_u(2 * N * nkv * HD / 8, 256), 256, 0, st>>>(
         partial, nq / nkv, N, nkv, dk, dv, lddv);
   } else {
     fa128_dkdv_kernel<<<dim3((unsigned)nkv, (unsigned)n_tiles), 256, 0, st>>>(
-        q, k, v, ldv, lse, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, nullptr, N,
+        q, k, v, ldv, lse2, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, nullptr, N,
         nq, nkv, B, scale);
   }
   ALODLM_CHECK_LAUNCH("attention_bwd_fa128");

@@ -29,6 +29,16 @@ __device__ __forceinline__ bf16_t float_to_bf16(float f) {
   return __builtin_bit_cast(bf16_t, (__bf16)f);
 }
 
+// Two floats rounded to nearest-even bf16, `lo` in the low half: one
+// v_cvt_pk_bf16_f32 with both sources (two scalar conversions OR-ed together
+// compile to two conversions plus the shift and the OR).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const f32x2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
+}
+
 // Round a float to the nearest bf16 value and return it as float.
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_float(float_to_bf16(f)); }
 
@@ -138,7 +148,7 @@ template <> struct Vec8<bf16_t> {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)float_to_bf16(v[2 * i]) | ((uint32_t)float_to_bf16(v[2 * i + 1]) << 16);
+      w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 };

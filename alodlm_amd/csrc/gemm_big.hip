@@ -289,8 +289,8 @@ gemm_big_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restr
         if (vec && n + 4 <= N) {
           if (EPI == ALODLM_EPI_STORE) {
             *reinterpret_cast<uint2*>(Cb + m * ldc + n) =
-                make_uint2((uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16),
-                           (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16));
+                make_uint2(pack_bf16x2(v[0], v[1]),
+                           pack_bf16x2(v[2], v[3]));
           } else if (EPI == ALODLM_EPI_RESIDUAL) {
             const uint2 r = *reinterpret_cast<const uint2*>(R + m * ldr + n);
             const float rv[4] = {bf16_to_float((bf16_t)(r.x & 0xffff)), bf16_to_float((bf16_t)(r.x >> 16)),
@@ -299,8 +299,8 @@ gemm_big_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restr
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = rv[e] + round_bf16(v[e]);
             *reinterpret_cast<uint2*>(Cb + m * ldc + n) =
-                make_uint2((uint32_t)float_to_bf16(o[0]) | ((uint32_t)float_to_bf16(o[1]) << 16),
-                           (uint32_t)float_to_bf16(o[2]) | ((uint32_t)float_to_bf16(o[3]) << 16));
+                make_uint2(pack_bf16x2(o[0], o[1]),
+                           pack_bf16x2(o[2], o[3]));
           } else if (P) {
             *reinterpret_cast<float4*>(P + m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
           } else {

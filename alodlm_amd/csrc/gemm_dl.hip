@@ -318,8 +318,8 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
             const int chunk = (wn * WN + j * 32) / 8 + jj;
             const f32x16_t& a = acc[i][j];
             *reinterpret_cast<uint2*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4) + half * 8) =
-                make_uint2((uint32_t)float_to_bf16(alpha * a[jj * 4]) | ((uint32_t)float_to_bf16(alpha * a[jj * 4 + 1]) << 16),
-                           (uint32_t)float_to_bf16(alpha * a[jj * 4 + 2]) | ((uint32_t)float_to_bf16(alpha * a[jj * 4 + 3]) << 16));
+                make_uint2(pack_bf16x2(alpha * a[jj * 4], alpha * a[jj * 4 + 1]),
+                           pack_bf16x2(alpha * a[jj * 4 + 2], alpha * a[jj * 4 + 3]));
           }
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -340,7 +340,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
             for (int e = 0; e < 4; ++e) {
               const float lo = bf16_to_float((bf16_t)(rv[e] & 0xffff)) + bf16_to_float((bf16_t)(wv[e] & 0xffff));
               const float hi = bf16_to_float((bf16_t)(rv[e] >> 16)) + bf16_to_float((bf16_t)(wv[e] >> 16));
-              ov[e] = (uint32_t)float_to_bf16(lo) | ((uint32_t)float_to_bf16(hi) << 16);
+              ov[e] = pack_bf16x2(lo, hi);
             }
             *reinterpret_cast<uint4*>(dst) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
           } else {
@@ -413,8 +413,8 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
         if (vec && n + 4 <= N) {
           if (EPI == ALODLM_EPI_STORE) {
             *reinterpret_cast<uint2*>(Cb + m * ldc + n) =
-                make_uint2((uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16),
-                           (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16));
+                make_uint2(pack_bf16x2(v[0], v[1]),
+                           pack_bf16x2(v[2], v[3]));
           } else if (EPI == ALODLM_EPI_RESIDUAL) {
             const uint2 r = *reinterpret_cast<const uint2*>(R + m * ldr + n);
             const float rv[4] = {bf16_to_float((bf16_t)(r.x & 0xffff)), bf16_to_float((bf16_t)(r.x >> 16)),
@@ -423,8 +423,8 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = rv[e] + round_bf16(v[e]);
             *reinterpret_cast<uint2*>(Cb + m * ldc + n) =
-                make_uint2((uint32_t)float_to_bf16(o[0]) | ((uint32_t)float_to_bf16(o[1]) << 16),
-                           (uint32_t)float_to_bf16(o[2]) | ((uint32_t)float_to_bf16(o[3]) << 16));
+                make_uint2(pack_bf16x2(o[0], o[1]),
+                           pack_bf16x2(o[2], o[3]));
           } else if (P) {
             *reinterpret_cast<float4*>(P + m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
           } else {

@@ -124,8 +124,8 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
       if (separate) {
         if constexpr (sizeof(T) == 2) {
           *reinterpret_cast<uint2*>(p + j) =
-              make_uint2((uint32_t)float_to_bf16(wv[0]) | ((uint32_t)float_to_bf16(wv[1]) << 16),
-                         (uint32_t)float_to_bf16(wv[2]) | ((uint32_t)float_to_bf16(wv[3]) << 16));
+              make_uint2(pack_bf16x2(wv[0], wv[1]),
+                         pack_bf16x2(wv[2], wv[3]));
         } else {
           *reinterpret_cast<float4*>(p + j) = make_float4(wv[0], wv[1], wv[2], wv[3]);
         }

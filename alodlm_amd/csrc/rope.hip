@@ -187,8 +187,8 @@ __device__ __forceinline__ void load4(const bf16_t* p, float* v) {
 }
 __device__ __forceinline__ void store4(bf16_t* p, const float* v) {
   *reinterpret_cast<uint2*>(p) =
-      make_uint2((uint32_t)float_to_bf16(v[0]) | ((uint32_t)float_to_bf16(v[1]) << 16),
-                 (uint32_t)float_to_bf16(v[2]) | ((uint32_t)float_to_bf16(v[3]) << 16));
+      make_uint2(pack_bf16x2(v[0], v[1]),
+                 pack_bf16x2(v[2], v[3]));
 }
 
 __global__ void __launch_bounds__(64 * ROPE_WAVES)
