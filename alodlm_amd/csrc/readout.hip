@@ -176,13 +176,17 @@ __global__ void scatter_rows_kernel(const T* __restrict__ src, const int32_t* __
   dst[(int64_t)sel[j] * H + c] = src[i];
 }
 
+#define CE_LOG2E 1.4426950408889634f
+
 // ce = lse - logit[target] (rounded like the reference's CE output),
-// entropy = lse - sum p*logit, logits <- coef*(softmax - onehot).
+// entropy = lse - sum p*logit, logits <- coef*(softmax - onehot).  float
+// logits keep expf throughout; bf16 logits take the exp2 path.
 template <typename T, bool V8>
 __global__ void __launch_bounds__(256)
 cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
                      const float* __restrict__ coef, const int32_t* __restrict__ n_rows,
                      int64_t V, float* __restrict__ ce, float* __restrict__ entropy) {
+  constexpr bool FAST = sizeof(T) == 2;
   __shared__ float sm[4], ss[4], st[4];
   const int64_t row = blockIdx.x;
   if (row >= n_rows[0]) return;
@@ -200,7 +204,30 @@ cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
       t += e * x;
     }
   };
-  if (V8) {
+  if (V8 && FAST) {
+    // bf16 logits: one rescale per 8 values and the hardware exp2 (its error,
+    // a few float ulps, is far below the bf16 rounding of every output)
+    for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
+      float v[8];
+      Vec8<T>::load(lr + c, v);
+      float cm = v[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) cm = fmaxf(cm, v[i]);
+      if (cm > m) {
+        const float scale = __builtin_amdgcn_exp2f((m - cm) * CE_LOG2E);  // 0 when m = -inf
+        s *= scale;
+        t *= scale;
+        m = cm;
+      }
+      const float m2 = m * CE_LOG2E;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(v[i], CE_LOG2E, -m2));
+        s += e;
+        t = fmaf(e, v[i], t);
+      }
+    }
+  } else if (V8) {
     for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
       float v[8];
       Vec8<T>::load(lr + c, v);
@@ -236,7 +263,17 @@ cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
   }
   if (!valid) tg = -1;
   __syncthreads();  // the target logit is read above before it is overwritten
-  if (V8) {
+  if (V8 && FAST) {
+    const float lse2 = lse * CE_LOG2E;
+    for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
+      float v[8];
+      Vec8<T>::load(lr + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        v[i] = cf * (__builtin_amdgcn_exp2f(fmaf(v[i], CE_LOG2E, -lse2)) - (c + i == tg ? 1.f : 0.f));
+      Vec8<T>::store(lr + c, v);
+    }
+  } else if (V8) {
     for (int64_t c = (int64_t)threadIdx.x * 8; c < V; c += 256 * 8) {
       float v[8];
       Vec8<T>::load(lr + c, v);
@@ -251,6 +288,101 @@ cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
     }
   }
 }
+
+// The same for one bf16 row of at most 8 * 512 * NCH logits held in the
+// registers of 512 threads (up to 256 VGPRs each): the row is read from memory once and written
+// once (the two-pass kernel above reads it twice, and a row of a large
+// vocabulary does not stay in L2 between the passes).
+template <int NCH>
+__global__ void __launch_bounds__(512)
+cross_entropy_row_kernel(bf16_t* __restrict__ logits, const int32_t* __restrict__ target,
+                         const float* __restrict__ coef, const int32_t* __restrict__ n_rows,
+                         int64_t V, float* __restrict__ ce, float* __restrict__ entropy) {
+  __shared__ float red[2][8];
+  const int64_t row = blockIdx.x;
+  if (row >= n_rows[0]) return;
+  bf16_t* lr = logits + row * V;
+  // a wave-uniform row base plus a 32-bit byte offset per access, so that no
+  // 64-bit address per chunk stays live between the load and the store
+  char* rowb = reinterpret_cast<char*>(lr);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint4 buf[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = (j * 512 + (int)threadIdx.x) * 8;
+    buf[j] = c < V ? *reinterpret_cast<const uint4*>(rowb + (uint32_t)c * 2u)
+                   : make_uint4(0, 0, 0, 0);
+  }
+  auto value = [&](int j, int i) {
+    const uint32_t w = (&buf[j].x)[i >> 1];
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  };
+  auto live = [&](int j) { return (j * 512 + (int)threadIdx.x) * 8 < V; };
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    if (live(j))
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, value(j, i));
+  m = wave_max(m);
+  if (lane == 0) red[0][wave] = m;
+  __syncthreads();
+  float M = red[0][0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) M = fmaxf(M, red[0][w]);
+  const float m2 = M * CE_LOG2E;
+  float s = 0.f, t = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    if (live(j))
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float x = value(j, i);
+        const float e = __builtin_amdgcn_exp2f(fmaf(x, CE_LOG2E, -m2));
+        s += e;
+        t = fmaf(e, x, t);
+      }
+  s = wave_sum(s);
+  t = wave_sum(t);
+  __syncthreads();  // every wave has read red[0]
+  if (lane == 0) { red[0][wave] = s; red[1][wave] = t; }
+  __syncthreads();
+  float S = 0.f, Tt = 0.f;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) { S += red[0][w]; Tt += red[1][w]; }
+  const float lse = M + logf(S);
+  int tg = target[row];
+  const float cf = coef[row];
+  const bool valid = tg >= 0 && tg < V;  // an out-of-range target yields NaN, never a read
+  if (threadIdx.x == 0) {
+    const float xt = valid ? bf16_to_float(lr[tg]) : NAN;
+    ce[row] = round_bf16(lse - xt);
+    if (entropy) entropy[row] = lse - Tt / S;
+  }
+  if (!valid) tg = -1;
+  __syncthreads();  // the target logit is read above before it is overwritten
+  const float lse2 = lse * CE_LOG2E;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = (j * 512 + (int)threadIdx.x) * 8;
+    if (c < V) {
+      float g[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        g[i] = __builtin_amdgcn_exp2f(fmaf(value(j, i), CE_LOG2E, -lse2));
+      if ((unsigned)(tg - c) < 8u) {  // the target's chunk (one lane of the row)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] -= c + i == tg ? 1.f : 0.f;
+      }
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(cf * g[2 * i], cf * g[2 * i + 1]);
+      *reinterpret_cast<uint4*>(rowb + (uint32_t)c * 2u) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
+constexpr int CE_ROW_NCH = 38;  // rows of up to 155648 bf16 logits
 
 __global__ void scatter_ce_kernel(const float* __restrict__ ce, const int32_t* __restrict__ sel,
                                   const int32_t* __restrict__ n_rows, int64_t max_rows,
@@ -402,6 +534,13 @@ extern "C" int alodlm_cross_entropy(void* logits, const int32_t* target, const f
   ALODLM_CHECK_ARG(vocab > 0, "cross_entropy: bad vocab");
   if (max_rows == 0) return ALODLM_OK;
   const bool v8 = vocab % 8 == 0 && aligned8(logits, dtype);
+  if (v8 && dtype == ALODLM_BF16 && vocab > 8 * 512 * (CE_ROW_NCH / 2) &&
+      vocab <= 8 * 512 * CE_ROW_NCH) {
+    cross_entropy_row_kernel<CE_ROW_NCH><<<(unsigned)max_rows, 512, 0, as_stream(stream)>>>(
+        (bf16_t*)logits, target, coef, n_rows, vocab, ce, entropy);
+    ALODLM_CHECK_LAUNCH("cross_entropy_row");
+    return ALODLM_OK;
+  }
   ALODLM_DISPATCH(dtype, T, {
     if (v8) cross_entropy_kernel<T, true><<<(unsigned)max_rows, 256, 0, as_stream(stream)>>>(
         (T*)logits, target, coef, n_rows, vocab, ce, entropy);
