@@ -198,6 +198,39 @@ class StepEngine:
         # rotary inverse frequencies exactly as [tf] modeling_qwen3.py:115-117 (float32)
         inv = 1.0 / (d.theta ** (torch.arange(0, d.head_dim, 2, dtype=torch.float32) / d.head_dim))
         self.inv_freq = inv.to(self.device)
+        # Which forward outputs the backward reuses instead of recomputing
+        # (rotary q/k, then the two norm outputs of every layer application):
+        # decided once, at the second step, from the first step's measured
+        # memory peak; the values are the same either way.
+        self._keep = None
+        self._step_alloc = None
+
+    # ------------------------------------------------------------------ memory policy
+    KEEP_FRACTION = 0.9  # of the device memory a step may plan to use
+
+    def _decide_keep(self, N):
+        """(keep rotary q/k, keep norm outputs) for this step.  The first step
+        keeps neither and records its peak; the second decides, keeping each
+        set only if the allocations now live plus the first step's growth plus
+        the set's bytes stay under KEEP_FRACTION of the device memory."""
+        dev = self.device
+        if self._keep is not None:
+            return self._keep
+        if self._step_alloc is None:
+            self._step_alloc = torch.cuda.memory_allocated(dev)
+            return (False, False)
+        growth = torch.cuda.max_memory_allocated(dev) - self._step_alloc
+        budget = self.KEEP_FRACTION * torch.cuda.get_device_properties(dev).total_memory
+        d, cfg = self.dims, self.cfg
+        apps = cfg.loop_start + cfg.max_depth * (d.layers - cfg.loop_start)
+        elem = 2 if self.dtype == torch.bfloat16 else 4
+        rotary = apps * N * (d.heads + d.kv_heads) * d.head_dim * elem
+        norms = apps * N * 2 * d.hidden * elem
+        used = torch.cuda.memory_allocated(dev) + growth
+        keep_rot = used + rotary <= budget
+        keep_norm = keep_rot and used + rotary + norms <= budget
+        self._keep = (keep_rot, keep_norm)
+        return self._keep
 
     # ------------------------------------------------------------------ helpers
     def _stream(self):
@@ -253,7 +286,9 @@ class StepEngine:
         call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), ptr(rstd1), N, H, d.eps, c, st)
         qkv = self._empty(N, W)
         self._gemm(h1, H, 1, w.wqkv_t, W, 0, qkv, W, N, W, H)
-        del h1
+        keep_rot, keep_norm = self._keep_now if save is not None else (False, False)
+        if not keep_norm:
+            h1 = None
         q = self._empty(N, d.heads * d.head_dim)
         k = self._empty(N, d.kv_heads * d.head_dim)
         call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
@@ -262,7 +297,8 @@ class StepEngine:
         lse = self._empty(d.heads, N, dtype=torch.float32)
         v = qkv[:, (d.heads + d.kv_heads) * d.head_dim:]
         self._attention_fwd(q, k, v, o, lse, b)
-        del q, k
+        if not keep_rot:
+            q = k = None
         x1 = self._empty(N, H)
         self._gemm(o, d.heads * d.head_dim, 1, w.wo_t, H, 0, x1, H, N, H,
                    d.heads * d.head_dim, epi=EPI_RESIDUAL, R=x, ldr=H)
@@ -271,17 +307,18 @@ class StepEngine:
         call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), ptr(rstd2), N, H, d.eps, c, st)
         gu = self._empty(N, 2 * I)
         self._gemm(h2, H, 1, w.wgu_t, 2 * I, 0, gu, 2 * I, N, 2 * I, H)
-        del h2
+        if not keep_norm:
+            h2 = None
         act = self._empty(N, I)
         call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
         y = self._empty(N, H)
         self._gemm(act, I, 1, w.wd_t, H, 0, y, H, N, H, I, epi=EPI_RESIDUAL, R=x1, ldr=H)
         if save is not None:
-            save.append((li, x, rstd1, qkv, o, lse, x1, rstd2, gu))
+            save.append((li, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2))
         return y
 
     def _layer_bwd(self, dy, saved, b, g):
-        li, x, rstd1, qkv, o, lse, x1, rstd2, gu = saved
+        li, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2 = saved
         d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
         w, gw = self.layers[li], self.grad_layers[li]
         H, W, I = d.hidden, d.qkv_width, d.intermediate
@@ -295,8 +332,9 @@ class StepEngine:
         del dact
         self._gemm(dy, H, 0, act, I, 0, gw.wd, I, H, I, N, epi=EPI_ACCUM)
         del act
-        h2 = self._empty(N, H)
-        call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
+        if h2 is None:
+            h2 = self._empty(N, H)
+            call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
         dh2 = self._empty(N, H)
         self._gemm(dgu, 2 * I, 1, w.wgu, H, 0, dh2, H, N, H, 2 * I)
         self._gemm(dgu, 2 * I, 0, h2, H, 0, gw.wgu, H, 2 * I, H, N, epi=EPI_ACCUM)
@@ -310,10 +348,12 @@ class StepEngine:
         do = self._empty(N, QD)
         self._gemm(dx1, H, 1, w.wo, QD, 0, do, QD, N, QD, H)
         self._gemm(dx1, H, 0, o, QD, 0, gw.wo, QD, H, QD, N, epi=EPI_ACCUM)
-        q = self._empty(N, QD)
-        k = self._empty(N, d.kv_heads * d.head_dim)
-        call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
-             ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
+        if q is None:
+            q = self._empty(N, QD)
+            k = self._empty(N, d.kv_heads * d.head_dim)
+            call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
+                 ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps,
+                 c, st)
         dq = self._empty(N, QD)
         dk = self._empty(N, d.kv_heads * d.head_dim)
         dqkv = self._empty(N, W)
@@ -327,8 +367,9 @@ class StepEngine:
              ptr(b.positions), ptr(self.inv_freq), ptr(dqkv), ptr(gw.qn), ptr(gw.kn), ptr(ws), N,
              d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
         del dq, dk
-        h1 = self._empty(N, H)
-        call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, N, H, d.eps, c, st)
+        if h1 is None:
+            h1 = self._empty(N, H)
+            call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, N, H, d.eps, c, st)
         dh1 = self._empty(N, H)
         self._gemm(dqkv, W, 1, w.wqkv, H, 0, dh1, H, N, H, W)
         self._gemm(dqkv, W, 0, h1, H, 0, gw.wqkv, H, W, H, N, epi=EPI_ACCUM)
@@ -361,6 +402,7 @@ class StepEngine:
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         S = b.boundaries.numel() - 1
         saves = [] if need_grad else None
+        self._keep_now = self._decide_keep(N) if need_grad else (False, False)
         x = self._empty(N, H)
         call("alodlm_embed_gather", ptr(self.embed), ptr(b.ids), ptr(x), N, H, V, c, st)
         for li in range(cfg.loop_start):

@@ -297,6 +297,9 @@ def main():
                    "dual_stream_rows": 2 * tokens,
                    "parallelism": "none (1 GPU)"},
         "device": device_info(),
+        "memory": {"peak_allocated_gib": round(torch.cuda.max_memory_allocated(device) / 2**30, 1),
+                   "kept_forward_outputs": {"rotary_qk": bool(engine._keep and engine._keep[0]),
+                                            "norm_outputs": bool(engine._keep and engine._keep[1])}},
         "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
         "step_tflop": round(step_f / 1e12, 1),
     }

@@ -184,3 +184,29 @@ def test_tiny_bf16_step_matches_oracle():
     worst_exact = min(cosine(grads[_golden_name(n)], q[n].grad) for n in O.param_names(dims))
     log(f"tiny bf16: loss {out[0]:.6f} vs {loss.item():.6f} (unrounded {exact.item():.6f}); "
         f"worst grad cosine {worst:.6f} (unrounded oracle {worst_exact:.6f})")
+
+
+@pytest.mark.parametrize("keep", [(True, False), (True, True)])
+def test_kept_forward_outputs_match_recompute(keep):
+    """The backward gives the same bits whether it reuses the rotary q/k and
+    the norm outputs kept from the forward or recomputes them (the policy the
+    engine picks from its memory budget)."""
+    log(f"kept forward outputs {keep}")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=1)
+    model = make_model(dims, obj, params, dtype=torch.bfloat16)
+    ids, labels, bounds = _tiny_inputs()
+    draws, uniforms = cpu_draws(labels, bounds, obj.block_size, 1, obj.max_depth)
+    engine = model.engine()
+    results = []
+    for policy in ((False, False), keep):
+        engine._keep = policy
+        out, _, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
+        results.append((out, grads))
+    assert torch.equal(results[0][0], results[1][0])
+    for name, g in results[0][1].items():
+        if name == "backbone.model.embed_tokens.weight":
+            # rows of repeated token ids are summed by float atomics, in no fixed order
+            torch.testing.assert_close(g, results[1][1][name], rtol=1e-5, atol=1e-7)
+        else:
+            assert torch.equal(g, results[1][1][name]), name
