@@ -204,22 +204,28 @@ class StepEngine:
         # memory peak; the values are the same either way.
         self._keep = None
         self._step_alloc = None
+        self._step_peak = None
 
     # ------------------------------------------------------------------ memory policy
-    KEEP_FRACTION = 0.9  # of the device memory a step may plan to use
+    KEEP_FRACTION = 0.95  # of the device memory a step may plan to use
 
     def _decide_keep(self, N):
         """(keep rotary q/k, keep norm outputs) for this step.  The first step
-        keeps neither and records its peak; the second decides, keeping each
-        set only if the allocations now live plus the first step's growth plus
-        the set's bytes stay under KEEP_FRACTION of the device memory."""
+        keeps neither and measures how far its forward and backward raise the
+        allocated memory (the device's peak statistics are reset at its start);
+        the second step decides once, keeping each set only if the allocations
+        live at its start (the optimizer state included by then) plus that
+        growth plus the set's bytes stay under KEEP_FRACTION of the device."""
         dev = self.device
         if self._keep is not None:
             return self._keep
         if self._step_alloc is None:
+            torch.cuda.reset_peak_memory_stats(dev)
             self._step_alloc = torch.cuda.memory_allocated(dev)
             return (False, False)
-        growth = torch.cuda.max_memory_allocated(dev) - self._step_alloc
+        if self._step_peak is None:  # the first step ran no backward
+            return (False, False)
+        growth = self._step_peak - self._step_alloc
         budget = self.KEEP_FRACTION * torch.cuda.get_device_properties(dev).total_memory
         d, cfg = self.dims, self.cfg
         apps = cfg.loop_start + cfg.max_depth * (d.layers - cfg.loop_start)
@@ -550,4 +556,6 @@ class StepEngine:
             dx = self._layer_bwd(dx, saved, b, grads)
         call("alodlm_embed_scatter_add", ptr(dx), ptr(b.ids), None, 0, ptr(g_embed), N, H, V, c,
              st)
+        if self._step_alloc is not None and self._step_peak is None:
+            self._step_peak = torch.cuda.max_memory_allocated(self.device)
         return grads
