@@ -240,6 +240,26 @@ __global__ void splitk_reduce4_kernel(const float* __restrict__ partial, int64_t
   }
 }
 
+// C[m, n] = bf16(sum_s partial[s, m, n]) (split order; the partials carry
+// alpha): the STORE epilogue of a split product, rounded once.
+__global__ void splitk_store_kernel(const float* __restrict__ partial, int64_t splits, int64_t M,
+                                    int64_t N, bf16_t* __restrict__ C, int64_t ldc) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t plane = M * N;
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+    float s = partial[m * N + n];
+    for (int64_t p = 1; p < splits; ++p) s += partial[p * plane + m * N + n];
+    C[m * ldc + n] = float_to_bf16(s);
+  }
+}
+
+static void splitk_store(const float* partial, int64_t splits, int64_t M, int64_t N, bf16_t* C,
+                         int64_t ldc, hipStream_t st) {
+  const dim3 grid(ceil_div_u(N, 256), (unsigned)(M < 65535 ? M : 65535));
+  splitk_store_kernel<<<grid, 256, 0, st>>>(partial, splits, M, N, C, ldc);
+}
+
 static void splitk_reduce(const float* partial, int64_t splits, int64_t M, int64_t N, float* C,
                           int64_t ldc, hipStream_t st) {
   const bool vec = N % 4 == 0 && ldc % 4 == 0 &&
@@ -334,6 +354,7 @@ void gemm_big_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B
 bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int64_t M, int64_t N,
                       int64_t K);
 int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K);
+int64_t gemm_dl_store_splits(int64_t M, int64_t N, int64_t K);
 void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
@@ -346,7 +367,12 @@ static bool use_big(int64_t M, int64_t N, int64_t K, bool any_kmajor = false) {
 }
 
 extern "C" int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype) {
-  if (epilogue != ALODLM_EPI_ACCUM || dtype != ALODLM_BF16) return 0;
+  if (dtype != ALODLM_BF16) return 0;
+  if (epilogue == ALODLM_EPI_STORE) {
+    const int64_t s = (M >= 256 && N >= 256 && K % 32 == 0) ? gemm_dl_store_splits(M, N, K) : 1;
+    return s > 1 ? s * M * N : 0;
+  }
+  if (epilogue != ALODLM_EPI_ACCUM) return 0;
   int64_t s = splitk_count(M, N, K);
   if (use_big(M, N, K)) {
     const int64_t b = gemm_big_splits(M, N, K);
@@ -393,16 +419,24 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
       gemm_dl_eligible(lda, a_kmajor, ldb, b_kmajor, M, N, K)) {
     int64_t splits = 1;
-    if (epilogue == ALODLM_EPI_ACCUM) {
-      splits = gemm_dl_splits(M, N, K);
-      if (splits > 1 && workspace == nullptr) splits = 1;
+    if (epilogue == ALODLM_EPI_ACCUM) splits = gemm_dl_splits(M, N, K);
+    else if (epilogue == ALODLM_EPI_STORE) splits = gemm_dl_store_splits(M, N, K);
+    if (splits > 1 && workspace == nullptr) splits = 1;
+    if (splits > 1) {  // the launch splits K into chunks of whole 32-deep stages
+      const int64_t kps = (((K + splits - 1) / splits) + 31) / 32 * 32;
+      if ((K + kps - 1) / kps < 2) splits = 1;
     }
+    // a split STORE product writes float partials (the ACCUM kernel with a
+    // partial buffer), then one reduction rounds their sum to bf16
+    const int launch_epi = (epilogue == ALODLM_EPI_STORE && splits > 1) ? ALODLM_EPI_ACCUM : epilogue;
     int64_t nsplit = 1;
     gemm_dl_launch((const bf16_t*)A, lda, a_kmajor, (const bf16_t*)B, ldb, b_kmajor, C, ldc,
-                   (const bf16_t*)R, ldr, M, N, K, alpha, epilogue, workspace, splits, &nsplit, st);
+                   (const bf16_t*)R, ldr, M, N, K, alpha, launch_epi, workspace, splits, &nsplit,
+                   st);
     ALODLM_CHECK_LAUNCH("gemm_bf16_dl");
-    if (epilogue == ALODLM_EPI_ACCUM && nsplit > 1) {
-      splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st);
+    if (launch_epi == ALODLM_EPI_ACCUM && nsplit > 1) {
+      if (epilogue == ALODLM_EPI_STORE) splitk_store(workspace, nsplit, M, N, (bf16_t*)C, ldc, st);
+      else splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st);
       ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
     }
     return ALODLM_OK;

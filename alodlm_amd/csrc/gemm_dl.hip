@@ -468,6 +468,25 @@ int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K) {
   return s;
 }
 
+// Splits of a bf16-output (STORE) product: the fewest that bring the rounds
+// of 256 workgroups (one per CU) within 8 % of the split-free work, so that a
+// long-K product with few output tiles (the LM head's dX) does not leave CUs
+// idle in its last round; only K >= 16384 (the partials' traffic is then
+// small next to the product) and every split keeps >= 2048 of K.  1 when the
+// tiles already fill the rounds.
+int64_t gemm_dl_store_splits(int64_t M, int64_t N, int64_t K) {
+  if (K < 16384) return 1;
+  const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
+  const int64_t cus = 256;
+  auto cost = [&](int64_t s) { return (double)((tiles * s + cus - 1) / cus) / (double)s; };
+  const double ideal = (double)tiles / (double)cus;
+  if (cost(1) <= 1.08 * ideal) return 1;
+  int64_t best = 1;
+  for (int64_t s = 2; s <= 8 && K / s >= 2048; ++s)
+    if (cost(s) < cost(best) && cost(best) - cost(s) > 0.02 * cost(1)) best = s;
+  return best;
+}
+
 template <bool AK, bool BK, int NW, int KD, int ST>
 static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                       int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N, int64_t K,

@@ -84,6 +84,37 @@ def test_gemm_layouts_and_epilogues(M, N, K, ak, bk, dtype, epi):
     assert err <= tol, f"max rel err {err}"
 
 
+@pytest.mark.parametrize("M,N", [(512, 512), (300, 260)])
+def test_gemm_store_splitk_long_k(M, N):
+    """A bf16-output product with few output tiles and a long K (the LM head's
+    dX shape: dlogits [rows, V] times the head weight) is split over K; the
+    float partials are summed in split order and rounded once."""
+    L = lib()
+    K = 20480
+    log(f"gemm store splitk M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M + N)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    Bt = torch.randn(K, N, generator=g).to(torch.bfloat16)  # n-contiguous like the head weight
+    ws_n = L.query("alodlm_gemm_workspace", M, N, K, 0, 1)
+    assert ws_n >= 2 * M * N, "the long-K product should be split"
+    ws = torch.empty(ws_n, dtype=torch.float32, device=DEV)
+    Ad, Bd = A.to(DEV), Bt.to(DEV)
+    C = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    L.call("alodlm_gemm", L.ptr(Ad), K, 1, L.ptr(Bd), N, 0, L.ptr(C), N, None, 0, M, N, K, 0.5,
+           0, 1, L.ptr(ws), st())
+    torch.cuda.synchronize()
+    ref = (A.double() @ Bt.double()) * 0.5
+    scale = ref.abs().max().item()
+    err = (C.cpu().double() - ref).abs().max().item() / scale
+    assert err <= 8e-3, f"max rel err {err}"
+    # the same product without a workspace runs unsplit: equal within bf16 rounding
+    C1 = torch.empty_like(C)
+    L.call("alodlm_gemm", L.ptr(Ad), K, 1, L.ptr(Bd), N, 0, L.ptr(C1), N, None, 0, M, N, K, 0.5,
+           0, 1, None, st())
+    torch.cuda.synchronize()
+    assert (C1.cpu().double() - C.cpu().double()).abs().max().item() <= 8e-3 * scale
+
+
 def test_gemm_splitk_accumulates_large_k():
     """dW-shaped product (both operands m/n-contiguous, K = 8192 rows) uses split-K."""
     L = lib()
