@@ -140,8 +140,11 @@ int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv, cons
  * epilogue: ALODLM_EPI_STORE    C = alpha*acc                (C in dtype)
  *           ALODLM_EPI_RESIDUAL C = R + cast(alpha*acc)       (C, R in dtype; may alias)
  *           ALODLM_EPI_ACCUM    Cf32 += alpha*acc             (C is float)
- * workspace: float scratch of alodlm_gemm_workspace(M, N, K, flags) floats for
- * split-K reductions of ALODLM_EPI_ACCUM (may be NULL when that is 0).
+ * workspace: float scratch of alodlm_gemm_workspace(M, N, K, epilogue, dtype)
+ * floats for split-K partials: ALODLM_EPI_ACCUM products with few output
+ * tiles, and bf16 ALODLM_EPI_STORE products with K >= 16384 and few output
+ * tiles (summed in split order, then rounded once).  May be NULL (the
+ * product then runs unsplit); unused when the query returns 0.
  * ------------------------------------------------------------------------ */
 enum { ALODLM_EPI_STORE = 0, ALODLM_EPI_RESIDUAL = 1, ALODLM_EPI_ACCUM = 2 };
 int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype);
