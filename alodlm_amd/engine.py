@@ -203,6 +203,7 @@ class StepEngine:
         # decided once, at the second step, from the first step's measured
         # memory peak; the values are the same either way.
         self._keep = None
+        self._keep_rows = 0
         self._step_alloc = None
         self._step_peak = None
 
@@ -218,7 +219,9 @@ class StepEngine:
         growth plus the set's bytes stay under KEEP_FRACTION of the device."""
         dev = self.device
         if self._keep is not None:
-            return self._keep
+            # a pack with more rows than the one the decision was made for
+            # keeps nothing: its activations alone outgrow that estimate
+            return self._keep if N <= self._keep_rows else (False, False)
         if self._step_alloc is None:
             torch.cuda.reset_peak_memory_stats(dev)
             self._step_alloc = torch.cuda.memory_allocated(dev)
@@ -236,6 +239,7 @@ class StepEngine:
         keep_rot = used + rotary <= budget
         keep_norm = keep_rot and used + rotary + norms <= budget
         self._keep = (keep_rot, keep_norm)
+        self._keep_rows = N
         return self._keep
 
     # ------------------------------------------------------------------ helpers

@@ -200,7 +200,7 @@ def test_kept_forward_outputs_match_recompute(keep):
     engine = model.engine()
     results = []
     for policy in ((False, False), keep):
-        engine._keep = policy
+        engine._keep, engine._keep_rows = policy, 2 * len(ids)
         out, _, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
         results.append((out, grads))
     assert torch.equal(results[0][0], results[1][0])
