@@ -95,3 +95,31 @@ def test_mask_draws_match_restatement():
     for b, perm in enumerate(perms):
         if perm is not None:
             assert np.array_equal(buf[po[b]:po[b] + int(block_n[b])], perm), b
+
+
+def test_mask_draws_with_own_generator():
+    """build_batch's `generator` argument: the draws come from that CUDA
+    generator (not the default one) and advance only it."""
+    from alodlm_amd.batch import _device_draws, block_supervised_counts
+    lengths, block_size = [700, 300], 32
+    labels = _labels(lengths, 0.1, 4)
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).tolist()
+    seg_block = [0]
+    for n in lengths:
+        seg_block.append(seg_block[-1] + (n + block_size - 1) // block_size)
+    default_before = torch.cuda.get_rng_state()
+    ref_gen = torch.Generator(device="cuda").manual_seed(31)
+    probs, counts, perms = draw_masking(labels, offsets, block_size, "cuda", ref_gen)
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    block_n = np.concatenate(block_supervised_counts(labels, offsets, block_size))
+    p_t, c_t, po_t, perm_buf = _device_draws(block_n, seg_block, block_size,
+                                             torch.device("cuda"), gen)
+    torch.cuda.synchronize()
+    assert gen.get_offset() == ref_gen.get_offset()
+    assert torch.equal(torch.cuda.get_rng_state(), default_before)
+    assert np.array_equal(p_t.cpu().numpy().view(np.uint32), probs.view(np.uint32))
+    assert np.array_equal(c_t.cpu().numpy(), counts)
+    buf, po = perm_buf.cpu().numpy(), po_t.cpu().numpy()
+    for b, perm in enumerate(perms):
+        if perm is not None:
+            assert np.array_equal(buf[po[b]:po[b] + int(block_n[b])], perm.cpu().numpy()), b
