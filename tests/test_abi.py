@@ -54,3 +54,25 @@ def test_library_loads_and_reports_abi():
     with pytest.raises(ValueError):
         _lib.call("alodlm_objective", None, None, None, None, None, None, None, None, 1, 4, 99,
                   0.4, 0.1, 1.0, None, None, None, None)
+
+
+def test_gemm_workspace_policy():
+    """The GEMM workspace query (host only): long-K bf16-output products with
+    few output tiles ask for split-K partials, products that fill the chip's
+    rounds and float32 outputs do not, and dW products split when their tiles
+    are few."""
+    from alodlm_amd import _lib
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    q = lambda *a: _lib.query("alodlm_gemm_workspace", *a)
+    STORE, ACCUM, BF16, F32 = 0, 2, 1, 0
+    # LM head dX at 1.7B (21504 rows, hidden 2048, vocab 151936): 672 tiles, 3 splits
+    assert q(21504, 2048, 151936, STORE, BF16) == 3 * 21504 * 2048
+    # LM head dX at 8B (about 2700 rows, hidden 4096): 176 tiles, 7 splits
+    assert q(2700, 4096, 151936, STORE, BF16) == 7 * 2700 * 4096
+    # forward products of the 1.7B step: whole rounds, or K too short to split
+    assert q(32768, 12288, 2048, STORE, BF16) == 0
+    assert q(4096, 6144, 4096, STORE, BF16) == 0
+    assert q(21504, 2048, 151936, STORE, F32) == 0
+    # dW of the 1.7B QKV projection (4096 x 2048 over 32768 rows): 128 tiles, split 4
+    assert q(4096, 2048, 32768, ACCUM, BF16) == 4 * 4096 * 2048
