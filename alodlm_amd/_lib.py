@@ -34,6 +34,7 @@ SIGNATURES = {
     "alodlm_rmsnorm_fwd": [P, P, P, P, I64, I64, F32, I32, P],
     "alodlm_rmsnorm_bwd_workspace": [I64, I64],
     "alodlm_rmsnorm_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, P],
+    "alodlm_rmsnorm_bwd_noalloc": [P, P, P, P, P, P, P, I64, I64, I32, P],
     "alodlm_qknorm_rope_fwd": [P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
     "alodlm_qknorm_rope_bwd_workspace": [I64, I64, I64, I64],
     "alodlm_qknorm_rope_bwd": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],

@@ -21,3 +21,12 @@ static inline int64_t bwd_rows_per_block(int64_t rows) {
   r = (r + 3) / 4 * 4;
   return r < 4 ? 4 : (r > 32 ? 32 : r);
 }
+
+// RMSNorm backward (and the carry-norm backward when skip_exits is set: rows
+// with skip_exits[r] <= skip_depth pass dres through).  `workspace` holds
+// alodlm_rmsnorm_bwd_workspace(rows, cols) floats; every element of it the
+// launch reads is written earlier in the same launch sequence.
+int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, const void* w,
+                       const void* dres, void* dx, float* dw_accum, float* workspace,
+                       int64_t rows, int64_t cols, int dtype, const int32_t* skip_exits,
+                       int64_t skip_depth, hipStream_t st);

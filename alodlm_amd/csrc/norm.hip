@@ -407,7 +407,7 @@ extern "C" int64_t alodlm_rmsnorm_bwd_workspace(int64_t rows, int64_t cols) {
   return ((rows + rpb - 1) / rpb + COLUMN_REDUCE_MAX_GROUPS) * cols;
 }
 
-static int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, const void* w,
+int rmsnorm_bwd_launch(const void* dy, const void* x, const float* rstd, const void* w,
                               const void* dres, void* dx, float* dw_accum, float* workspace,
                               int64_t rows, int64_t cols, int dtype, const int32_t* skip_exits,
                               int64_t skip_depth, hipStream_t st) {

@@ -109,6 +109,22 @@ int alodlm_rmsnorm_bwd(const void* dy, const void* x, const float* rstd, const v
                        const void* dres, void* dx, float* dw_accum, float* workspace,
                        int64_t rows, int64_t cols, int dtype, void* stream);
 
+/* alodlm_rmsnorm_bwd without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Its scratch is a library-held device
+ * array of ALODLM_NOALLOC_SCRATCH_FLOATS floats per GPU (16 MiB, held until
+ * the process ends); shapes whose alodlm_rmsnorm_bwd_workspace(rows, cols)
+ * exceeds it return ALODLM_EINVAL (e.g. 32768 x 2048 and 4096 x 4096 fit,
+ * 65536 x 2048 does not).  Results are bit-identical to alodlm_rmsnorm_bwd.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams or threads without ordering) race; calls ordered on
+ * one stream are safe. */
+#define ALODLM_NOALLOC_SCRATCH_FLOATS 4194304
+int alodlm_rmsnorm_bwd_noalloc(const void* dy, const void* x, const float* rstd, const void* w,
+                               const void* dres, void* dx, float* dw_accum, int64_t rows,
+                               int64_t cols, int dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * q_norm/k_norm + rotary (alodlm/model.py:41-46,58; [tf] :126-137).
  * qkv: [rows, (nq+2*nkv)*dh] projections (q | k | v).  positions: int64 [rows].

@@ -76,3 +76,17 @@ def test_gemm_workspace_policy():
     assert q(21504, 2048, 151936, STORE, F32) == 0
     # dW of the 1.7B QKV projection (4096 x 2048 over 32768 rows): 128 tiles, split 4
     assert q(4096, 2048, 32768, ACCUM, BF16) == 4 * 4096 * 2048
+
+
+def test_no_alloc_rmsnorm_bwd_rejects_oversize_on_the_host():
+    """The allocation-free RMSNorm backward checks its scratch limit before
+    touching the device (32768 x 2048 fits the 4 Mi-float scratch, 65536 x 2048
+    does not)."""
+    from alodlm_amd import _lib
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    assert _lib.query("alodlm_rmsnorm_bwd_workspace", 32768, 2048) <= 4194304
+    assert _lib.query("alodlm_rmsnorm_bwd_workspace", 65536, 2048) > 4194304
+    with pytest.raises(ValueError, match="scratch"):
+        _lib.call("alodlm_rmsnorm_bwd_noalloc", None, None, None, None, None, None, None,
+                  65536, 2048, _lib.BF16_CODE, None)
