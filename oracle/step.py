@@ -321,11 +321,15 @@ _METRICS = ("denoising", "actor", "sampled_mean_depth", "prediction_cost",
             "regularization_cost", "profile_mean_depth", "first_pass_halt_probability")
 
 
-def outcome_loss(ce, gates, exits, masked, mask_probability, packed_boundaries, cfg):
+def outcome_loss(ce, gates, exits, masked, mask_probability, packed_boundaries, cfg,
+                 credit_ce=None):
     """NELBO denoising term plus the sequence score-function actor (alodlm/loss.py:35-90).
 
     ce: [K, M] masked-token cross-entropies; gates: list of K [N] gate logits;
-    exits: [N] sampled exit depth in 1..K.
+    exits: [N] sampled exit depth in 1..K.  ``credit_ce`` ([K, M], optional)
+    replaces ``ce`` inside the credit's prediction cost only, which is a
+    sampled cost without gradient (loss.py:72-78): a test then compares two
+    implementations with the same realisation of that cost.
     """
     masked = torch.as_tensor(masked)
     M = int(masked.sum())
@@ -350,7 +354,8 @@ def outcome_loss(ce, gates, exits, masked, mask_probability, packed_boundaries, 
         log_prior = torch.log_softmax(-cfg.depth_prior_c * torch.arange(1, K + 1, dtype=g.dtype), 0)
         qbar = log_exit.detach().exp().mean(1).clamp_min(1e-12)
         marginal = qbar.log()[z - 1]
-        prediction = ce.detach().gather(0, (z - 1)[None]).squeeze(0) - ce[0].detach()
+        costs = (ce if credit_ce is None else torch.as_tensor(credit_ce).to(ce.dtype)).detach()
+        prediction = costs.gather(0, (z - 1)[None]).squeeze(0) - costs[0]
         mi_cost = cfg.kl_beta_mi * (logq - marginal)
         budget_cost = cfg.kl_beta_marg * (marginal - log_prior[z - 1])
         credit = (prediction + mi_cost) + budget_cost                   # loss.py:75-78
@@ -400,11 +405,13 @@ def autoregressive_loss(logits, labels, packed_boundaries, ce_dtype=None):
     return logits.new_zeros((), requires_grad=True)
 
 
-def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms, ce_dtype=None):
+def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms, ce_dtype=None,
+              credit_ce=None):
     """The full ALoDLM._forward_loss (alodlm/model.py:176-187) from explicit draws.
 
     ``ce_dtype`` (e.g. torch.bfloat16) rounds every per-token cross-entropy to
     that dtype, as the reference's bf16 run does; None keeps full precision.
+    ``credit_ce`` is passed to ``outcome_loss``.
     Returns (total loss, metrics dict, extras dict with batch/gates/exits/ce).
     """
     batch = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id, draws)
@@ -416,7 +423,7 @@ def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms, ce_dt
                                                      reduction="none"), ce_dtype)
                       for lg in logits])
     den_actor, metrics = outcome_loss(ce, gates, exits, masked, batch["mask_probability"],
-                                      batch["boundaries"], cfg)
+                                      batch["boundaries"], cfg, credit_ce)
     ar = torch.stack([autoregressive_loss(lg, labels, batch["boundaries"], ce_dtype)
                       for lg in logits]).mean()
     total = (den_actor + ar) / 2

@@ -19,7 +19,12 @@ def gpu_available():
 
 
 def hf_backbone(dims, dtype=torch.float32):
+    """A Qwen3ForCausalLM of these dimensions with uninitialised parameters
+    (built on the meta device, so large vocabularies cost no random init);
+    callers load every parameter.  The rotary embedding's frequency buffer is
+    computed as transformers computes it."""
     from transformers import Qwen3Config, Qwen3ForCausalLM
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
     cfg = Qwen3Config(
         hidden_size=dims.hidden, intermediate_size=dims.intermediate,
         num_hidden_layers=dims.layers, num_attention_heads=dims.heads,
@@ -27,7 +32,11 @@ def hf_backbone(dims, dtype=torch.float32):
         max_position_embeddings=4096, rms_norm_eps=dims.eps,
         rope_parameters={"rope_type": "default", "rope_theta": dims.theta},
         bos_token_id=1, eos_token_id=2, pad_token_id=0, tie_word_embeddings=False)
-    return Qwen3ForCausalLM(cfg).to(dtype)
+    with torch.device("meta"):
+        model = Qwen3ForCausalLM(cfg)
+    model = model.to_empty(device="cpu")
+    model.model.rotary_emb = Qwen3RotaryEmbedding(config=cfg)
+    return model.to(dtype)
 
 
 def make_model(dims, objective, params, device="cuda", dtype=torch.float32):

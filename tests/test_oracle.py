@@ -161,6 +161,29 @@ def test_outcome_loss_matches_analytic_restatement(K, depths):
         torch.testing.assert_close(a, e if e is not None else torch.zeros_like(a))
 
 
+def test_outcome_loss_credit_costs_from_outside_enter_only_the_credit():
+    """credit_ce equal to ce changes nothing; another credit_ce changes the
+    actor through the credit's prediction cost only: the denoising term and
+    every gradient with respect to ce stay the same (the credit carries no
+    gradient, alodlm/loss.py:72-78)."""
+    K = 3
+    cfg = O.Objective(max_depth=K, gate_init_pi=(1 / K,) * K)
+    ce = torch.tensor([[3., 4., 5., 6.], [2., 3., 3., 4.], [1., 2., 2., 3.]], requires_grad=True)
+    gates = [torch.tensor([-.4, .2, -.3, .7], requires_grad=True) for _ in range(K)]
+    args = (torch.tensor([1, 3, 2, 3]), torch.ones(4, dtype=torch.bool),
+            torch.tensor([.2, .4, .5, .8]), torch.tensor([0, 2, 4]), cfg)
+    base, m0 = O.outcome_loss(ce, gates, *args)
+    same, m1 = O.outcome_loss(ce, gates, *args, credit_ce=ce.detach().clone())
+    torch.testing.assert_close(base, same)
+    other, m2 = O.outcome_loss(ce, gates, *args, credit_ce=ce.detach() + torch.tensor(
+        [[0.], [0.5], [1.0]]))
+    assert float(m2["denoising"]) == float(m0["denoising"])
+    assert float(m2["actor"]) != float(m0["actor"])
+    g0 = torch.autograd.grad(base, ce, retain_graph=True)[0]
+    g2 = torch.autograd.grad(other, ce)[0]
+    torch.testing.assert_close(g0, g2)
+
+
 def test_outcome_loss_no_masked_rows_is_zero():
     cfg = O.Objective(max_depth=3, gate_init_pi=(1 / 3,) * 3)
     ce = torch.zeros(3, 0, requires_grad=True)

@@ -131,6 +131,9 @@ def test_tiny_fp32_step_matches_reference_golden_and_oracle():
     out, state, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
     _check_batch(state, g)
     np.testing.assert_array_equal(state["exits"].cpu().numpy(), g["exits"])
+    # per-pass gate logits, hence halting probabilities, of the reference run
+    torch.testing.assert_close(state["gates"].cpu(), torch.as_tensor(g["gates"]), rtol=1e-5,
+                               atol=1e-6)
     assert abs(out[0] - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
     for i, key in enumerate(METRICS, 1):
         ref = float(g["metric_" + key])
@@ -172,6 +175,9 @@ def test_tiny_bf16_step_matches_oracle():
     np.testing.assert_array_equal(state["exits"].cpu().numpy(), extra["exits"].numpy())
     np.testing.assert_array_equal(state["batch"].masked.cpu().numpy(), extra["batch"]["masked"])
     assert abs(out[0] - loss.item()) <= 1e-2 * abs(loss.item())
+    for d, ref in enumerate(extra["gates"]):
+        diff = (torch.sigmoid(state["gates"][d].cpu().double()) - torch.sigmoid(ref.detach())).abs()
+        assert diff.max().item() <= 1e-2, (d, diff.max().item())
     worst = 1.0
     for name in O.param_names(dims):
         c = cosine(grads[_golden_name(name)], p[name].grad)
@@ -210,3 +216,53 @@ def test_kept_forward_outputs_match_recompute(keep):
             torch.testing.assert_close(g, results[1][1][name], rtol=1e-5, atol=1e-7)
         else:
             assert torch.equal(g, results[1][1][name]), name
+
+
+def test_tiny_step_without_masked_rows_or_targets():
+    """A pack whose labels are all ignored (-100): no block has a candidate, so
+    M = 0 and there is no autoregressive target.  The reference returns
+    ce.sum() + 0 * gates = 0 with zero metrics (alodlm/loss.py:43-48) and an
+    AR loss of 0 (loss.py:31-32); every gradient is zero."""
+    log("tiny step, M = 0, no AR targets")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=2)
+    model = make_model(dims, obj, params)
+    ids, _, bounds = _tiny_inputs(seed=2)
+    labels = torch.full_like(ids, -100)
+    engine = model.engine()
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    out, state = engine.forward(ids.cuda(), labels.cuda(), bounds, True, generator=gen)
+    grads = engine.backward(state, 1.0)
+    torch.cuda.synchronize()
+    assert int(state["batch"].masked.sum()) == 0
+    assert torch.equal(out.cpu()[:9], torch.zeros(9))
+    assert torch.equal(grads.cpu(), torch.zeros_like(grads.cpu()))
+
+
+def test_tiny_step_without_masked_rows_matches_oracle():
+    """Masking draws that mask nothing (every block's count round(n * p) = 0):
+    M = 0, so the objective is the autoregressive loss alone; loss and every
+    gradient against the oracle."""
+    log("tiny step, M = 0 with AR targets")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=3)
+    model = make_model(dims, obj, params)
+    ids, labels, bounds = _tiny_inputs(seed=3)
+    nblocks = sum(-(-(int(b) - int(a)) // obj.block_size) for a, b in zip(bounds, bounds[1:]))
+    draws = (np.full(nblocks, 1e-8, dtype=np.float32), np.zeros(nblocks, dtype=np.int32),
+             [None] * nblocks)
+    uniforms = [torch.rand(2 * len(ids), generator=torch.Generator().manual_seed(d))
+                for d in range(obj.max_depth - 1)]
+    out, state, grads = _run_engine(model, ids, labels, bounds, draws, uniforms)
+    assert int(state["batch"].masked.sum()) == 0
+    p = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    od = oracle_draws(draws, [int(v) for v in bounds], obj.block_size)
+    loss, metrics, _ = O.step_loss(p, ids, labels, bounds, dims, obj, od, uniforms)
+    loss.backward()
+    assert abs(out[0] - loss.item()) <= 1e-5 * abs(loss.item())
+    assert abs(out[8] - metrics["ar_loss"].item()) <= 1e-5 * abs(metrics["ar_loss"].item())
+    assert torch.equal(out[1:8], torch.zeros(7, dtype=out.dtype))
+    for name in O.param_names(dims):
+        mine, ref = grads[_golden_name(name)].double(), p[name].grad.double()
+        scale = ref.abs().max().item() + 1e-12
+        assert (mine - ref).abs().max().item() <= 1e-4 * scale, name
