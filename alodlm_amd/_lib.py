@@ -38,6 +38,11 @@ SIGNATURES = {
     "alodlm_qknorm_rope_fwd": [P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
     "alodlm_qknorm_rope_bwd_workspace": [I64, I64, I64, I64],
     "alodlm_qknorm_rope_bwd": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
+    "alodlm_qknorm_rotary_fwd": [P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
+    "alodlm_qknorm_rotary_bwd": [P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32,
+                                 P],
+    "alodlm_rotary_fwd": [P, P, P, P, I64, I64, I64, I32, P],
+    "alodlm_rotary_bwd": [P, P, P, P, I64, I64, I64, I32, P],
     "alodlm_gemm_workspace": [I64, I64, I64, I32, I32],
     "alodlm_gemm": [P, I64, I32, P, I64, I32, P, I64, P, I64, I64, I64, I64, F32, I32, I32, P, P],
     "alodlm_attention_fwd": [P, P, P, I64, P, P, P, I64, P, P, I64, I64, I64, I64, I64, I32, P],
@@ -59,6 +64,10 @@ SIGNATURES = {
     "alodlm_decode_readout": [P, I64, I64, P, P, I32, P],
     "alodlm_objective_workspace": [I64, I64, I64],
     "alodlm_objective": [P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P],
+    "alodlm_outcome_loss": [P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P, P],
+    "alodlm_masked_sequence_ids": [P, P, I64, I64, P, P, P],
+    "alodlm_sequence_score": [P, P, P, I64, I64, P, P, P, P],
+    "alodlm_ar_targets": [P, P, I64, I64, P, P],
     "alodlm_gate_bwd_workspace": [I64, I64],
     "alodlm_gate_bwd": [P, P, F32, P, P, P, I64, I64, I64, P, I32, P],
     "alodlm_grad_norm": [P, P, P, P, I64, I64, I32, P, P, P],

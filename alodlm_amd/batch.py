@@ -21,16 +21,19 @@ import torch
 
 from . import _lib
 from .attention import plan_to_device, sparse_plan
+from .layers import DualStreamMask, allowed_pairs, attention_tiles  # noqa: F401 (re-exported)
 
 
 @dataclass
 class Batch:
     """Dual-stream rows of one pack (fields of alodlm/batch.py:12-20).
 
-    ``attention_mask`` is the string ``"dual-stream"`` (the kernels derive the
-    mask from ``boundaries``) unless a dense mask or a range plan was requested.
-    ``row_segment`` and ``ar_target`` are the per-row segment index and
-    next-token target the step kernels use.
+    ``attention_mask`` is a ``layers.DualStreamMask`` (the kernels derive the
+    mask from the segment boundaries; ``.dense()`` builds the reference's
+    boolean [N, N] block-diagonal mask) for the "sdpa" backend, or the range
+    plan of ``attention.plan_to_device`` for the others.  ``kernel_mask`` is
+    the DualStreamMask in either case.  ``row_segment`` and ``ar_target`` are
+    the per-row segment index and next-token target the step kernels use.
     """
     ids: torch.Tensor
     original: torch.Tensor
@@ -44,17 +47,7 @@ class Batch:
     ar_count: int = 0
     pairs: int = 0
     tiles: torch.Tensor = None
-
-
-def allowed_pairs(length, block_size):
-    """Number of (query, key) pairs the dual-stream mask allows in one segment:
-    the causal clean stream plus, per noisy block, its causal self-block and
-    the clean rows of all earlier blocks."""
-    total = length * (length + 1) // 2
-    for left in range(0, length, block_size):
-        width = min(block_size, length - left)
-        total += width * (width + 1) // 2 + width * left
-    return total
+    kernel_mask: DualStreamMask = None
 
 
 def attention_mask(length, block_size, device):
@@ -94,10 +87,16 @@ def block_supervised_counts(labels_host, offsets, block_size):
 
 
 _LOG_THRESHOLD_12 = math.log(0.9) * 12
-# torch's uniform_ gives element i the first draw of Philox subsequence i while
-# its grid (256-thread blocks, at most 8 per compute unit) covers every
-# element: 256 * 8 * 256 on a 256-CU device.
-MAX_SEGMENT_BLOCKS = 1 << 19
+
+
+def max_segment_blocks(device):
+    """Most masking blocks one segment may have on ``device``: torch's
+    ``uniform_`` gives element i the first draw of Philox subsequence i only
+    while its grid (256-thread blocks, max_threads_per_multi_processor / 256
+    of them per compute unit) covers every element, i.e. up to compute units
+    x max threads per compute unit elements (524288 on a 256-CU MI355X)."""
+    props = torch.cuda.get_device_properties(device)
+    return props.multi_processor_count * props.max_threads_per_multi_processor
 
 
 @functools.lru_cache(maxsize=None)
@@ -119,9 +118,11 @@ def _device_draws(block_n, seg_block, block_size, device, generator):
     advanced past every random number the reference's calls would consume.
 
     Returns device tensors (p, count, perm_offset, perms) for batch_build."""
-    if max(b - a for a, b in zip(seg_block, seg_block[1:])) > MAX_SEGMENT_BLOCKS:
-        raise ValueError(f"a segment of more than {MAX_SEGMENT_BLOCKS} masking blocks is "
-                         "not supported")
+    limit = max_segment_blocks(device)
+    if max(b - a for a, b in zip(seg_block, seg_block[1:])) > limit:
+        raise ValueError(f"a segment of more than {limit} masking blocks is not supported on "
+                         "this device (torch's uniform_ would draw them from shared Philox "
+                         "subsequences)")
     gen = _generator_of(device, generator)
     seed, offset = gen.initial_seed(), gen.get_offset()
     nblocks = len(block_n)
@@ -245,34 +246,12 @@ def build_batch(ids, labels, boundaries, block_size, mask_token_id, backend="sdp
     for a, b in zip(offsets, offsets[1:]):
         if b - a >= 2:
             ar_count += int((labels_host[a + 1:b] != -100).sum())
+    kernel_mask = DualStreamMask(offsets, block_size, device, boundaries=out["bounds"],
+                                 row_segment=out["row_segment"])
     if backend == "sdpa":
-        mask = "dual-stream"
+        mask = kernel_mask
     else:
         mask = plan_to_device(sparse_plan([2 * v for v in offsets], block_size, backend), device)
-    pairs = sum(allowed_pairs(b - a, block_size) for a, b in zip(offsets, offsets[1:]))
-    tiles = _to_device(np.asarray(attention_tiles(offsets), dtype=np.int32), device).view(-1, 2)
     return Batch(out["ids"], out["original"], out["positions"], out["masked"], out["prob"],
-                 out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count, pairs,
-                 tiles)
-
-
-TILE_ROWS = 128
-
-
-def attention_tiles(offsets):
-    """(segment, in-segment start) of every 128-row tile of each segment's clean
-    and noisy stream; tiles never cross a stream or a segment.
-
-    Tiles are listed by decreasing start within their stream.  A query tile's
-    key range grows with its start and a key tile's query range shrinks with
-    it, so the forward/dQ kernels (which take the list in order) and the dK/dV
-    kernel (which takes it in reverse) both dispatch their heaviest tiles
-    first."""
-    tiles = []
-    for s, (a, b) in enumerate(zip(offsets, offsets[1:])):
-        length = b - a
-        for stream in (0, length):
-            for start in range(0, length, TILE_ROWS):
-                tiles.append((start, s, stream + start))
-    tiles.sort(key=lambda t: -t[0])
-    return [v for _, s, start in tiles for v in (s, start)]
+                 out["bounds"], mask, out["row_segment"], out["ar_target"], ar_count,
+                 kernel_mask.pairs, kernel_mask.tiles, kernel_mask)

@@ -1,6 +1,8 @@
 // The step objective on [K, rows]: truncated-stick denoising, the sequence
 // score-function actor with the geometric prior and the sampled-history
-// marginal, the autoregressive mean, the metrics, and d(total)/d(gate).
+// marginal, the autoregressive mean, the metrics, and d(total)/d(gate)
+// (total = (denoising + actor + AR) / 2 for the step; denoising + actor for
+// alodlm_outcome_loss, which also writes d(denoising)/d(ce)).
 // (alodlm/loss.py:35-90, alodlm/credit.py:7-40, alodlm/model.py:183-187.)
 //
 // One workgroup of 1024 threads.  Every sum has a fixed order, so the result
@@ -29,7 +31,8 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
                  const float* __restrict__ ce, const float* __restrict__ ar_ce,
                  const int32_t* __restrict__ ar_target, const int64_t* __restrict__ bounds,
                  int64_t S, int64_t rows, int K, float prior_c, float beta_mi, float beta_marg,
-                 float* __restrict__ out, float* __restrict__ dgate, float* __restrict__ ws) {
+                 float* __restrict__ out, float* __restrict__ dgate, float* __restrict__ dce,
+                 float dgate_scale, float* __restrict__ ws) {
   __shared__ float scratch[16];
   __shared__ float qbar_log[OBJ_MAX_DEPTH], prior_log[OBJ_MAX_DEPTH];
   __shared__ float sh_M, sh_wsum;
@@ -79,7 +82,13 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
   // ---- pass 2: logq, credit, denoising, prediction and regularisation -------
   float den = 0.f, pred_sum = 0.f, reg_sum = 0.f;
   for (int64_t r = threadIdx.x; r < rows; r += OBJ_THREADS) {
-    if (!masked[r] || exits[r] < 1 || exits[r] > K) { logq[r] = 0.f; credit[r] = 0.f; continue; }
+    if (!masked[r] || exits[r] < 1 || exits[r] > K) {
+      logq[r] = 0.f;
+      credit[r] = 0.f;
+      if (dce)
+        for (int d = 0; d < K; ++d) dce[(int64_t)d * rows + r] = 0.f;
+      continue;
+    }
     float le[OBJ_MAX_DEPTH];
     stick_logs(gates, rows, r, K, le);
     const int z = exits[r];
@@ -97,7 +106,11 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
       const float stick = (d == z - 1) ? expf(log_surv) : expf(le[d]);
       acc += stick * ce[(int64_t)d * rows + r];
       log_surv -= softplusf(gates[(int64_t)d * rows + r]);
+      // d denoising / d ce[d, r]: the detached stick times the row's weight
+      if (dce) dce[(int64_t)d * rows + r] = w * stick;
     }
+    if (dce)
+      for (int d = z; d < K; ++d) dce[(int64_t)d * rows + r] = 0.f;
     den += w * acc;
   }
   const float DEN = block_sum(den, scratch);
@@ -106,7 +119,7 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
 
   // ---- autoregressive mean over depths (loss.py:12-32; model.py:183-184) ----
   float ar_sum = 0.f, ar_cnt = 0.f;
-  for (int64_t r = threadIdx.x; r < rows; r += OBJ_THREADS) {
+  for (int64_t r = threadIdx.x; ar_target != nullptr && r < rows; r += OBJ_THREADS) {
     if (ar_target[r] < 0) continue;
     ar_cnt += 1.f;
     for (int d = 0; d < K; ++d) ar_sum += ar_ce[(int64_t)d * rows + r];
@@ -143,7 +156,7 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
       int64_t mid = (lo + hi) >> 1;
       if (bounds[mid] <= r) lo = mid; else hi = mid;
     }
-    const float a = 0.5f * seg_R[lo] / sh_M;
+    const float a = dgate_scale * seg_R[lo] / sh_M;
     const int z = exits[r];
     for (int d = 0; d < K; ++d) {
       const float g = gates[(int64_t)d * rows + r];
@@ -197,7 +210,152 @@ extern "C" int alodlm_objective(const float* gates, const int32_t* exits, const 
   ALODLM_CHECK_ARG(rows > 0 && n_segments > 0, "objective: empty input");
   objective_kernel<<<1, OBJ_THREADS, 0, as_stream(stream)>>>(
       gates, exits, masked, mask_prob, ce_full, ar_ce, ar_target, bounds, n_segments, rows,
-      (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, workspace);
+      (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, nullptr, 0.5f,
+      workspace);
   ALODLM_CHECK_LAUNCH("objective");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_outcome_loss(const float* gates, const int32_t* exits, const uint8_t* masked,
+                                   const float* mask_prob, const float* ce_full,
+                                   const int64_t* bounds, int64_t n_segments, int64_t rows,
+                                   int64_t max_depth, float depth_prior_c, float kl_beta_mi,
+                                   float kl_beta_marg, float* out, float* dgate, float* dce,
+                                   float* workspace, void* stream) {
+  ALODLM_CHECK_ARG(max_depth >= 2 && max_depth <= OBJ_MAX_DEPTH,
+                   "outcome_loss: max_depth must be in [2, %d]", OBJ_MAX_DEPTH);
+  ALODLM_CHECK_ARG(rows > 0 && n_segments > 0, "outcome_loss: empty input");
+  objective_kernel<<<1, OBJ_THREADS, 0, as_stream(stream)>>>(
+      gates, exits, masked, mask_prob, ce_full, nullptr, nullptr, bounds, n_segments, rows,
+      (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, dce, 1.0f, workspace);
+  ALODLM_CHECK_LAUNCH("outcome_loss");
+  return ALODLM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Sequence credit primitives (alodlm/credit.py:7-40), one workgroup each.
+// ---------------------------------------------------------------------------
+
+// out[j] = segment of the j-th masked row (rows in order); *count = M.  The
+// segment of row r is the number of segment ends bounds[1..S] at or before r
+// (torch.bucketize(r, bounds[1:], right=True)).
+__global__ void __launch_bounds__(1024)
+masked_sequence_ids_kernel(const uint8_t* __restrict__ masked, const int64_t* __restrict__ bounds,
+                           int64_t S, int64_t rows, int64_t* __restrict__ out,
+                           int64_t* __restrict__ count) {
+  __shared__ int64_t wave_total[16];
+  __shared__ int64_t base;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) base = 0;
+  __syncthreads();
+  for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
+    const int64_t r = r0 + threadIdx.x;
+    const bool m = r < rows && masked[r];
+    const uint64_t ballot = __ballot(m);
+    const int64_t before = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_total[wave] = __popcll(ballot);
+    __syncthreads();
+    int64_t offset = base;
+    for (int w = 0; w < wave; ++w) offset += wave_total[w];
+    if (m) {
+      int64_t lo = 0, hi = S;  // first s with bounds[s + 1] > r
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (bounds[mid + 1] <= r) lo = mid + 1; else hi = mid;
+      }
+      out[offset + before] = lo;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int64_t t = 0;
+      for (int w = 0; w < 16; ++w) t += wave_total[w];
+      base += t;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) count[0] = base;
+}
+
+extern "C" int alodlm_masked_sequence_ids(const uint8_t* masked, const int64_t* bounds,
+                                          int64_t n_segments, int64_t rows, int64_t* out,
+                                          int64_t* count, void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && n_segments >= 1, "masked_sequence_ids: bad shape");
+  masked_sequence_ids_kernel<<<1, 1024, 0, as_stream(stream)>>>(masked, bounds, n_segments, rows,
+                                                               out, count);
+  ALODLM_CHECK_LAUNCH("masked_sequence_ids");
+  return ALODLM_OK;
+}
+
+// value[0] = sum_s R_s * Q_s / n with R_s = sum_{ids = s} credit and
+// Q_s = sum_{ids = s} logq (rows in order within a segment; one wavefront
+// per segment, fixed reduction order); dlogq[i] = R_{ids[i]} / n.
+// `ws` holds 2 * S floats.
+__global__ void __launch_bounds__(1024)
+sequence_score_kernel(const float* __restrict__ credit, const float* __restrict__ logq,
+                      const int64_t* __restrict__ ids, int64_t n, int64_t S,
+                      float* __restrict__ value, float* __restrict__ dlogq,
+                      float* __restrict__ ws) {
+  __shared__ float scratch[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float* seg_R = ws;
+  float* seg_Q = ws + S;
+  for (int64_t s = wave; s < S; s += 16) {
+    float R = 0.f, Q = 0.f;
+    for (int64_t i = lane; i < n; i += 64)
+      if (ids[i] == s) { R += credit[i]; Q += logq[i]; }
+    R = wave_sum(R);
+    Q = wave_sum(Q);
+    if (lane == 0) { seg_R[s] = R; seg_Q[s] = Q; }
+  }
+  __syncthreads();
+  float acc = 0.f;
+  for (int64_t s = threadIdx.x; s < S; s += 1024) acc += seg_R[s] * seg_Q[s];
+  const float total = block_sum(acc, scratch);
+  for (int64_t i = threadIdx.x; i < n; i += 1024) dlogq[i] = seg_R[ids[i]] / (float)n;
+  if (threadIdx.x == 0) value[0] = total / (float)n;
+}
+
+extern "C" int alodlm_sequence_score(const float* credit, const float* logq, const int64_t* ids,
+                                     int64_t n, int64_t sequence_count, float* value,
+                                     float* dlogq, float* workspace, void* stream) {
+  ALODLM_CHECK_ARG(n > 0 && sequence_count >= 1, "sequence_score: bad shape");
+  sequence_score_kernel<<<1, 1024, 0, as_stream(stream)>>>(credit, logq, ids, n, sequence_count,
+                                                          value, dlogq, workspace);
+  ALODLM_CHECK_LAUNCH("sequence_score");
+  return ALODLM_OK;
+}
+
+// AR targets of alodlm/loss.py:12-32 over the dual-stream rows of a pack:
+// for the segment with dual-stream rows [start, end) and L = (end - start)/2,
+// clean row start + i (i < L - 1) predicts labels[start/2 + 1 + i]; every
+// other row, and ignored labels (-100), get -1.
+__global__ void ar_targets_kernel(const int64_t* __restrict__ labels,
+                                  const int64_t* __restrict__ bounds, int64_t S, int64_t rows,
+                                  int32_t* __restrict__ target) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  int64_t lo = 0, hi = S;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (bounds[mid + 1] <= r) lo = mid + 1; else hi = mid;
+  }
+  int32_t t = -1;
+  if (lo < S) {
+    const int64_t start = bounds[lo], L = (bounds[lo + 1] - start) / 2, i = r - start;
+    if (L >= 2 && i < L - 1) {
+      const int64_t label = labels[start / 2 + 1 + i];
+      if (label != -100) t = (int32_t)label;
+    }
+  }
+  target[r] = t;
+}
+
+extern "C" int alodlm_ar_targets(const int64_t* labels, const int64_t* bounds, int64_t n_segments,
+                                 int64_t rows, int32_t* target, void* stream) {
+  ALODLM_CHECK_ARG(rows >= 0 && n_segments >= 1, "ar_targets: bad shape");
+  if (rows == 0) return ALODLM_OK;
+  ar_targets_kernel<<<ceil_div_u(rows, 256), 256, 0, as_stream(stream)>>>(labels, bounds,
+                                                                         n_segments, rows, target);
+  ALODLM_CHECK_LAUNCH("ar_targets");
   return ALODLM_OK;
 }

@@ -15,26 +15,46 @@
 #define ROPE_WAVES 4
 #define ROPE_MAX_T 2  // pairs per lane: dh/2 <= 128
 
-template <typename T>
+// The rotation of element pair (i, i + dh/2) of a row: cos/sin of the first
+// and of the second element.  From positions, both halves share the angle
+// pos * inv_freq[i] ([tf] modeling_qwen3.py:126-137 builds cat(freqs, freqs));
+// from caller tables ([rows, dh] in the storage type, alodlm/model.py:41-46)
+// each element takes its own entry.
+template <typename T, bool TAB>
+__device__ __forceinline__ void rope_pair(const int64_t* positions, const float* inv_freq,
+                                          const T* cos_tab, const T* sin_tab, int64_t row,
+                                          int i, int dh, float& ca, float& cb, float& sa,
+                                          float& sb) {
+  if (TAB) {
+    const int64_t base = row * dh;
+    ca = Elem<T>::load(cos_tab, base + i); cb = Elem<T>::load(cos_tab, base + i + dh / 2);
+    sa = Elem<T>::load(sin_tab, base + i); sb = Elem<T>::load(sin_tab, base + i + dh / 2);
+  } else {
+    const float ang = (float)positions[row] * inv_freq[i];
+    ca = cb = Elem<T>::round(cosf(ang));
+    sa = sb = Elem<T>::round(sinf(ang));
+  }
+}
+
+template <typename T, bool TAB>
 __global__ void __launch_bounds__(64 * ROPE_WAVES)
 qknorm_rope_fwd_kernel(const T* __restrict__ qkv, const T* __restrict__ wq, const T* __restrict__ wk,
                        const int64_t* __restrict__ positions, const float* __restrict__ inv_freq,
+                       const T* __restrict__ cos_tab, const T* __restrict__ sin_tab,
                        T* __restrict__ q_out, T* __restrict__ k_out, int64_t rows, int nq, int nkv,
                        int dh, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * ROPE_WAVES + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int half = dh / 2;
-  const float pos = (float)positions[row];
-  float cs[ROPE_MAX_T], sn[ROPE_MAX_T];
+  float csa[ROPE_MAX_T], csb[ROPE_MAX_T], sna[ROPE_MAX_T], snb[ROPE_MAX_T];
   float wqa[ROPE_MAX_T], wqb[ROPE_MAX_T], wka[ROPE_MAX_T], wkb[ROPE_MAX_T];
 #pragma unroll
   for (int t = 0; t < ROPE_MAX_T; ++t) {
     const int i = lane + 64 * t;
     if (i < half) {
-      const float ang = pos * inv_freq[i];
-      cs[t] = Elem<T>::round(cosf(ang));
-      sn[t] = Elem<T>::round(sinf(ang));
+      rope_pair<T, TAB>(positions, inv_freq, cos_tab, sin_tab, row, i, dh, csa[t], csb[t],
+                        sna[t], snb[t]);
       wqa[t] = Elem<T>::load(wq, i); wqb[t] = Elem<T>::load(wq, i + half);
       wka[t] = Elem<T>::load(wk, i); wkb[t] = Elem<T>::load(wk, i + half);
     }
@@ -64,8 +84,8 @@ qknorm_rope_fwd_kernel(const T* __restrict__ qkv, const T* __restrict__ wq, cons
       if (i < half) {
         const float a = Elem<T>::round((is_q ? wqa[t] : wka[t]) * Elem<T>::round(xa[t] * r));
         const float b = Elem<T>::round((is_q ? wqb[t] : wkb[t]) * Elem<T>::round(xb[t] * r));
-        Elem<T>::store(dst, i, Elem<T>::round(a * cs[t]) + Elem<T>::round(-b * sn[t]));
-        Elem<T>::store(dst, i + half, Elem<T>::round(b * cs[t]) + Elem<T>::round(a * sn[t]));
+        Elem<T>::store(dst, i, Elem<T>::round(a * csa[t]) + Elem<T>::round(-b * sna[t]));
+        Elem<T>::store(dst, i + half, Elem<T>::round(b * csb[t]) + Elem<T>::round(a * snb[t]));
       }
     }
   }
@@ -75,11 +95,12 @@ qknorm_rope_fwd_kernel(const T* __restrict__ qkv, const T* __restrict__ wq, cons
 // norm-weight partials stay in registers; the block writes one partial row
 // [q grads (dh) | k grads (dh)].
 
-template <typename T>
+template <typename T, bool TAB>
 __global__ void __launch_bounds__(64 * ROPE_WAVES)
 qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const T* __restrict__ qkv,
                        const T* __restrict__ wq, const T* __restrict__ wk,
                        const int64_t* __restrict__ positions, const float* __restrict__ inv_freq,
+                       const T* __restrict__ cos_tab, const T* __restrict__ sin_tab,
                        T* __restrict__ dqkv, float* __restrict__ partial, int64_t rows, int nq,
                        int nkv, int dh, float eps, int64_t rows_per_block) {
   extern __shared__ float lds[];  // [ROPE_WAVES][2*dh]
@@ -100,17 +121,14 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
   }
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += ROPE_WAVES) {
-    const float pos = (float)positions[row];
-    float cs[ROPE_MAX_T], sn[ROPE_MAX_T];
+    float csa[ROPE_MAX_T], csb[ROPE_MAX_T], sna[ROPE_MAX_T], snb[ROPE_MAX_T];
 #pragma unroll
     for (int t = 0; t < ROPE_MAX_T; ++t) {
       const int i = lane + 64 * t;
-      cs[t] = sn[t] = 0.f;
-      if (i < half) {
-        const float ang = pos * inv_freq[i];
-        cs[t] = Elem<T>::round(cosf(ang));
-        sn[t] = Elem<T>::round(sinf(ang));
-      }
+      csa[t] = csb[t] = sna[t] = snb[t] = 0.f;
+      if (i < half)
+        rope_pair<T, TAB>(positions, inv_freq, cos_tab, sin_tab, row, i, dh, csa[t], csb[t],
+                          sna[t], snb[t]);
     }
     for (int head = 0; head < nq + nkv; ++head) {
       const bool is_q = head < nq;
@@ -126,8 +144,8 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
           xa[t] = Elem<T>::load(x, i);
           xb[t] = Elem<T>::load(x, i + half);
           const float go = Elem<T>::load(g, i), gh = Elem<T>::load(g, i + half);
-          ta[t] = go * cs[t] + gh * sn[t];   // d/d t[i]
-          tb[t] = gh * cs[t] - go * sn[t];   // d/d t[i + half]
+          ta[t] = go * csa[t] + gh * snb[t];   // d/d t[i]
+          tb[t] = gh * csb[t] - go * sna[t];   // d/d t[i + half]
           ss += xa[t] * xa[t] + xb[t] * xb[t];
           s += ta[t] * (is_q ? wqa[t] : wka[t]) * xa[t] + tb[t] * (is_q ? wqb[t] : wkb[t]) * xb[t];
         }
@@ -350,10 +368,10 @@ extern "C" int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const voi
           (bf16_t*)q_out, (bf16_t*)k_out, rows, (int)nq, (int)nkv, eps);
       break;
     }
-    qknorm_rope_fwd_kernel<T><<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
-                                as_stream(stream)>>>(
-        (const T*)qkv, (const T*)wq, (const T*)wk, positions, inv_freq, (T*)q_out, (T*)k_out,
-        rows, (int)nq, (int)nkv, (int)dh, eps);
+    qknorm_rope_fwd_kernel<T, false><<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
+                                       as_stream(stream)>>>(
+        (const T*)qkv, (const T*)wq, (const T*)wk, positions, inv_freq, nullptr, nullptr,
+        (T*)q_out, (T*)k_out, rows, (int)nq, (int)nkv, (int)dh, eps);
   });
   ALODLM_CHECK_LAUNCH("qknorm_rope_fwd");
   return ALODLM_OK;
@@ -387,14 +405,137 @@ extern "C" int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void
           (int)nkv, eps, rpb);
       break;
     }
-    qknorm_rope_bwd_kernel<T><<<(unsigned)nparts, 64 * ROPE_WAVES,
-                                ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
+    qknorm_rope_bwd_kernel<T, false><<<(unsigned)nparts, 64 * ROPE_WAVES,
+                                       ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
         (const T*)dq, (const T*)dk, (const T*)qkv, (const T*)wq, (const T*)wk, positions,
-        inv_freq, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps, rpb);
+        inv_freq, nullptr, nullptr, (T*)dqkv, workspace, rows, (int)nq, (int)nkv, (int)dh, eps,
+        rpb);
   });
   ALODLM_CHECK_LAUNCH("qknorm_rope_bwd");
   float* tmp = workspace + nparts * 2 * dh;
   rc = column_reduce(workspace, nparts, 2 * dh, 0, dh, dwq_accum, tmp, st);
   if (rc) return rc;
   return column_reduce(workspace, nparts, 2 * dh, dh, dh, dwk_accum, tmp, st);
+}
+
+// ---------------------------------------------------------------------------
+// Table-driven forms (alodlm/model.py:41-46 takes cos/sin tables [rows, dh]):
+// q/k norm + rotary on the projections, and the rotary alone.
+// ---------------------------------------------------------------------------
+extern "C" int alodlm_qknorm_rotary_fwd(const void* qkv, const void* wq, const void* wk,
+                                        const void* cos_tab, const void* sin_tab, void* q_out,
+                                        void* k_out, int64_t rows, int64_t nq, int64_t nkv,
+                                        int64_t dh, float eps, int dtype, void* stream) {
+  int rc = check_rope(rows, nq, nkv, dh);
+  if (rc) return rc;
+  if (rows == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    qknorm_rope_fwd_kernel<T, true><<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
+                                      as_stream(stream)>>>(
+        (const T*)qkv, (const T*)wq, (const T*)wk, nullptr, nullptr, (const T*)cos_tab,
+        (const T*)sin_tab, (T*)q_out, (T*)k_out, rows, (int)nq, (int)nkv, (int)dh, eps);
+  });
+  ALODLM_CHECK_LAUNCH("qknorm_rotary_fwd");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_qknorm_rotary_bwd(const void* dq, const void* dk, const void* qkv,
+                                        const void* wq, const void* wk, const void* cos_tab,
+                                        const void* sin_tab, void* dqkv, float* dwq_accum,
+                                        float* dwk_accum, float* workspace, int64_t rows,
+                                        int64_t nq, int64_t nkv, int64_t dh, float eps, int dtype,
+                                        void* stream) {
+  int rc = check_rope(rows, nq, nkv, dh);
+  if (rc) return rc;
+  if (rows == 0) return ALODLM_OK;
+  const int64_t rpb = bwd_rows_per_block(rows);
+  const int64_t nparts = (rows + rpb - 1) / rpb;
+  hipStream_t st = as_stream(stream);
+  ALODLM_DISPATCH(dtype, T, {
+    qknorm_rope_bwd_kernel<T, true><<<(unsigned)nparts, 64 * ROPE_WAVES,
+                                      ROPE_WAVES * 2 * dh * sizeof(float), st>>>(
+        (const T*)dq, (const T*)dk, (const T*)qkv, (const T*)wq, (const T*)wk, nullptr, nullptr,
+        (const T*)cos_tab, (const T*)sin_tab, (T*)dqkv, workspace, rows, (int)nq, (int)nkv,
+        (int)dh, eps, rpb);
+  });
+  ALODLM_CHECK_LAUNCH("qknorm_rotary_bwd");
+  float* tmp = workspace + nparts * 2 * dh;
+  rc = column_reduce(workspace, nparts, 2 * dh, 0, dh, dwq_accum, tmp, st);
+  if (rc) return rc;
+  return column_reduce(workspace, nparts, 2 * dh, dh, dh, dwk_accum, tmp, st);
+}
+
+// out = x * cos + rotate_half(x) * sin for every head of a row, with the
+// reference's three roundings (product, product, sum); BWD applies the
+// transpose: dx[i] = dy[i] cos[i] + dy[i+h] sin[i+h],
+// dx[i+h] = dy[i+h] cos[i+h] - dy[i] sin[i], each product rounded and the
+// sum rounded, as the reference's bf16 autograd accumulates them (float32:
+// every product and the sum rounded once, no contraction).
+template <typename T, bool BWD>
+__global__ void __launch_bounds__(256)
+rotary_kernel(const T* __restrict__ x, const T* __restrict__ cos_tab,
+              const T* __restrict__ sin_tab, T* __restrict__ out, int64_t rows, int heads,
+              int dh) {
+  // products and sums stay separately rounded, as the reference evaluates
+  // them (no fused multiply-add)
+#pragma clang fp contract(off)
+  const int half = dh / 2;
+  const int64_t n = rows * heads * half;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(e % half);
+    const int64_t rh = e / half;          // row * heads + head
+    const int64_t row = rh / heads;
+    const float a = Elem<T>::load(x, rh * dh + i), b = Elem<T>::load(x, rh * dh + i + half);
+    const float ca = Elem<T>::load(cos_tab, row * dh + i);
+    const float cb = Elem<T>::load(cos_tab, row * dh + i + half);
+    const float sa = Elem<T>::load(sin_tab, row * dh + i);
+    const float sb = Elem<T>::load(sin_tab, row * dh + i + half);
+    float lo, hi;
+    if (BWD) {
+      lo = Elem<T>::round(a * ca) + Elem<T>::round(b * sb);
+      hi = Elem<T>::round(b * cb) + Elem<T>::round(-a * sa);
+    } else {
+      lo = Elem<T>::round(a * ca) + Elem<T>::round(-b * sa);
+      hi = Elem<T>::round(b * cb) + Elem<T>::round(a * sb);
+    }
+    Elem<T>::store(out, rh * dh + i, lo);
+    Elem<T>::store(out, rh * dh + i + half, hi);
+  }
+}
+
+static int rotary_launch(const void* x, const void* cos_tab, const void* sin_tab, void* out,
+                         int64_t rows, int64_t heads, int64_t dh, int dtype, bool bwd,
+                         hipStream_t st) {
+  ALODLM_CHECK_ARG(rows >= 0 && heads > 0 && dh > 0 && dh % 2 == 0,
+                   "rotary: head_dim must be even and the head count positive");
+  if (rows == 0) return ALODLM_OK;
+  const int64_t n = rows * heads * (dh / 2);
+  const unsigned grid = (unsigned)(n / 256 + 1 < 65536 ? n / 256 + 1 : 65536);
+  ALODLM_DISPATCH(dtype, T, {
+    if (bwd)
+      rotary_kernel<T, true><<<grid, 256, 0, st>>>((const T*)x, (const T*)cos_tab,
+                                                   (const T*)sin_tab, (T*)out, rows, (int)heads,
+                                                   (int)dh);
+    else
+      rotary_kernel<T, false><<<grid, 256, 0, st>>>((const T*)x, (const T*)cos_tab,
+                                                    (const T*)sin_tab, (T*)out, rows, (int)heads,
+                                                    (int)dh);
+  });
+  ALODLM_CHECK_LAUNCH("rotary");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_rotary_fwd(const void* x, const void* cos_tab, const void* sin_tab,
+                                 void* out, int64_t rows, int64_t heads, int64_t dh, int dtype,
+                                 void* stream) {
+  return rotary_launch(x, cos_tab, sin_tab, out, rows, heads, dh, dtype, false,
+                       as_stream(stream));
+}
+
+extern "C" int alodlm_rotary_bwd(const void* dout, const void* cos_tab, const void* sin_tab,
+                                 void* dx, int64_t rows, int64_t heads, int64_t dh, int dtype,
+                                 void* stream) {
+  return rotary_launch(dout, cos_tab, sin_tab, dx, rows, heads, dh, dtype, true,
+                       as_stream(stream));
 }

@@ -31,8 +31,9 @@ import math
 import torch
 
 from . import _lib
-from ._lib import EPI_ACCUM, EPI_RESIDUAL, EPI_STORE, call, ptr, query
+from ._lib import EPI_ACCUM, call, ptr, query
 from .batch import build_batch
+from .layers import Kernels, LayerGrads, LayerWeights, Rope
 
 METRIC_NAMES = ("denoising", "actor", "sampled_mean_depth", "prediction_cost",
                 "regularization_cost", "profile_mean_depth", "first_pass_halt_probability")
@@ -116,23 +117,23 @@ class Arena:
                    for n, p in zip(self.names, self.params))
 
 
-class _Layer:
-    """Views of one decoder layer's weights (and gradients) in an arena buffer."""
-
-    def __init__(self, arena, buf, index):
-        d = arena.dims
-        pre = f"backbone.model.layers.{index}."
-        off = arena.offsets
-        q = off[pre + "self_attn.q_proj.weight"]
-        self.wqkv = buf[q:q + d.qkv_width * d.hidden].view(d.qkv_width, d.hidden)
-        g = off[pre + "mlp.gate_proj.weight"]
-        self.wgu = buf[g:g + 2 * d.intermediate * d.hidden].view(2 * d.intermediate, d.hidden)
-        self.wo = arena.view(buf, pre + "self_attn.o_proj.weight")
-        self.wd = arena.view(buf, pre + "mlp.down_proj.weight")
-        self.ln1 = arena.view(buf, pre + "input_layernorm.weight")
-        self.ln2 = arena.view(buf, pre + "post_attention_layernorm.weight")
-        self.qn = arena.view(buf, pre + "self_attn.q_norm.weight")
-        self.kn = arena.view(buf, pre + "self_attn.k_norm.weight")
+def _layer_views(arena, buf, index, grads=False):
+    """Views of one decoder layer's weights (or their gradients) in an arena
+    buffer: q|k|v and gate|up are adjacent there, so each pair is one matrix."""
+    d = arena.dims
+    pre = f"backbone.model.layers.{index}."
+    off = arena.offsets
+    q = off[pre + "self_attn.q_proj.weight"]
+    g = off[pre + "mlp.gate_proj.weight"]
+    views = (buf[q:q + d.qkv_width * d.hidden].view(d.qkv_width, d.hidden),
+             arena.view(buf, pre + "self_attn.o_proj.weight"),
+             buf[g:g + 2 * d.intermediate * d.hidden].view(2 * d.intermediate, d.hidden),
+             arena.view(buf, pre + "mlp.down_proj.weight"),
+             arena.view(buf, pre + "input_layernorm.weight"),
+             arena.view(buf, pre + "post_attention_layernorm.weight"),
+             arena.view(buf, pre + "self_attn.q_norm.weight"),
+             arena.view(buf, pre + "self_attn.k_norm.weight"))
+    return LayerGrads(*views) if grads else LayerWeights(*views)
 
 
 class _TransposedWeights:
@@ -167,26 +168,23 @@ class _TransposedWeights:
             call("alodlm_transpose", ptr(src), ptr(dst), rows, cols, code, stream)
 
 
-class StepEngine:
+class StepEngine(Kernels):
     """Runs the ALoDLM step of one model on its GPU (see the module docstring)."""
 
     def __init__(self, model):
         backbone = model.backbone
         self.model = model
         self.cfg = model.config
-        self.dims = Dims.from_hf(backbone.config)
         params = list(model.named_parameters())
-        self.device = params[0][1].device
-        self.dtype = params[0][1].dtype
-        if self.device.type != "cuda":
+        device, dtype = params[0][1].device, params[0][1].dtype
+        if device.type != "cuda":
             raise ValueError("the HIP training step needs the model on a CUDA (ROCm) device")
-        self.code = _lib.dtype_code(self.dtype)
-        _lib.load()
+        super().__init__(Dims.from_hf(backbone.config), dtype, device)
         self.arena = Arena(params, self.dims, self.device, self.dtype)
         d = self.dims
         if d.head_dim % 2:
             raise ValueError("head_dim must be even for the rotary embedding")
-        self.layers = [_Layer(self.arena, self.arena.flat, i) for i in range(d.layers)]
+        self.layers = [_layer_views(self.arena, self.arena.flat, i) for i in range(d.layers)]
         a = self.arena
         self.embed = a.view(a.flat, "backbone.model.embed_tokens.weight")
         self.final_norm = a.view(a.flat, "backbone.model.norm.weight")
@@ -242,153 +240,15 @@ class StepEngine:
         self._keep_rows = N
         return self._keep
 
-    # ------------------------------------------------------------------ helpers
-    def _stream(self):
-        return _lib.stream_handle(self.device)
-
-    def _empty(self, *shape, dtype=None):
-        return torch.empty(*shape, dtype=dtype or self.dtype, device=self.device)
-
-    def _gemm(self, A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=EPI_STORE, R=None,
-              ldr=0):
-        ws = None
-        need = query("alodlm_gemm_workspace", M, N, K, epi, self.code)
-        if need:
-            ws = self._workspace(need)
-        call("alodlm_gemm", ptr(A), lda, a_k, ptr(B), ldb, b_k, ptr(C), ldc, ptr(R), ldr, M, N, K,
-             alpha, epi, self.code, ptr(ws), self._stream())
-
-    def _attention_fwd(self, q, k, v, o, lse, b):
-        d = self.dims
-        call("alodlm_attention_fwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(b.boundaries),
-             ptr(b.row_segment), ptr(b.tiles), b.tiles.shape[0], ptr(o), ptr(lse), q.shape[0],
-             d.heads, d.kv_heads, d.head_dim, self.cfg.block_size, self.code, self._stream())
-
-    def _attention_bwd(self, q, k, v, o, lse, do, dq, dk, dv, b):
-        d, N = self.dims, q.shape[0]
-        ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads, d.kv_heads,
-                                   d.head_dim, b.tiles.shape[0]))
-        call("alodlm_attention_bwd", ptr(q), ptr(k), ptr(v), d.qkv_width, ptr(o), ptr(lse),
-             ptr(do), ptr(b.boundaries), ptr(b.row_segment), ptr(b.tiles), b.tiles.shape[0],
-             ptr(dq), ptr(dk), ptr(dv), d.qkv_width, ptr(ws), N, d.heads, d.kv_heads,
-             d.head_dim, self.cfg.block_size, self.code, self._stream())
-
-    def _attention_fwd_flops(self, q, k, v, o, lse, b):
-        """Algorithmic forward FLOPs: 4*dh per allowed (q, k) pair and head."""
-        return 4.0 * self.dims.head_dim * self.dims.heads * b.pairs
-
-    def _attention_bwd_flops(self, q, k, v, o, lse, do, dq, dk, dv, b):
-        """Algorithmic backward FLOPs: 8*dh per allowed pair and head."""
-        return 8.0 * self.dims.head_dim * self.dims.heads * b.pairs
-
-    def _workspace(self, n):
-        if self._ws is None or self._ws.numel() < n:
-            self._ws = torch.empty(max(n, 1), dtype=torch.float32, device=self.device)
-        return self._ws
-
     # ------------------------------------------------------------------ layer fwd/bwd
     def _layer_fwd(self, li, x, b, save):
-        d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
-        w = self.layers[li]
-        H, W, I = d.hidden, d.qkv_width, d.intermediate
-        h1 = self._empty(N, H)
-        rstd1 = self._empty(N, dtype=torch.float32)
-        call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), ptr(rstd1), N, H, d.eps, c, st)
-        qkv = self._empty(N, W)
-        self._gemm(h1, H, 1, w.wqkv_t, W, 0, qkv, W, N, W, H)
-        keep_rot, keep_norm = self._keep_now if save is not None else (False, False)
-        if not keep_norm:
-            h1 = None
-        q = self._empty(N, d.heads * d.head_dim)
-        k = self._empty(N, d.kv_heads * d.head_dim)
-        call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
-             ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
-        o = self._empty(N, d.heads * d.head_dim)
-        lse = self._empty(d.heads, N, dtype=torch.float32)
-        v = qkv[:, (d.heads + d.kv_heads) * d.head_dim:]
-        self._attention_fwd(q, k, v, o, lse, b)
-        if not keep_rot:
-            q = k = None
-        x1 = self._empty(N, H)
-        self._gemm(o, d.heads * d.head_dim, 1, w.wo_t, H, 0, x1, H, N, H,
-                   d.heads * d.head_dim, epi=EPI_RESIDUAL, R=x, ldr=H)
-        h2 = self._empty(N, H)
-        rstd2 = self._empty(N, dtype=torch.float32)
-        call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), ptr(rstd2), N, H, d.eps, c, st)
-        gu = self._empty(N, 2 * I)
-        self._gemm(h2, H, 1, w.wgu_t, 2 * I, 0, gu, 2 * I, N, 2 * I, H)
-        if not keep_norm:
-            h2 = None
-        act = self._empty(N, I)
-        call("alodlm_swiglu_fwd", ptr(gu), ptr(act), N, I, c, st)
-        y = self._empty(N, H)
-        self._gemm(act, I, 1, w.wd_t, H, 0, y, H, N, H, I, epi=EPI_RESIDUAL, R=x1, ldr=H)
-        if save is not None:
-            save.append((li, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2))
-        return y
+        return self.layer_fwd(self.layers[li], x, b.kernel_mask, self._rope, save,
+                              keep=self._keep_now if save is not None else (False, False), tag=li)
 
     def _layer_bwd(self, dy, saved, b, g):
-        li, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2 = saved
-        d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
-        w, gw = self.layers[li], self.grad_layers[li]
-        H, W, I = d.hidden, d.qkv_width, d.intermediate
-        QD = d.heads * d.head_dim
-        # ---- MLP: y = x1 + act . Wd^T  (the SwiGLU backward also rewrites act)
-        dact = self._empty(N, I)
-        self._gemm(dy, H, 1, w.wd, I, 0, dact, I, N, I, H)
-        act = self._empty(N, I)
-        dgu = self._empty(N, 2 * I)
-        call("alodlm_swiglu_bwd", ptr(dact), ptr(gu), ptr(dgu), ptr(act), N, I, c, st)
-        del dact
-        self._gemm(dy, H, 0, act, I, 0, gw.wd, I, H, I, N, epi=EPI_ACCUM)
-        del act
-        if h2 is None:
-            h2 = self._empty(N, H)
-            call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
-        dh2 = self._empty(N, H)
-        self._gemm(dgu, 2 * I, 1, w.wgu, H, 0, dh2, H, N, H, 2 * I)
-        self._gemm(dgu, 2 * I, 0, h2, H, 0, gw.wgu, H, 2 * I, H, N, epi=EPI_ACCUM)
-        del dgu, h2
-        dx1 = self._empty(N, H)
-        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
-        call("alodlm_rmsnorm_bwd", ptr(dh2), ptr(x1), ptr(rstd2), ptr(w.ln2), ptr(dy), ptr(dx1),
-             ptr(gw.ln2), ptr(ws), N, H, c, st)
-        del dh2
-        # ---- attention: x1 = x + o . Wo^T
-        do = self._empty(N, QD)
-        self._gemm(dx1, H, 1, w.wo, QD, 0, do, QD, N, QD, H)
-        self._gemm(dx1, H, 0, o, QD, 0, gw.wo, QD, H, QD, N, epi=EPI_ACCUM)
-        if q is None:
-            q = self._empty(N, QD)
-            k = self._empty(N, d.kv_heads * d.head_dim)
-            call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(b.positions),
-                 ptr(self.inv_freq), ptr(q), ptr(k), N, d.heads, d.kv_heads, d.head_dim, d.eps,
-                 c, st)
-        dq = self._empty(N, QD)
-        dk = self._empty(N, d.kv_heads * d.head_dim)
-        dqkv = self._empty(N, W)
-        v = qkv[:, (d.heads + d.kv_heads) * d.head_dim:]
-        dv = dqkv[:, (d.heads + d.kv_heads) * d.head_dim:]
-        self._attention_bwd(q, k, v, o, lse, do, dq, dk, dv, b)
-        del q, k, do
-        ws = self._workspace(query("alodlm_qknorm_rope_bwd_workspace", N, d.heads, d.kv_heads,
-                                   d.head_dim))
-        call("alodlm_qknorm_rope_bwd", ptr(dq), ptr(dk), ptr(qkv), ptr(w.qn), ptr(w.kn),
-             ptr(b.positions), ptr(self.inv_freq), ptr(dqkv), ptr(gw.qn), ptr(gw.kn), ptr(ws), N,
-             d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
-        del dq, dk
-        if h1 is None:
-            h1 = self._empty(N, H)
-            call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, N, H, d.eps, c, st)
-        dh1 = self._empty(N, H)
-        self._gemm(dqkv, W, 1, w.wqkv, H, 0, dh1, H, N, H, W)
-        self._gemm(dqkv, W, 0, h1, H, 0, gw.wqkv, H, W, H, N, epi=EPI_ACCUM)
-        del dqkv, h1
-        dx = self._empty(N, H)
-        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
-        call("alodlm_rmsnorm_bwd", ptr(dh1), ptr(x), ptr(rstd1), ptr(w.ln1), ptr(dx1), ptr(dx),
-             ptr(gw.ln1), ptr(ws), N, H, c, st)
-        return dx
+        li = saved[0]
+        return self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li], b.kernel_mask,
+                              self._rope)
 
     # ------------------------------------------------------------------ step
     def forward(self, ids, labels, boundaries, need_grad, exit_uniforms=None, draws=None,
@@ -409,6 +269,7 @@ class StepEngine:
         labels = pin(labels).to(self.device, non_blocking=True)
         b = build_batch(ids, labels, boundaries, cfg.block_size, cfg.mask_token_id,
                         generator=generator, draws=draws, labels_host=labels_host)
+        self._rope = Rope(positions=b.positions, inv_freq=self.inv_freq)
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         S = b.boundaries.numel() - 1
         saves = [] if need_grad else None
@@ -507,7 +368,7 @@ class StepEngine:
         b = state["batch"]
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
-        self.grad_layers = [_Layer(self.arena, grads, i) for i in range(d.layers)]
+        self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
         a = self.arena
         g_embed = a.view(grads, "backbone.model.embed_tokens.weight")
         g_norm = a.view(grads, "backbone.model.norm.weight")

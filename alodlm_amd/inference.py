@@ -37,8 +37,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, query
-
-TILE_ROWS = 128
+from .layers import Rope, WindowMask
 
 
 @dataclass
@@ -149,34 +148,6 @@ class PrefixCache:
         self.length += n
 
 
-class _WindowLayout:
-    """Synthetic dual-stream layout for one window's attention.
-
-    The window's W query rows are rows [P, P + W) of a segment of length
-    L = P + W whose clean stream is the cache.  The MFMA kernels take 128-row
-    query tiles from ``base`` = floor(P / 128) * 128, so the query buffer also
-    holds rows [base, P) (zeros; their outputs are ignored); the reference
-    kernels take any row, so ``base`` = P there.  Segment row r is buffer row
-    r - base for queries and cache row r for keys (pointers offset by base).
-    """
-
-    def __init__(self, prefix, window, tiled, device):
-        self.prefix, self.window = prefix, window
-        L = prefix + window
-        self.base = (prefix // TILE_ROWS) * TILE_ROWS if tiled else prefix
-        self.q_rows = L - self.base          # query / output buffer rows
-        self.q_off = prefix - self.base      # first window row in those buffers
-        self.bounds = torch.tensor([-self.base, 2 * L - self.base], dtype=torch.int64,
-                                   device=device)
-        self.row_segment = torch.zeros(self.q_rows, dtype=torch.int32, device=device)
-        if tiled:
-            starts = list(range(self.base, L, TILE_ROWS))[::-1]
-            self.tiles = torch.tensor([v for s in starts for v in (0, s)], dtype=torch.int32,
-                                      device=device).view(-1, 2)
-        else:
-            self.tiles = None
-
-
 class Decoder:
     """Adaptive recurrent decoding (alodlm/inference.py:66-246) on the HIP kernels."""
 
@@ -203,43 +174,9 @@ class Decoder:
         """One decoder layer over the window rows (alodlm/model.py:49-76), with
         the prefix K/V of ``key``; the window's K/V land in the cache rows
         [P, P + W) of that key."""
-        d, st, c = e.dims, e._stream(), e.code
-        w = e.layers[li]
-        W_ = x.shape[0]
-        H, QW, I = d.hidden, d.qkv_width, d.intermediate
-        QD, KD = d.heads * d.head_dim, d.kv_heads * d.head_dim
-        esize = x.element_size()
-        h1 = e._empty(W_, H)
-        call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, W_, H, d.eps, c, st)
-        qkv = e._empty(W_, QW)
-        e._gemm(h1, H, 1, w.wqkv_t, QW, 0, qkv, QW, W_, QW, H)
         kbuf, vbuf = cache.buffers(key)
-        q_all = e._empty(lay.q_rows, QD)
-        if lay.q_off:
-            q_all[:lay.q_off].zero_()
-        call("alodlm_qknorm_rope_fwd", ptr(qkv), ptr(w.qn), ptr(w.kn), ptr(positions),
-             ptr(e.inv_freq), ptr(q_all) + lay.q_off * QD * esize,
-             ptr(kbuf) + lay.prefix * KD * esize, W_, d.heads, d.kv_heads, d.head_dim, d.eps, c, st)
-        vbuf[lay.prefix:lay.prefix + W_].view(W_, KD).copy_(qkv[:, QD + KD:])
-        o_all = e._empty(lay.q_rows, QD)
-        lse = e._empty(d.heads, lay.q_rows, dtype=torch.float32)
-        shift = lay.base * KD * esize
-        call("alodlm_attention_fwd", ptr(q_all), ptr(kbuf) + shift, ptr(vbuf) + shift, KD,
-             ptr(lay.bounds), ptr(lay.row_segment), ptr(lay.tiles),
-             0 if lay.tiles is None else lay.tiles.shape[0], ptr(o_all), ptr(lse), lay.q_rows,
-             d.heads, d.kv_heads, d.head_dim, self.model.config.block_size, c, st)
-        o = o_all[lay.q_off:]
-        x1 = e._empty(W_, H)
-        e._gemm(o, QD, 1, w.wo_t, H, 0, x1, H, W_, H, QD, epi=_lib.EPI_RESIDUAL, R=x, ldr=H)
-        h2 = e._empty(W_, H)
-        call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, W_, H, d.eps, c, st)
-        gu = e._empty(W_, 2 * I)
-        e._gemm(h2, H, 1, w.wgu_t, 2 * I, 0, gu, 2 * I, W_, 2 * I, H)
-        act = e._empty(W_, I)
-        call("alodlm_swiglu_fwd", ptr(gu), ptr(act), W_, I, c, st)
-        y = e._empty(W_, H)
-        e._gemm(act, I, 1, w.wd_t, H, 0, y, H, W_, H, I, epi=_lib.EPI_RESIDUAL, R=x1, ldr=H)
-        return y
+        return e.layer_window(e.layers[li], x, Rope(positions=positions, inv_freq=e.inv_freq),
+                              lay, kbuf, vbuf)
 
     def _window(self, ids, positions, cache, mask_rows, config, logical_mask_positions):
         """Run one window (alodlm/inference.py:71-146).
@@ -261,7 +198,7 @@ class Decoder:
         cache._bind(d.kv_heads, d.head_dim, e.dtype, dev)
         cache.reserve(P + length)
         tiled = e.dtype == torch.bfloat16 and d.head_dim in (64, 128)
-        lay = _WindowLayout(P, length, tiled, dev)
+        lay = WindowMask(P, length, tiled, dev, block_size=c.block_size)
         H, V = d.hidden, d.vocab
         window = {}
 

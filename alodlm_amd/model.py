@@ -128,6 +128,13 @@ class ALoDLM(nn.Module):
         torch.save(gate, path / "exit_gate.pt")
         (path / "alodlm_config.json").write_text(json.dumps(asdict(self.config), indent=2) + "\n")
 
+    def rollout(self, batch, generator=None, exit_uniforms=None):
+        """Sample commitments and return per-depth logits, gates and exits
+        (alodlm/model.py:130-169), each operation a differentiable kernel
+        launch (see ``alodlm_amd.rollout``)."""
+        from .rollout import rollout
+        return rollout(self, batch, generator=generator, exit_uniforms=exit_uniforms)
+
     def engine(self):
         """The step engine bound to the current parameter storage."""
         if self._engine is None or not self._engine.arena.valid():

@@ -144,6 +144,27 @@ int alodlm_qknorm_rope_bwd(const void* dq, const void* dk, const void* qkv, cons
                            void* dqkv, float* dwq_accum, float* dwk_accum, float* workspace,
                            int64_t rows, int64_t nq, int64_t nkv, int64_t dh, float eps,
                            int dtype, void* stream);
+/* The same with the rotation read from caller tables cos_tab / sin_tab
+ * [rows, dh] in the storage dtype (the cos, sin arguments of
+ * alodlm/model.py:41-46 and layer_forward, model.py:49-58), element i of
+ * each head rotating with entry i of its row. */
+int alodlm_qknorm_rotary_fwd(const void* qkv, const void* wq, const void* wk, const void* cos_tab,
+                             const void* sin_tab, void* q_out, void* k_out, int64_t rows,
+                             int64_t nq, int64_t nkv, int64_t dh, float eps, int dtype,
+                             void* stream);
+int alodlm_qknorm_rotary_bwd(const void* dq, const void* dk, const void* qkv, const void* wq,
+                             const void* wk, const void* cos_tab, const void* sin_tab, void* dqkv,
+                             float* dwq_accum, float* dwk_accum, float* workspace, int64_t rows,
+                             int64_t nq, int64_t nkv, int64_t dh, float eps, int dtype,
+                             void* stream);
+/* The rotary alone (alodlm/model.py:41-46, `rotary`): out = x * cos +
+ * rotate_half(x) * sin for x [rows, heads, dh] and tables [rows, dh], each
+ * product and the sum rounded to the storage dtype; bwd gives dx from dout
+ * (the transposed rotation, rounded like the reference's bf16 autograd). */
+int alodlm_rotary_fwd(const void* x, const void* cos_tab, const void* sin_tab, void* out,
+                      int64_t rows, int64_t heads, int64_t dh, int dtype, void* stream);
+int alodlm_rotary_bwd(const void* dout, const void* cos_tab, const void* sin_tab, void* dx,
+                      int64_t rows, int64_t heads, int64_t dh, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * GEMM for every linear layer (nn.Linear at alodlm/model.py:55-57,74-75,161;
@@ -307,6 +328,38 @@ int alodlm_objective(const float* gates, const int32_t* exits, const uint8_t* ma
                      int64_t rows, int64_t max_depth, float depth_prior_c, float kl_beta_mi,
                      float kl_beta_marg, float* out, float* dgate, float* workspace,
                      void* stream);
+/* outcome_loss alone (alodlm/loss.py:35-90): the objective above without the
+ * autoregressive part; out[0..9] as above with out[0] = (denoising + actor)
+ * / 2 and out[8] = 0, so the outcome loss is out[1] + out[2].  dgate [K, rows]
+ * = d(denoising + actor)/d gate and dce [K, rows] = d(denoising)/d ce (the
+ * row's weight times the detached stick at d < z, else 0).  Same workspace as
+ * alodlm_objective. */
+int alodlm_outcome_loss(const float* gates, const int32_t* exits, const uint8_t* masked,
+                        const float* mask_prob, const float* ce_full, const int64_t* bounds,
+                        int64_t n_segments, int64_t rows, int64_t max_depth, float depth_prior_c,
+                        float kl_beta_mi, float kl_beta_marg, float* out, float* dgate,
+                        float* dce, float* workspace, void* stream);
+/* masked_sequence_ids (alodlm/credit.py:7-21): out[j] = segment of the j-th
+ * masked row in row order (bucketize(rows, bounds[1:], right=True)[masked]),
+ * *count = number of masked rows (device int64).  bounds [S+1] as the
+ * caller's cum_seqlens; the host-side validation of credit.py:8-19 stays with
+ * the caller.  One workgroup. */
+int alodlm_masked_sequence_ids(const uint8_t* masked, const int64_t* bounds, int64_t n_segments,
+                               int64_t rows, int64_t* out, int64_t* count, void* stream);
+/* sequence_score_function (alodlm/credit.py:23-40): value[0] =
+ * sum_s R_s Q_s / n with R_s, Q_s the per-sequence sums of credit and logq
+ * (rows in order within a sequence), dlogq[i] = R_{ids[i]} / n.  ids in
+ * [0, sequence_count); `workspace` holds 2 * sequence_count floats.  One
+ * workgroup, one wavefront per sequence (cost n * sequence_count / 1024). */
+int alodlm_sequence_score(const float* credit, const float* logq, const int64_t* ids, int64_t n,
+                          int64_t sequence_count, float* value, float* dlogq, float* workspace,
+                          void* stream);
+/* Next-token targets of autoregressive_loss (alodlm/loss.py:12-32) over the
+ * dual-stream rows: clean row start + i of a segment [start, end) with
+ * L = (end - start) / 2 >= 2 and i < L - 1 predicts labels[start/2 + 1 + i];
+ * every other row and ignored labels (-100) get -1. */
+int alodlm_ar_targets(const int64_t* labels, const int64_t* bounds, int64_t n_segments,
+                      int64_t rows, int32_t* target, void* stream);
 
 /* Gate-head backward (GateHead.forward, model.py:37-38, differentiated):
  * gw_accum[H] += scale * sum_r dgate[r]*readout[r]; gb_accum[0] and

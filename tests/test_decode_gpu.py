@@ -104,7 +104,7 @@ def test_window_attention_layout(dtype, dh, tiled, prefix, window):
     each window row over every prefix key and the window keys up to itself
     (alodlm/inference.py:77-79), against torch float32."""
     from alodlm_amd import _lib
-    from alodlm_amd.inference import _WindowLayout
+    from alodlm_amd.layers import WindowMask
     _lib.load()
     log(f"layout {dtype} dh={dh} tiled={tiled} P={prefix} W={window}")
     nq, nkv = 4, 2
@@ -112,7 +112,7 @@ def test_window_attention_layout(dtype, dh, tiled, prefix, window):
     q = torch.randn(window, nq * dh, generator=g).to(dtype)
     kc = torch.randn(prefix + window, nkv * dh, generator=g).to(dtype)
     vc = torch.randn(prefix + window, nkv * dh, generator=g).to(dtype)
-    lay = _WindowLayout(prefix, window, tiled, DEV)
+    lay = WindowMask(prefix, window, tiled, DEV, block_size=4)
     q_all = torch.zeros(lay.q_rows, nq * dh, dtype=dtype, device=DEV)
     q_all[lay.q_off:] = q.to(DEV)
     kd, vd = kc.to(DEV), vc.to(DEV)
@@ -120,7 +120,7 @@ def test_window_attention_layout(dtype, dh, tiled, prefix, window):
     lse = torch.empty(nq, lay.q_rows, dtype=torch.float32, device=DEV)
     shift = lay.base * nkv * dh * kd.element_size()
     _lib.call("alodlm_attention_fwd", _lib.ptr(q_all), _lib.ptr(kd) + shift, _lib.ptr(vd) + shift,
-              nkv * dh, _lib.ptr(lay.bounds), _lib.ptr(lay.row_segment), _lib.ptr(lay.tiles),
+              nkv * dh, _lib.ptr(lay.boundaries), _lib.ptr(lay.row_segment), _lib.ptr(lay.tiles),
               0 if lay.tiles is None else lay.tiles.shape[0], _lib.ptr(o_all), _lib.ptr(lse),
               lay.q_rows, nq, nkv, dh, 4, _lib.dtype_code(dtype), _lib.stream_handle(DEV))
     torch.cuda.synchronize()
