@@ -250,6 +250,137 @@ class StepEngine(Kernels):
         return self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li], b.kernel_mask,
                               self._rope)
 
+    # ------------------------------------------------------------------ shared pieces
+    def _carry(self, core_out, b, exits, depth):
+        """Input of core pass ``depth``: exits <= depth ? E[original] :
+        norm(core_out) (alodlm/model.py:150-151,168), one launch."""
+        d = self.dims
+        N, H = core_out.shape
+        xin = self._empty(N, H)
+        rstd = self._empty(N, dtype=torch.float32)
+        call("alodlm_carry_select", ptr(core_out), ptr(self.final_norm), ptr(self.embed),
+             ptr(b.original), ptr(exits), depth, ptr(xin), ptr(rstd), N, H, d.vocab, d.eps,
+             self.code, self._stream())
+        return xin, rstd
+
+    def _carry_bwd(self, dnext, core_out, rstd, b, exits, depth, dres, g_norm, g_embed):
+        """Backward of ``_carry`` at ``depth``: carried rows go back through the
+        carry norm into the previous core output (plus ``dres``), re-embedded
+        rows into the embedding table."""
+        N, H = core_out.shape
+        dcore = self._empty(N, H)
+        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        call("alodlm_carry_select_bwd", ptr(dnext), ptr(core_out), ptr(rstd),
+             ptr(self.final_norm), ptr(exits), depth, ptr(b.original), ptr(dres), ptr(dcore),
+             ptr(g_norm), ptr(g_embed), ptr(ws), N, H, self.dims.vocab, self.code, self._stream())
+        return dcore
+
+    def _gate_pass(self, r, depth, gates, exits, b, exit_uniforms, generator, rec):
+        """Final norm and gate of pass ``depth`` (alodlm/model.py:160-162) and,
+        before the last pass, the exit sampling (model.py:163-167)."""
+        d, K = self.dims, self.cfg.max_depth
+        N, H = r.shape
+        st, c = self._stream(), self.code
+        readout = self._empty(N, H)
+        rstd_f = self._empty(N, dtype=torch.float32)
+        call("alodlm_final_norm_gate", ptr(r), ptr(self.final_norm), ptr(self.gate_w),
+             ptr(self.gate_b), ptr(self.depth_bias), depth, ptr(readout), ptr(rstd_f),
+             ptr(gates[depth]), N, H, d.eps, c, st)
+        rec["final_in"], rec["readout"], rec["rstd_f"] = r, readout, rstd_f
+        if depth < K - 1:
+            if exit_uniforms is not None:
+                u = exit_uniforms[depth].to(device=self.device, dtype=torch.float32).contiguous()
+            else:
+                u = torch.rand(N, device=self.device, generator=generator)
+            call("alodlm_exit_update", ptr(gates[depth]), ptr(u), ptr(b.masked), ptr(exits),
+                 depth, K, N, st)
+        return readout
+
+    def _lm_readout(self, readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad, rec):
+        """Loss-bearing rows of pass ``depth`` through the LM head and the
+        vocabulary cross-entropy (alodlm/model.py:161,180-181; loss.py:12-32):
+        rows are selected and weighted by alodlm_select_rows, their logits
+        become dL/dlogits in place."""
+        d, K = self.dims, self.cfg.max_depth
+        N, H = readout.shape
+        V = d.vocab
+        st, c = self._stream(), self.code
+        sel_rows = torch.empty(N, dtype=torch.int32, device=self.device)
+        sel_target = torch.empty(N, dtype=torch.int32, device=self.device)
+        sel_coef = torch.empty(N, dtype=torch.float32, device=self.device)
+        sel_count = torch.empty(1, dtype=torch.int32, device=self.device)
+        call("alodlm_select_rows", ptr(b.masked), ptr(exits), ptr(b.original), ptr(b.ar_target),
+             ptr(gates), ptr(b.mask_probability), ptr(wsum), ar_coef, depth, K, N, ptr(sel_rows),
+             ptr(sel_target), ptr(sel_coef), ptr(sel_count), st)
+        R = int(sel_count.item())
+        rec["R"], rec["sel_rows"] = R, sel_rows
+        if R:
+            # Rows padded to a multiple of 32 with zeros: their logits and
+            # dL/dlogits are exactly zero, and the LM-head dW product (whose
+            # depth is the row count) runs on whole 32-deep k stages.
+            Rp = -(-R // 32) * 32
+            xsel = self._empty(Rp, H)
+            if Rp > R:
+                xsel[R:].zero_()
+            call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
+            logits = self._empty(Rp, V)
+            self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
+            ce = torch.empty(R, dtype=torch.float32, device=self.device)
+            call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
+                 ptr(sel_count), R, V, ptr(ce), None, c, st)
+            call("alodlm_scatter_ce", ptr(ce), ptr(sel_rows), ptr(sel_count), R,
+                 ptr(ce_all[depth]), N, st)
+            if need_grad:
+                rec["xsel"], rec["dlogits"] = xsel, logits
+
+    def _objective(self, gates, exits, b, ce_all, N, S, K):
+        out = torch.empty(10, dtype=torch.float32, device=self.device)
+        dgate = torch.empty(K, N, dtype=torch.float32, device=self.device)
+        cfg = self.cfg
+        ws = self._workspace(query("alodlm_objective_workspace", N, S, K))
+        call("alodlm_objective", ptr(gates), ptr(exits), ptr(b.masked), ptr(b.mask_probability),
+             ptr(ce_all), ptr(ce_all), ptr(b.ar_target), ptr(b.boundaries), S, N, K,
+             cfg.depth_prior_c, cfg.kl_beta_mi, cfg.kl_beta_marg, ptr(out), ptr(dgate), ptr(ws),
+             self._stream())
+        return out, dgate
+
+    def _readout_bwd(self, rec, depth, dgate, grad_scale, g_lm, g_norm, g_gw, g_gb, g_db):
+        """Backward of pass ``depth``'s readout: LM head dX/dW, gate head, final
+        norm; returns d final_in."""
+        d = self.dims
+        N, H = rec["readout"].shape
+        V = d.vocab
+        st, c = self._stream(), self.code
+        R = rec["R"]
+        dread = self._empty(N, H)
+        if R:
+            dsel = self._empty(R, H)
+            # d readout = dlogits . W_lm ; dW_lm += dlogits^T . readout
+            self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
+                       alpha=grad_scale)
+            self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H,
+                       rec["xsel"].shape[0], alpha=grad_scale, epi=EPI_ACCUM)
+            call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
+                 c, st)
+            del dsel
+        else:
+            dread.zero_()
+        ws = self._workspace(query("alodlm_gate_bwd_workspace", N, H))
+        call("alodlm_gate_bwd", ptr(dgate), ptr(rec["readout"]), grad_scale, ptr(g_gw), ptr(g_gb),
+             ptr(g_db), depth, N, H, ptr(ws), c, st)
+        dr = self._empty(N, H)
+        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        call("alodlm_rmsnorm_bwd", ptr(dread), ptr(rec["final_in"]), ptr(rec["rstd_f"]),
+             ptr(self.final_norm), None, ptr(dr), ptr(g_norm), ptr(ws), N, H, c, st)
+        return dr
+
+    def _grad_views(self, grads):
+        a = self.arena
+        names = ("backbone.model.embed_tokens.weight", "backbone.model.norm.weight",
+                 "backbone.lm_head.weight", "exit_gate.net.weight", "exit_gate.net.bias",
+                 "exit_gate.depth_bias")
+        return [a.view(grads, n) for n in names]
+
     # ------------------------------------------------------------------ step
     def forward(self, ids, labels, boundaries, need_grad, exit_uniforms=None, draws=None,
                 generator=None):
@@ -289,13 +420,7 @@ class StepEngine(Kernels):
         for depth in range(K):
             rec = {}
             if depth:
-                xin = self._empty(N, H)
-                rstd_c = self._empty(N, dtype=torch.float32)
-                call("alodlm_carry_select", ptr(core_out), ptr(self.final_norm), ptr(self.embed),
-                     ptr(b.original), ptr(exits), depth, ptr(xin), ptr(rstd_c), N, H, V, d.eps,
-                     c, st)
-                depths[-1]["carry_rstd"] = rstd_c
-                core_in = xin
+                core_in, depths[-1]["carry_rstd"] = self._carry(core_out, b, exits, depth)
             h = core_in
             rec["core_saves"] = [] if need_grad else None
             for li in range(cfg.loop_start, cfg.loop_end):
@@ -306,56 +431,11 @@ class StepEngine(Kernels):
             rec["coda_saves"] = [] if need_grad else None
             for li in range(cfg.loop_end, d.layers):
                 r = self._layer_fwd(li, r, b, rec["coda_saves"])
-            rec["final_in"] = r
-            readout = self._empty(N, H)
-            rstd_f = self._empty(N, dtype=torch.float32)
-            call("alodlm_final_norm_gate", ptr(r), ptr(self.final_norm), ptr(self.gate_w),
-                 ptr(self.gate_b), ptr(self.depth_bias), depth, ptr(readout), ptr(rstd_f),
-                 ptr(gates[depth]), N, H, d.eps, c, st)
-            rec["readout"], rec["rstd_f"] = readout, rstd_f
-            if depth < K - 1:
-                if exit_uniforms is not None:
-                    u = exit_uniforms[depth].to(device=self.device, dtype=torch.float32).contiguous()
-                else:
-                    u = torch.rand(N, device=self.device, generator=generator)
-                call("alodlm_exit_update", ptr(gates[depth]), ptr(u), ptr(b.masked), ptr(exits),
-                     depth, K, N, st)
-            sel_rows = torch.empty(N, dtype=torch.int32, device=self.device)
-            sel_target = torch.empty(N, dtype=torch.int32, device=self.device)
-            sel_coef = torch.empty(N, dtype=torch.float32, device=self.device)
-            sel_count = torch.empty(1, dtype=torch.int32, device=self.device)
-            call("alodlm_select_rows", ptr(b.masked), ptr(exits), ptr(b.original),
-                 ptr(b.ar_target), ptr(gates), ptr(b.mask_probability), ptr(wsum), ar_coef, depth,
-                 K, N, ptr(sel_rows), ptr(sel_target), ptr(sel_coef), ptr(sel_count), st)
-            R = int(sel_count.item())
-            rec["R"], rec["sel_rows"] = R, sel_rows
-            if R:
-                # Rows padded to a multiple of 32 with zeros: their logits and
-                # dL/dlogits are exactly zero, and the LM-head dW product (whose
-                # depth is the row count) runs on whole 32-deep k stages.
-                Rp = -(-R // 32) * 32
-                xsel = self._empty(Rp, H)
-                if Rp > R:
-                    xsel[R:].zero_()
-                call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
-                logits = self._empty(Rp, V)
-                self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
-                ce = torch.empty(R, dtype=torch.float32, device=self.device)
-                call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
-                     ptr(sel_count), R, V, ptr(ce), None, c, st)
-                call("alodlm_scatter_ce", ptr(ce), ptr(sel_rows), ptr(sel_count), R,
-                     ptr(ce_all[depth]), N, st)
-                if need_grad:
-                    rec["xsel"], rec["dlogits"] = xsel, logits
-                else:
-                    del logits, xsel
+            readout = self._gate_pass(r, depth, gates, exits, b, exit_uniforms, generator, rec)
+            self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad,
+                             rec)
             depths.append(rec)
-        out = torch.empty(10, dtype=torch.float32, device=self.device)
-        dgate = torch.empty(K, N, dtype=torch.float32, device=self.device)
-        ws = self._workspace(query("alodlm_objective_workspace", N, S, K))
-        call("alodlm_objective", ptr(gates), ptr(exits), ptr(b.masked), ptr(b.mask_probability),
-             ptr(ce_all), ptr(ce_all), ptr(b.ar_target), ptr(b.boundaries), S, N, K,
-             cfg.depth_prior_c, cfg.kl_beta_mi, cfg.kl_beta_marg, ptr(out), ptr(dgate), ptr(ws), st)
+        out, dgate = self._objective(gates, exits, b, ce_all, N, S, K)
         self.last_rows = [rec["R"] for rec in depths]
         state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "dgate": dgate,
                  "prelude": saves, "depths": depths}
@@ -369,50 +449,19 @@ class StepEngine(Kernels):
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
         self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
-        a = self.arena
-        g_embed = a.view(grads, "backbone.model.embed_tokens.weight")
-        g_norm = a.view(grads, "backbone.model.norm.weight")
-        g_lm = a.view(grads, "backbone.lm_head.weight")
-        g_gw = a.view(grads, "exit_gate.net.weight")
-        g_gb = a.view(grads, "exit_gate.net.bias")
-        g_db = a.view(grads, "exit_gate.depth_bias")
+        g_embed, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
         dnext = None  # gradient at the core input of depth+1
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
-            R = rec["R"]
-            dread = self._empty(N, H)
-            if R:
-                dsel = self._empty(R, H)
-                # d readout = dlogits . W_lm ; dW_lm += dlogits^T . readout
-                self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
-                           alpha=grad_scale)
-                self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H,
-                           rec["xsel"].shape[0], alpha=grad_scale, epi=EPI_ACCUM)
-                call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
-                     c, st)
-                del dsel
-            else:
-                dread.zero_()
-            ws = self._workspace(query("alodlm_gate_bwd_workspace", N, H))
-            call("alodlm_gate_bwd", ptr(state["dgate"][depth]), ptr(rec["readout"]), grad_scale,
-                 ptr(g_gw), ptr(g_gb), ptr(g_db), depth, N, H, ptr(ws), c, st)
-            dr = self._empty(N, H)
-            ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
-            call("alodlm_rmsnorm_bwd", ptr(dread), ptr(rec["final_in"]), ptr(rec["rstd_f"]),
-                 ptr(self.final_norm), None, ptr(dr), ptr(g_norm), ptr(ws), N, H, c, st)
-            del dread
+            dr = self._readout_bwd(rec, depth, state["dgate"][depth], grad_scale, g_lm, g_norm,
+                                   g_gw, g_gb, g_db)
             for saved in reversed(rec["coda_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             if dnext is not None:
                 # x_in(depth+1) = exits <= depth+1 ? E[original] : norm(core_out(depth))
-                dcore = self._empty(N, H)
-                ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
-                call("alodlm_carry_select_bwd", ptr(dnext), ptr(rec["core_out"]),
-                     ptr(rec["carry_rstd"]), ptr(self.final_norm), ptr(exits), depth + 1,
-                     ptr(b.original), ptr(dr), ptr(dcore), ptr(g_norm), ptr(g_embed), ptr(ws),
-                     N, H, V, c, st)
-                dr = dcore
+                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], b, exits,
+                                     depth + 1, dr, g_norm, g_embed)
             for saved in reversed(rec["core_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             dnext = dr
@@ -424,3 +473,128 @@ class StepEngine(Kernels):
         if self._step_alloc is not None and self._step_peak is None:
             self._step_peak = torch.cuda.max_memory_allocated(self.device)
         return grads
+
+    # ------------------------------------------------------------------ stages
+    def core_forward(self, x0, batch, need_grad=True, exit_uniforms=None, generator=None):
+        """The shared recurrent core alone (alodlm/model.py:147-168 without the
+        prelude, coda and LM head): K passes of the core layers
+        [loop_start, loop_end) from the hidden states x0 [N, H], the gate on
+        the final norm of each pass's output, exit sampling, and between
+        passes the carry norm or, for committed rows, the re-embedding of
+        ``batch.original``.  ``batch`` is a build_batch result.
+
+        Returns (outputs: K tensors [N, H], gates [K, N] float32, exits [N]
+        int32, state for core_backward)."""
+        if not self.arena.valid():
+            raise RuntimeError("model parameters were moved after the step engine was built")
+        cfg, d = self.cfg, self.dims
+        K, N = cfg.max_depth, x0.shape[0]
+        if x0.shape != (batch.ids.numel(), d.hidden) or x0.dtype != self.dtype:
+            raise ValueError("x0 must be [rows, hidden] in the parameter dtype")
+        self._ws = None
+        self.transposed.refresh(self.code, self._stream())
+        b = batch
+        self._rope = Rope(positions=b.positions, inv_freq=self.inv_freq)
+        self._keep_now = (False, False)
+        gates = torch.empty(K, N, dtype=torch.float32, device=self.device)
+        exits = torch.full((N,), K, dtype=torch.int32, device=self.device)
+        depths, h = [], x0.contiguous()
+        for depth in range(K):
+            rec = {}
+            if depth:
+                h, depths[-1]["carry_rstd"] = self._carry(core_out, b, exits, depth)
+            rec["core_saves"] = [] if need_grad else None
+            for li in range(cfg.loop_start, cfg.loop_end):
+                h = self._layer_fwd(li, h, b, rec["core_saves"])
+            core_out = h
+            rec["core_out"] = core_out
+            self._gate_pass(core_out, depth, gates, exits, b, exit_uniforms, generator, rec)
+            depths.append(rec)
+        state = {"batch": b, "gates": gates, "exits": exits, "depths": depths}
+        return [rec["core_out"] for rec in depths], gates, exits, state
+
+    def core_backward(self, state, douts, dgates=None):
+        """Backward of core_forward for output gradients ``douts`` (K tensors
+        [N, H]) and optional gate-logit gradients ``dgates`` [K, N] float32
+        (they reach only the gate parameters: the gate reads the detached
+        readout).  Returns (dx0, float32 gradients in the arena layout)."""
+        cfg, d = self.cfg, self.dims
+        K = cfg.max_depth
+        b = state["batch"]
+        grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
+        self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
+        g_embed, g_norm, _, g_gw, g_gb, g_db = self._grad_views(grads)
+        exits = state["exits"]
+        dnext = None
+        for depth in reversed(range(K)):
+            rec = state["depths"][depth]
+            N, H = rec["core_out"].shape
+            dr = douts[depth].to(self.dtype).contiguous()
+            if dgates is not None:
+                g = dgates[depth].to(torch.float32).contiguous()
+                ws = self._workspace(query("alodlm_gate_bwd_workspace", N, H))
+                call("alodlm_gate_bwd", ptr(g), ptr(rec["readout"]), 1.0, ptr(g_gw), ptr(g_gb),
+                     ptr(g_db), depth, N, H, ptr(ws), self.code, self._stream())
+            if dnext is not None:
+                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], b, exits,
+                                     depth + 1, dr, g_norm, g_embed)
+            for saved in reversed(rec["core_saves"]):
+                dr = self._layer_bwd(dr, saved, b, grads)
+            dnext = dr
+        return dnext, grads
+
+    def readout_forward(self, finals, batch, need_grad=True, exit_uniforms=None, generator=None):
+        """The fused readout and objective alone (alodlm/model.py:157-187 from
+        the final hidden states): for each of the K passes, the final norm of
+        ``finals[d]`` [N, H] with the gate, exit sampling, the LM head over the
+        loss-bearing rows (masked rows not yet exited, and rows with an
+        autoregressive target), the vocabulary cross-entropy; then the
+        objective.  ``batch`` holds masked, original (targets),
+        mask_probability, boundaries (segment offsets over the N rows),
+        ar_target and ar_count.
+
+        Returns (out[10] as the step's, state for readout_backward)."""
+        cfg, d = self.cfg, self.dims
+        K = cfg.max_depth
+        N = finals[0].shape[0]
+        if len(finals) != K or any(f.shape != (N, d.hidden) or f.dtype != self.dtype
+                                   for f in finals):
+            raise ValueError("finals must be max_depth tensors [rows, hidden] in the parameter dtype")
+        self._ws = None
+        st = self._stream()
+        self.transposed.refresh(self.code, st)
+        b = batch
+        S = b.boundaries.numel() - 1
+        gates = torch.empty(K, N, dtype=torch.float32, device=self.device)
+        exits = torch.full((N,), K, dtype=torch.int32, device=self.device)
+        ce_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
+        wsum = torch.empty(1, dtype=torch.float32, device=self.device)
+        call("alodlm_inverse_weight_sum", ptr(b.masked), ptr(b.mask_probability), N, ptr(wsum), st)
+        ar_coef = 0.5 / (K * b.ar_count) if b.ar_count else 0.0
+        depths = []
+        for depth in range(K):
+            rec = {}
+            readout = self._gate_pass(finals[depth].contiguous(), depth, gates, exits, b,
+                                      exit_uniforms, generator, rec)
+            self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad,
+                             rec)
+            depths.append(rec)
+        out, dgate = self._objective(gates, exits, b, ce_all, N, S, K)
+        self.last_rows = [rec["R"] for rec in depths]
+        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "dgate": dgate,
+                 "depths": depths}
+        return out, state
+
+    def readout_backward(self, state, grad_scale=1.0):
+        """Backward of readout_forward: returns (K gradients [N, H] of the final
+        hidden states, float32 gradients in the arena layout: LM head, final
+        norm, gate)."""
+        K = self.cfg.max_depth
+        grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
+        _, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
+        dfinals = [None] * K
+        for depth in reversed(range(K)):
+            dfinals[depth] = self._readout_bwd(state["depths"][depth], depth,
+                                               state["dgate"][depth], grad_scale, g_lm, g_norm,
+                                               g_gw, g_gb, g_db)
+        return dfinals, grads

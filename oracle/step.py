@@ -16,7 +16,7 @@ import torch.nn.functional as F
 __all__ = [
     "Dims", "Objective", "draw_mask_randomness", "build_batch", "attention_mask",
     "packed_attention_mask", "sparse_plan", "rope_tables", "rmsnorm", "layer_forward",
-    "gate_depth_bias", "rollout", "outcome_loss", "autoregressive_loss",
+    "gate_depth_bias", "rollout", "readout_objective", "outcome_loss", "autoregressive_loss",
     "masked_sequence_ids", "sequence_score_function", "step_loss", "init_params",
     "param_names", "clip_coefficient", "adamw_update", "cosine_lr_multiplier",
 ]
@@ -240,10 +240,30 @@ def gate_depth_bias(initial_mass):
     return bias + [0.0]
 
 
-def rollout(p, batch, dims, cfg, exit_uniforms, allowed=None):
+def _gate(p, readout, depth):
+    """GateHead on the detached readout (alodlm/model.py:37-38,162)."""
+    gate = (readout.detach() @ p["exit_gate.net.weight"].T).squeeze(-1) + p["exit_gate.net.bias"]
+    return gate + p["exit_gate.depth_bias"][depth]
+
+
+def _sample_exits(gate, uniforms, masked, exits, depth, K):
+    """alodlm/model.py:163-167: rows still at K whose uniform falls under the
+    hazard exit after pass depth + 1."""
+    with torch.no_grad():
+        hazard = torch.sigmoid(gate.float())
+        chosen = (torch.as_tensor(uniforms) < hazard) & masked & (exits == K)
+    return torch.where(chosen, depth + 1, exits)
+
+
+def rollout(p, batch, dims, cfg, exit_uniforms, allowed=None, x0=None, trace=None,
+            lm_head=True):
     """alodlm/model.py:130-169 with the K-1 exit uniforms given explicitly.
 
-    Returns (logits list [N,V], gates list [N], exits [N] int64).
+    Returns (logits list [N,V], gates list [N], exits [N] int64).  ``x0``
+    replaces the embedding and the prelude as the first core input (the
+    core block alone); ``trace`` (a dict) receives the per-pass core outputs
+    ("core_out") and final-norm inputs ("final_in"); ``lm_head=False`` skips
+    the logits.
     """
     K = cfg.max_depth
     emb = p["model.embed_tokens.weight"]
@@ -255,33 +275,38 @@ def rollout(p, batch, dims, cfg, exit_uniforms, allowed=None):
     if allowed is None:
         allowed = packed_attention_mask(batch["boundaries"], cfg.block_size)
     allowed = torch.as_tensor(allowed)
+    trace = {} if trace is None else trace
+    trace["core_in"], trace["core_out"], trace["final_in"] = [], [], []
 
     def layer(i, h):
         return layer_forward(p, f"model.layers.{i}.", h, cos, sin, allowed, dims)
 
-    hidden = emb[ids]
-    for i in range(cfg.loop_start):
-        hidden = layer(i, hidden)
+    if x0 is None:
+        hidden = emb[ids]
+        for i in range(cfg.loop_start):
+            hidden = layer(i, hidden)
+    else:
+        hidden = x0
     gold = emb[original]
     exits = torch.full_like(ids, K)
     logits, gates = [], []
     for depth in range(K):
         if depth:
             hidden = torch.where((exits <= depth)[:, None], gold, hidden)
+        trace["core_in"].append(hidden)
         for i in range(cfg.loop_start, cfg.loop_end):
             hidden = layer(i, hidden)
+        trace["core_out"].append(hidden)
         readout = hidden
         for i in range(cfg.loop_end, dims.layers):
             readout = layer(i, readout)
+        trace["final_in"].append(readout)
         readout = rmsnorm(readout, p["model.norm.weight"], dims.eps)
-        logits.append(readout @ p["lm_head.weight"].T)
-        gate = (readout.detach() @ p["exit_gate.net.weight"].T).squeeze(-1) + p["exit_gate.net.bias"]
-        gates.append(gate + p["exit_gate.depth_bias"][depth])          # model.py:37-38
+        if lm_head:
+            logits.append(readout @ p["lm_head.weight"].T)
+        gates.append(_gate(p, readout, depth))
         if depth < K - 1:
-            with torch.no_grad():
-                hazard = torch.sigmoid(gates[-1].float())
-                chosen = (torch.as_tensor(exit_uniforms[depth]) < hazard) & masked & (exits == K)
-            exits = torch.where(chosen, depth + 1, exits)
+            exits = _sample_exits(gates[-1], exit_uniforms[depth], masked, exits, depth, K)
             hidden = rmsnorm(hidden, p["model.norm.weight"], dims.eps)
     return logits, gates, exits
 
@@ -431,6 +456,40 @@ def step_loss(p, ids, labels, boundaries, dims, cfg, draws, exit_uniforms, ce_dt
     metrics = {**metrics, "ar_loss": ar.detach(), "loss": total.detach()}
     return total, metrics, {"batch": batch, "gates": gates, "exits": exits, "ce": ce,
                             "logits": logits}
+
+
+def readout_objective(p, finals, batch, dims, cfg, exit_uniforms, labels=None, ce_dtype=None,
+                      credit_ce=None):
+    """The readout and objective of alodlm/model.py:157-187 from given final
+    hidden states (the inputs of the final norm), one per pass: final norm,
+    LM head, gate, exit sampling, masked cross-entropy, outcome_loss and -
+    with ``labels`` - the autoregressive loss; total = (outcome + AR) / 2.
+    ``batch`` holds masked, original, mask_probability and boundaries (the
+    segment offsets of the rows).  Returns (total, metrics, extras)."""
+    K = cfg.max_depth
+    masked = torch.as_tensor(batch["masked"])
+    original = torch.as_tensor(batch["original"])
+    exits = torch.full((masked.numel(),), K, dtype=torch.int64)
+    logits, gates = [], []
+    for depth in range(K):
+        readout = rmsnorm(finals[depth], p["model.norm.weight"], dims.eps)
+        logits.append(_round_through(readout @ p["lm_head.weight"].T, ce_dtype))
+        gates.append(_gate(p, readout, depth))
+        if depth < K - 1:
+            exits = _sample_exits(gates[-1], exit_uniforms[depth], masked, exits, depth, K)
+    ce = torch.stack([_round_through(F.cross_entropy(lg[masked], original[masked],
+                                                     reduction="none"), ce_dtype)
+                      for lg in logits])
+    den_actor, metrics = outcome_loss(ce, gates, exits, masked, batch["mask_probability"],
+                                      batch["boundaries"], cfg, credit_ce)
+    if labels is None:
+        ar = den_actor.new_zeros(())
+    else:
+        ar = torch.stack([autoregressive_loss(lg, labels, batch["boundaries"], ce_dtype)
+                          for lg in logits]).mean()
+    total = (den_actor + ar) / 2
+    metrics = {**metrics, "ar_loss": ar.detach(), "loss": total.detach()}
+    return total, metrics, {"gates": gates, "exits": exits, "ce": ce, "logits": logits}
 
 
 # ----------------------------------------------------------------------------

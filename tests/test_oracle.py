@@ -359,3 +359,51 @@ def test_cosine_schedule_closed_form():
     assert abs(O.cosine_lr_multiplier(52, 4, 100) - 0.5) < 1e-12
     assert O.cosine_lr_multiplier(100, 4, 100) == 0.0
 
+
+
+def _micro_case():
+    from tests import golden
+    from tests.helpers import cpu_draws, oracle_draws
+    g = golden.load("step_micro")
+    dims = O.Dims(hidden=32, heads=4, kv_heads=2, head_dim=8, intermediate=64, vocab=64,
+                  layers=3, eps=1e-6, theta=1e4)
+    obj = O.Objective(loop_start=1, loop_end=2, mask_token_id=3, block_size=4)
+    name = lambda n: n if n.startswith("exit_gate.") else "backbone." + n
+    p = {n: torch.as_tensor(g["param_" + name(n)]).double() for n in O.param_names(dims)}
+    labels = torch.as_tensor(g["in_labels"])
+    bounds = torch.as_tensor(g["in_boundaries"])
+    draws, uniforms = cpu_draws(labels, bounds, obj.block_size, int(g["seed"]), obj.max_depth)
+    od = oracle_draws(draws, [int(v) for v in bounds], obj.block_size)
+    batch = O.build_batch(g["in_ids"], labels, bounds, obj.block_size, obj.mask_token_id, od)
+    return g, dims, obj, p, labels, bounds, od, uniforms, batch
+
+
+def test_rollout_from_given_core_input_is_the_same_rollout():
+    """The x0 entry of the oracle rollout (the core block alone) reproduces the
+    golden-pinned rollout when given the first core input the rollout itself
+    computed: same logits, gates, exits and traced core outputs."""
+    g, dims, obj, p, labels, bounds, od, uniforms, batch = _micro_case()
+    t1, t2 = {}, {}
+    l1, g1, e1 = O.rollout(p, batch, dims, obj, uniforms, trace=t1)
+    l2, g2, e2 = O.rollout(p, batch, dims, obj, uniforms, x0=t1["core_in"][0], trace=t2)
+    assert torch.equal(e1, e2)
+    for a, b in zip(l1 + g1 + t1["core_out"], l2 + g2 + t2["core_out"]):
+        assert torch.equal(a, b)
+    np.testing.assert_array_equal(e1.numpy(), g["exits"])
+
+
+def test_readout_objective_from_traced_finals_is_the_step_loss():
+    """readout_objective on the rollout's own final-norm inputs gives the
+    golden-pinned step loss, metrics, gates and exits."""
+    g, dims, obj, p, labels, bounds, od, uniforms, batch = _micro_case()
+    q = {k: v.clone().requires_grad_(True) for k, v in p.items()}
+    total, metrics, extra = O.step_loss(q, g["in_ids"], labels, bounds, dims, obj, od, uniforms)
+    trace = {}
+    O.rollout(p, batch, dims, obj, uniforms, trace=trace)
+    t2, m2, x2 = O.readout_objective(p, trace["final_in"], batch, dims, obj, uniforms,
+                                     labels=labels)
+    assert abs(float(t2) - float(total)) <= 1e-12 * abs(float(total))
+    assert abs(float(t2) - float(g["loss"])) <= 1e-5 * abs(float(g["loss"]))
+    assert torch.equal(x2["exits"], extra["exits"])
+    for key in m2:
+        assert abs(float(m2[key]) - float(metrics[key])) <= 1e-12 * max(1.0, abs(float(metrics[key])))
