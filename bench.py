@@ -9,6 +9,20 @@ global-norm clip + AdamW with float32 masters, all on the HIP kernels.
   --model 8b              Qwen3-8B shapes, prelude 0-10 / core 10-26 / coda
                           26-36, K = 4, one sequence of 2048 tokens (N = 4096)
 
+After the headline step, the other benchmark workloads run as sub-records of
+the same line (``sub_records``; --no-sub-records skips them):
+
+  8b_step       the ALoDLM-8B step above (when the headline is 1.7B)
+  core_block    one Qwen3-8B layer (hidden 4096, 32/8 heads, intermediate
+                12288) run 4 times with shared weights from N(0, 1) hidden
+                states, 4 x 2048 tokens (16384 dual-stream rows) under the
+                training mask, gates after each pass, committed rows
+                re-embedded from a 151936 x 4096 table; forward + backward
+  readout       final hidden states [8192 x 2048] for each of 4 passes,
+                LM head 2048 x 151936, masked cross-entropy and the objective
+                (masks Bernoulli(t), t ~ U(0, 1) per 2048-row sequence);
+                forward + backward
+
 Prints one JSON line (metric of BASELINE: train tokens/s) with:
   roofline      the dominant kernel class (by time in the timed region, from
                 HIP events around its launches on the launch stream):
@@ -167,6 +181,212 @@ def profiled_traffic(path):
     return None
 
 
+def _roofline(timer, steps, spec=None):
+    """Roofline of the dominant kernel class (by time) from the HIP events."""
+    summary = timer.summary()
+    dom = max(summary, key=lambda k: summary[k]["ms"])
+    s = summary[dom]
+    achieved = s["flops"] / s["launches"] / (s["ms"] / s["launches"] / 1000.0)
+    roof = {"bound": "mfma", "kernel": dom, "launches_per_step": s["launches"] // steps,
+            "avg_launch_us": round(1000.0 * s["ms"] / s["launches"], 1),
+            "achieved": round(achieved / 1e12, 1), "peak": round(PEAK_BF16 / 1e12, 1),
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None}
+    if dom == "gemm_bf16":
+        roof["algorithmic_bytes_per_launch"] = timer.gemm_bytes // s["launches"]
+        if spec is not None:
+            traffic_profile = os.path.join(ROOT, "profiles", spec["traffic"])
+            roof["traffic"] = profiled_traffic(traffic_profile)
+            roof["traffic_source"] = os.path.relpath(traffic_profile, ROOT)
+    classes = {k: {"ms_per_step": round(v["ms"] / steps, 1),
+                   "tflops": round(v["flops"] / (v["ms"] / 1000) / 1e12, 1)}
+               for k, v in summary.items()}
+    return roof, classes
+
+
+def _release():
+    import gc
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def run_step(spec, device, steps, warmup, kernel_timing):
+    """The full training step of ``spec``: returns (record, model facts)."""
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    torch.cuda.reset_peak_memory_stats(device)
+    dtype = torch.bfloat16
+    model = build_model(spec, device, dtype)
+    engine = model.engine()
+    timer = None
+    gen = torch.Generator().manual_seed(0)
+    seg_lengths = spec["segments"]
+    ids = torch.randint(0, 151936, (sum(seg_lengths),), generator=gen).to(device)
+    labels = ids.clone()
+    bounds = torch.tensor([0] + [sum(seg_lengths[:i + 1]) for i in range(len(seg_lengths))])
+    torch.cuda.manual_seed(0)
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-5, max_grad_norm=1.0)
+
+    def one_step():
+        loss, metrics = model(ids, labels, bounds)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss.detach()
+
+    for i in range(warmup):
+        loss = one_step()
+        print(f"[bench] {spec['name']} warmup step {i} loss {float(loss):.4f}", file=sys.stderr,
+              flush=True)
+    if kernel_timing:
+        timer = KernelTimer()
+        timer.wrap(engine)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rows = []
+    for i in range(steps):
+        loss = one_step()
+        rows.append(list(engine.last_rows))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    print(f"[bench] {spec['name']}: timed {steps} steps in {elapsed:.3f}s loss {float(loss):.4f}",
+          file=sys.stderr, flush=True)
+    ms = 1000.0 * elapsed / steps
+    tokens = sum(seg_lengths)
+    gemm_f, attn_f, head_f = step_flops(engine.dims, model.config, seg_lengths,
+                                        [sum(r) / len(r) for r in zip(*rows)])
+    step_f = gemm_f + attn_f + head_f
+    record = {
+        "workload": (f"{spec['name']} full training step (fwd+bwd+clip+AdamW fp32 master): "
+                     f"{spec['qwen']} shapes, random init, untied, loop "
+                     f"{spec['loop'][0]}-{spec['loop'][1]}, max_depth 4"),
+        "value": round(tokens * steps / elapsed, 2), "unit": "tokens/s", "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 2), "global_batch": len(seg_lengths),
+        "seq_len": 2048, "dual_stream_rows": 2 * tokens,
+        "memory": {"peak_allocated_gib": round(torch.cuda.max_memory_allocated(device) / 2**30, 1),
+                   "kept_forward_outputs": {"rotary_qk": bool(engine._keep and engine._keep[0]),
+                                            "norm_outputs": bool(engine._keep and engine._keep[1])}},
+        "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
+        "step_tflop": round(step_f / 1e12, 1),
+    }
+    if timer is not None:
+        record["roofline"], record["kernel_classes"] = _roofline(timer, steps, spec)
+    cfg = model.config
+    facts = {"apps": cfg.loop_start + cfg.max_depth * (engine.dims.layers - cfg.loop_start),
+             "segments": len(seg_lengths), "tokens": tokens,
+             "readout_rows": sum(sum(r) for r in rows) / len(rows)}
+    del opt, model, engine, timer
+    _release()
+    return record, facts
+
+
+def run_core_block(device, steps, warmup, kernel_timing):
+    """One Qwen3-8B layer x 4 passes over 4 x 2048 tokens, forward + backward."""
+    from alodlm_amd.batch import allowed_pairs, build_batch
+    spec = dict(MODELS["8b"], num_hidden_layers=1, loop=(0, 1))
+    model = build_model(spec, device, torch.bfloat16, seed=1)
+    with torch.no_grad():
+        model.backbone.model.embed_tokens.weight.normal_(
+            0.0, 1.0, generator=torch.Generator(device=device).manual_seed(2))
+    engine = model.engine()
+    g = torch.Generator(device=device).manual_seed(3)
+    tokens = [2048] * 4
+    ids = torch.randint(0, 151936, (sum(tokens),), generator=g, device=device)
+    batch = build_batch(ids, ids.clone(), torch.tensor([0, 2048, 4096, 6144, 8192]), 32, 151665,
+                        generator=g)
+    N, H = 2 * sum(tokens), 4096
+    x0 = torch.randn(N, H, generator=g, device=device).to(torch.bfloat16)
+    douts = [torch.randn(N, H, generator=g, device=device).to(torch.bfloat16) for _ in range(4)]
+
+    def one_step():
+        outs, gates, exits, state = engine.core_forward(x0, batch, True, generator=g)
+        return engine.core_backward(state, douts)
+
+    for _ in range(warmup):
+        one_step()
+    timer = None
+    if kernel_timing:
+        timer = KernelTimer()
+        timer.wrap(engine)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = 1000.0 * elapsed / steps
+    d = engine.dims
+    qd, kd = d.heads * d.head_dim, d.kv_heads * d.head_dim
+    p_layer = H * (qd + 2 * kd) + qd * H + 3 * H * d.intermediate
+    pairs = sum(allowed_pairs(L, 32) for L in tokens)
+    flops = 4 * (6 * p_layer * N + 12 * d.head_dim * d.heads * pairs)
+    record = {"workload": ("core block: one Qwen3-8B layer (hidden 4096, 32/8 heads, head_dim "
+                           "128, intermediate 12288) x 4 passes with shared weights, 4 x 2048 "
+                           "tokens (16384 dual-stream rows) under the training mask, gates after "
+                           "each pass, committed rows re-embedded from a 151936 x 4096 table; "
+                           "fwd+bwd from N(0, 1) hidden states"),
+              "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 2),
+              "tflop_per_step": round(flops / 1e12, 2),
+              "value": round(flops / (ms / 1000.0) / 1e12, 1), "unit": "TFLOP/s",
+              "mfu": round(flops / (ms / 1000.0) / PEAK_BF16, 4)}
+    if timer is not None:
+        record["roofline"], record["kernel_classes"] = _roofline(timer, steps)
+    print(f"[bench] core block: {ms:.2f} ms/step", file=sys.stderr, flush=True)
+    del model, engine, timer, batch, x0, douts
+    _release()
+    return record
+
+
+def run_readout(device, steps, warmup, kernel_timing):
+    """Readout + objective from 4 passes of [8192 x 2048] final hidden states."""
+    from alodlm_amd.core import readout_batch
+    spec = dict(MODELS["1.7b"], num_hidden_layers=1, loop=(0, 1))
+    model = build_model(spec, device, torch.bfloat16, seed=4)
+    engine = model.engine()
+    g = torch.Generator(device=device).manual_seed(5)
+    N, H, S, L = 8192, 2048, 4, 2048
+    finals = [torch.randn(N, H, generator=g, device=device).to(torch.bfloat16) for _ in range(4)]
+    targets = torch.randint(0, 151936, (N,), generator=g, device=device)
+    t = torch.rand(S, generator=g, device=device).clamp_min(1e-8).repeat_interleave(L)
+    masked = torch.rand(N, generator=g, device=device) < t
+    prob = torch.where(masked, t, torch.zeros_like(t))
+    batch = readout_batch(targets, torch.arange(S + 1, device=device) * L, masked, prob)
+
+    def one_step():
+        out, state = engine.readout_forward(finals, batch, True, generator=g)
+        engine.readout_backward(state, 1.0)
+        return list(engine.last_rows)
+
+    for _ in range(warmup):
+        one_step()
+    timer = None
+    if kernel_timing:
+        timer = KernelTimer()
+        timer.wrap(engine)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rows = [one_step() for _ in range(steps)]
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = 1000.0 * elapsed / steps
+    mean_rows = sum(sum(r) for r in rows) / len(rows)
+    flops = 6 * H * 151936 * mean_rows + 6 * H * N * 4
+    record = {"workload": ("fused readout/objective: final hidden states [8192 x 2048] per pass "
+                           "x 4 passes, LM head 2048 x 151936, final norm + gate, exit sampling, "
+                           "masked cross-entropy and the NELBO / sequence-credit objective "
+                           "(masks Bernoulli(t), t ~ U(0, 1) per 2048-row sequence); fwd+bwd"),
+              "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 2),
+              "loss_bearing_rows_per_step": round(mean_rows, 1),
+              "tflop_per_step": round(flops / 1e12, 2),
+              "value": round(flops / (ms / 1000.0) / 1e12, 1), "unit": "TFLOP/s",
+              "mfu": round(flops / (ms / 1000.0) / PEAK_BF16, 4)}
+    if timer is not None:
+        record["roofline"], record["kernel_classes"] = _roofline(timer, steps)
+    print(f"[bench] readout: {ms:.2f} ms/step", file=sys.stderr, flush=True)
+    del model, engine, timer, finals, batch
+    _release()
+    return record
+
+
 def cpu_baseline(spec, cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     """Time the CPU oracle (float32, torch eager on this host) on a bounded
     sample: `layer_reps` decoder-layer fwd+bwd passes of the model's layer
@@ -223,6 +443,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-kernel-timing", action="store_true")
+    parser.add_argument("--no-sub-records", action="store_true",
+                        help="time the headline step only")
     parser.add_argument("--traffic-calibration", action="store_true",
                         help="first run one plain 1 GiB device copy (read 1 GiB, write "
                              "1 GiB) so that HBM byte counters can be scaled against it")
@@ -234,7 +456,6 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
-    from alodlm_amd.optim import FusedAdamW, param_groups
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     if args.traffic_calibration:
@@ -243,104 +464,44 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    dtype = torch.bfloat16
     spec = MODELS[args.model]
-    model = build_model(spec, device, dtype)
-    engine = model.engine()
-    timer = None
-    gen = torch.Generator().manual_seed(0)
-    seg_lengths = spec["segments"]
-    ids = torch.randint(0, 151936, (sum(seg_lengths),), generator=gen).to(device)
-    labels = ids.clone()
-    bounds = torch.tensor([0] + [sum(seg_lengths[:i + 1]) for i in range(len(seg_lengths))])
-    torch.cuda.manual_seed(0)
-    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-5, max_grad_norm=1.0)
-
-    def one_step():
-        loss, metrics = model(ids, labels, bounds)
-        loss.backward()
-        opt.step()
-        opt.zero_grad(set_to_none=True)
-        return loss
-
-    for i in range(args.warmup):
-        loss = one_step()
-        print(f"[bench] warmup step {i} loss {float(loss):.4f}", file=sys.stderr, flush=True)
-    if not args.no_kernel_timing:
-        timer = KernelTimer()
-        timer.wrap(engine)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    rows = []
-    for i in range(args.steps):
-        loss = one_step()
-        rows.append(list(engine.last_rows))
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    print(f"[bench] timed {args.steps} steps in {elapsed:.3f}s loss {float(loss):.4f}",
-          file=sys.stderr, flush=True)
-    ms = 1000.0 * elapsed / args.steps
-    tokens = sum(seg_lengths)
-    value = tokens * args.steps / elapsed
-    gemm_f, attn_f, head_f = step_flops(engine.dims, model.config, seg_lengths,
-                                        [sum(r) / len(rows) for r in zip(*rows)])
-    step_f = gemm_f + attn_f + head_f
+    timing = not args.no_kernel_timing
+    head, facts = run_step(spec, device, args.steps, args.warmup, timing)
     line = {
         "metric": "train tokens/s, ALoDLM-1.7B & 8B seq2048 on 1 MI355X; % bf16 MFMA peak",
-        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 2), "higher_is_better": True,
+        "value": head["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": (f"{spec['name']} full training step (fwd+bwd+clip+AdamW fp32 "
-                                f"master): {spec['qwen']} shapes, random init, untied, loop "
-                                f"{spec['loop'][0]}-{spec['loop'][1]}, max_depth 4"),
-                   "global_batch": len(seg_lengths), "seq_len": 2048,
-                   "dual_stream_rows": 2 * tokens,
+        "config": {"workload": head["workload"], "global_batch": head["global_batch"],
+                   "seq_len": head["seq_len"], "dual_stream_rows": head["dual_stream_rows"],
                    "parallelism": "none (1 GPU)"},
         "device": device_info(),
-        "memory": {"peak_allocated_gib": round(torch.cuda.max_memory_allocated(device) / 2**30, 1),
-                   "kept_forward_outputs": {"rotary_qk": bool(engine._keep and engine._keep[0]),
-                                            "norm_outputs": bool(engine._keep and engine._keep[1])}},
-        "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
-        "step_tflop": round(step_f / 1e12, 1),
+        "memory": head["memory"], "mfu": head["mfu"], "step_tflop": head["step_tflop"],
     }
-    if timer is not None:
-        summary = timer.summary()
-        dom = max(summary, key=lambda k: summary[k]["ms"])
-        s = summary[dom]
-        achieved = s["flops"] / s["launches"] / (s["ms"] / s["launches"] / 1000.0)
-        line["roofline"] = {"bound": "mfma", "kernel": dom,
-                            "launches_per_step": s["launches"] // args.steps,
-                            "avg_launch_us": round(1000.0 * s["ms"] / s["launches"], 1),
-                            "achieved": round(achieved / 1e12, 1),
-                            "peak": round(PEAK_BF16 / 1e12, 1), "unit": "TFLOP/s",
-                            "frac": round(achieved / PEAK_BF16, 4),
-                            "traffic": None}
-        if dom == "gemm_bf16":
-            traffic_profile = os.path.join(ROOT, "profiles", spec["traffic"])
-            line["roofline"]["algorithmic_bytes_per_launch"] = timer.gemm_bytes // s["launches"]
-            line["roofline"]["traffic"] = profiled_traffic(traffic_profile)
-            line["roofline"]["traffic_source"] = os.path.relpath(traffic_profile, ROOT)
-        line["kernel_classes"] = {k: {"ms_per_step": round(v["ms"] / args.steps, 1),
-                                      "tflops": round(v["flops"] / (v["ms"] / 1000) / 1e12, 1)}
-                                  for k, v in summary.items()}
+    if "roofline" in head:
+        line["roofline"], line["kernel_classes"] = head["roofline"], head["kernel_classes"]
     if not args.no_cpu_baseline:
-        cfg = model.config
-        model_apps = cfg.loop_start + cfg.max_depth * (engine.dims.layers - cfg.loop_start)
-        del opt, model, engine
-        torch.cuda.empty_cache()
         t_layer, t_row, threads = cpu_baseline(spec)
-        apps = model_apps
-        readout_rows = sum(sum(r) for r in rows) / len(rows)
-        t_step = apps * len(seg_lengths) * t_layer + readout_rows * t_row
+        t_step = facts["apps"] * facts["segments"] * t_layer + facts["readout_rows"] * t_row
         line["cpu_baseline"] = {
-            "value": round(tokens / t_step, 4), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"oracle fp32 eager: 3 decoder-layer fwd+bwd passes on one "
-                       f"4096x{spec['hidden_size']} dual-stream segment ({t_layer:.2f}s each) "
-                       f"+ LM head/CE fwd+bwd on 2048 rows x 151936 ({1000 * t_row:.2f} ms/row); "
-                       f"step = {apps} layer applications x {len(seg_lengths)} segments "
-                       f"+ {readout_rows:.0f} readout rows"),
+            "value": round(facts["tokens"] / t_step, 4), "unit": "tokens/s", "cores": threads,
+            "host_cpus": os.cpu_count(), "kind": "port", "extrapolated": True,
+            "sample": (f"oracle fp32 eager on {threads} threads: {3} decoder-layer fwd+bwd "
+                       f"passes on one 4096x{spec['hidden_size']} dual-stream segment "
+                       f"({t_layer:.2f}s each) + LM head/CE fwd+bwd on 2048 rows x 151936 "
+                       f"({1000 * t_row:.2f} ms/row); the step time is extrapolated from "
+                       f"these to {facts['apps']} layer applications x {facts['segments']} "
+                       f"segments + {facts['readout_rows']:.0f} readout rows"),
         }
+    if not args.no_sub_records:
+        subs = {}
+        # the other step configuration at a handful of steps, then the stages
+        other = "8b" if args.model == "1.7b" else "1.7b"
+        rec, _ = run_step(MODELS[other], device, min(args.steps, 5), 2, timing)
+        subs[f"{other.replace('.', 'p')}_step"] = rec
+        subs["core_block"] = run_core_block(device, 10, 2, timing)
+        subs["readout"] = run_readout(device, 10, 2, timing)
+        line["sub_records"] = subs
     print(json.dumps(line), flush=True)
 
 
