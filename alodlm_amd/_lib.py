@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -20,7 +20,7 @@ I32 = ctypes.c_int
 F32 = ctypes.c_float
 
 F32_CODE, BF16_CODE = 0, 1
-EPI_STORE, EPI_RESIDUAL, EPI_ACCUM = 0, 1, 2
+EPI_STORE, EPI_RESIDUAL, EPI_ACCUM, EPI_STORE_F32 = 0, 1, 2, 3
 
 # name -> argument types (every entry point returns int unless listed in _RESTYPE)
 SIGNATURES = {
@@ -71,7 +71,8 @@ SIGNATURES = {
     "alodlm_gate_bwd_workspace": [I64, I64],
     "alodlm_gate_bwd": [P, P, F32, P, P, P, I64, I64, I64, P, I32, P],
     "alodlm_grad_norm": [P, P, P, P, I64, I64, I32, P, P, P],
-    "alodlm_adamw": [P, P, P, P, P, P, P, P, P, I64, I64, P, F32, F32, F32, F32, F32, I64, I32, P],
+    "alodlm_adamw": [P, P, P, P, P, P, P, P, P, I64, I64, P, F32, F32, F32, F32, F32, I64, I32, I32,
+                     P],
     "alodlm_cast_f32": [P, P, P, I64, I32, P],
     "alodlm_scale_f32": [P, P, I64, P],
     "alodlm_transpose": [P, P, I64, I64, I32, P],

@@ -208,21 +208,25 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __rest
     }
 }
 
-// C[m, n] += sum_s partial[s, m, n] (partials summed in split order, then added)
+// C[m, n] (+)= sum_s partial[s, m, n] (partials summed in split order, then
+// added to C, or written over it when `overwrite`)
 __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int64_t splits, int64_t M,
-                                     int64_t N, float* __restrict__ C, int64_t ldc) {
+                                     int64_t N, float* __restrict__ C, int64_t ldc,
+                                     bool overwrite) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * N) return;
   float s = 0.f;
   for (int64_t p = 0; p < splits; ++p) s += partial[p * M * N + i];
-  C[(i / N) * ldc + (i % N)] += s;
+  float* dst = C + (i / N) * ldc + (i % N);
+  *dst = overwrite ? s : *dst + s;
 }
 
 // The same sum, 4 consecutive columns per thread (N, ldc multiples of 4, both
 // buffers 16-byte aligned): grid.x covers a row's N/4 column groups, grid.y
 // strides over rows, so no 64-bit division is needed.
 __global__ void splitk_reduce4_kernel(const float* __restrict__ partial, int64_t splits,
-                                      int64_t M, int64_t N, float* __restrict__ C, int64_t ldc) {
+                                      int64_t M, int64_t N, float* __restrict__ C, int64_t ldc,
+                                      bool overwrite) {
   const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= N) return;
   const int64_t plane = M * N;
@@ -234,9 +238,13 @@ __global__ void splitk_reduce4_kernel(const float* __restrict__ partial, int64_t
       s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
     }
     float4* dst = reinterpret_cast<float4*>(C + m * ldc + n);
-    float4 c = *dst;
-    c.x += s.x; c.y += s.y; c.z += s.z; c.w += s.w;
-    *dst = c;
+    if (overwrite) {
+      *dst = s;
+    } else {
+      float4 c = *dst;
+      c.x += s.x; c.y += s.y; c.z += s.z; c.w += s.w;
+      *dst = c;
+    }
   }
 }
 
@@ -261,15 +269,29 @@ static void splitk_store(const float* partial, int64_t splits, int64_t M, int64_
 }
 
 static void splitk_reduce(const float* partial, int64_t splits, int64_t M, int64_t N, float* C,
-                          int64_t ldc, hipStream_t st) {
+                          int64_t ldc, hipStream_t st, bool overwrite = false) {
   const bool vec = N % 4 == 0 && ldc % 4 == 0 &&
                    ((reinterpret_cast<uintptr_t>(partial) | reinterpret_cast<uintptr_t>(C)) & 15) == 0;
   if (vec) {
     const dim3 grid(ceil_div_u(N / 4, 256), (unsigned)(M < 65535 ? M : 65535));
-    splitk_reduce4_kernel<<<grid, 256, 0, st>>>(partial, splits, M, N, C, ldc);
+    splitk_reduce4_kernel<<<grid, 256, 0, st>>>(partial, splits, M, N, C, ldc, overwrite);
   } else {
-    splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(partial, splits, M, N, C, ldc);
+    splitk_reduce_kernel<<<ceil_div_u(M * N, 256), 256, 0, st>>>(partial, splits, M, N, C, ldc,
+                                                                 overwrite);
   }
+}
+
+// C[m, n] = 0 for an [M, N] float matrix with row stride ldc (a fill kernel,
+// not a memset, so that the launch can be captured in a graph).
+__global__ void zero_rows_kernel(float* __restrict__ C, int64_t M, int64_t N, int64_t ldc) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) C[m * ldc + n] = 0.f;
+}
+
+static void zero_rows(float* C, int64_t M, int64_t N, int64_t ldc, hipStream_t st) {
+  const dim3 grid(ceil_div_u(N, 256), (unsigned)(M < 65535 ? M : 65535));
+  zero_rows_kernel<<<grid, 256, 0, st>>>(C, M, N, ldc);
 }
 
 // ---------------------------------------------------------------------------
@@ -372,7 +394,7 @@ extern "C" int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int ep
     const int64_t s = (M >= 256 && N >= 256 && K % 32 == 0) ? gemm_dl_store_splits(M, N, K) : 1;
     return s > 1 ? s * M * N : 0;
   }
-  if (epilogue != ALODLM_EPI_ACCUM) return 0;
+  if (epilogue != ALODLM_EPI_ACCUM && epilogue != ALODLM_EPI_STORE_F32) return 0;
   int64_t s = splitk_count(M, N, K);
   if (use_big(M, N, K)) {
     const int64_t b = gemm_big_splits(M, N, K);
@@ -412,14 +434,15 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
                            int64_t M, int64_t N, int64_t K, float alpha, int epilogue, int dtype,
                            float* workspace, void* stream) {
   ALODLM_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "gemm: negative shape");
-  ALODLM_CHECK_ARG(epilogue >= 0 && epilogue <= 2, "gemm: bad epilogue");
+  ALODLM_CHECK_ARG(epilogue >= 0 && epilogue <= 3, "gemm: bad epilogue");
   ALODLM_CHECK_ARG(epilogue != ALODLM_EPI_RESIDUAL || R != nullptr, "gemm: residual needs R");
   if (M == 0 || N == 0) return ALODLM_OK;
   hipStream_t st = as_stream(stream);
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
       gemm_dl_eligible(lda, a_kmajor, ldb, b_kmajor, M, N, K)) {
     int64_t splits = 1;
-    if (epilogue == ALODLM_EPI_ACCUM) splits = gemm_dl_splits(M, N, K);
+    if (epilogue == ALODLM_EPI_ACCUM || epilogue == ALODLM_EPI_STORE_F32)
+      splits = gemm_dl_splits(M, N, K);
     else if (epilogue == ALODLM_EPI_STORE) splits = gemm_dl_store_splits(M, N, K);
     if (splits > 1 && workspace == nullptr) splits = 1;
     if (splits > 1) {  // the launch splits K into chunks of whole 32-deep stages
@@ -434,12 +457,19 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
                    (const bf16_t*)R, ldr, M, N, K, alpha, launch_epi, workspace, splits, &nsplit,
                    st);
     ALODLM_CHECK_LAUNCH("gemm_bf16_dl");
-    if (launch_epi == ALODLM_EPI_ACCUM && nsplit > 1) {
+    if ((launch_epi == ALODLM_EPI_ACCUM || launch_epi == ALODLM_EPI_STORE_F32) && nsplit > 1) {
       if (epilogue == ALODLM_EPI_STORE) splitk_store(workspace, nsplit, M, N, (bf16_t*)C, ldc, st);
-      else splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st);
+      else splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st,
+                         epilogue == ALODLM_EPI_STORE_F32);
       ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
     }
     return ALODLM_OK;
+  }
+  if (epilogue == ALODLM_EPI_STORE_F32) {
+    // the other kernels accumulate into a zeroed output
+    zero_rows((float*)C, M, N, ldc, st);
+    ALODLM_CHECK_LAUNCH("gemm_zero_output");
+    epilogue = ALODLM_EPI_ACCUM;
   }
   if (dtype == ALODLM_BF16 && mfma_eligible(A, lda, a_kmajor, B, ldb, b_kmajor, M, N, K) &&
       use_big(M, N, K, a_kmajor || b_kmajor)) {

@@ -284,7 +284,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   // (chunk' = chunk ^ (row & 31)), then each thread moves 16-byte chunks, 32
   // threads per row (and reads the matching 16 bytes of R).
   bf16_t* Cb = reinterpret_cast<bf16_t*>(C);
-  if constexpr (EPI != ALODLM_EPI_ACCUM) {
+  if constexpr (EPI == ALODLM_EPI_STORE || EPI == ALODLM_EPI_RESIDUAL) {
     const bool coalesced = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0 &&
                            (EPI != ALODLM_EPI_RESIDUAL ||
                             (ldr % 8 == 0 && reinterpret_cast<uintptr_t>(R) % 16 == 0));
@@ -427,6 +427,8 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
                            pack_bf16x2(o[2], o[3]));
           } else if (P) {
             *reinterpret_cast<float4*>(P + m * N + n) = make_float4(v[0], v[1], v[2], v[3]);
+          } else if (EPI == ALODLM_EPI_STORE_F32) {
+            *reinterpret_cast<float4*>(Cf + m * ldc + n) = make_float4(v[0], v[1], v[2], v[3]);
           } else {
             float4* dst = reinterpret_cast<float4*>(Cf + m * ldc + n);
             float4 o = *dst;
@@ -441,6 +443,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
             else if (EPI == ALODLM_EPI_RESIDUAL)
               Cb[m * ldc + n + e] = float_to_bf16(bf16_to_float(R[m * ldr + n + e]) + round_bf16(v[e]));
             else if (P) P[m * N + n + e] = v[e];
+            else if (EPI == ALODLM_EPI_STORE_F32) Cf[m * ldc + n + e] = v[e];
             else Cf[m * ldc + n + e] += v[e];
           }
         }
@@ -500,6 +503,9 @@ static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
   else if (epi == ALODLM_EPI_RESIDUAL)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
+  else if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE_F32, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
   else
     gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
@@ -516,7 +522,7 @@ static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t
 }
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
-// splits > 1 (ALODLM_EPI_ACCUM only), the caller reduces it.
+// splits > 1 (float-output epilogues only), the caller reduces it.
 void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
@@ -525,7 +531,7 @@ void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B,
   if (splits > 1) kps = (((K + splits - 1) / splits) + KMIN - 1) / KMIN * KMIN;
   const int64_t nsplit = (K + kps - 1) / kps;
   *nsplit_out = nsplit;
-  float* p = (epi == ALODLM_EPI_ACCUM && nsplit > 1) ? part : nullptr;
+  float* p = ((epi == ALODLM_EPI_ACCUM || epi == ALODLM_EPI_STORE_F32) && nsplit > 1) ? part : nullptr;
   if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
   else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
   else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);

@@ -60,7 +60,7 @@ final_norm_kernel(const float* __restrict__ partial, int64_t n, float* __restric
   if (threadIdx.x == 0) total[0] = sqrtf(s);
 }
 
-template <typename T>
+template <typename T, typename G>
 __global__ void __launch_bounds__(OPT_THREADS)
 adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master,
              float* const* __restrict__ exp_avg, float* const* __restrict__ exp_avg_sq,
@@ -80,7 +80,7 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   float* w = master[t];
   float* m = exp_avg[t];
   float* v = exp_avg_sq[t];
-  const T* g = reinterpret_cast<const T*>(grads[t]);
+  const G* g = reinterpret_cast<const G*>(grads[t]);
   const bool separate = reinterpret_cast<void*>(w) != reinterpret_cast<void*>(p);
   auto update = [&](float gi, float& wi, float& mi, float& vi) {
     gi *= clip;
@@ -94,9 +94,10 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   // float32 state 16-byte aligned; 4 gradient / parameter elements are 16
   // bytes (float) or 8 bytes (bf16)
   constexpr uintptr_t half = sizeof(T) == 2 ? 2 : 1;
+  constexpr uintptr_t ghalf = sizeof(G) == 2 ? 2 : 1;
   const uintptr_t align = reinterpret_cast<uintptr_t>(w + beg) | reinterpret_cast<uintptr_t>(m + beg) |
                           reinterpret_cast<uintptr_t>(v + beg) |
-                          reinterpret_cast<uintptr_t>(g + beg) * half |
+                          reinterpret_cast<uintptr_t>(g + beg) * ghalf |
                           (separate ? reinterpret_cast<uintptr_t>(p + beg) * half : 0);
   if ((align & 15) == 0) {
     // 4 elements per thread and step: 16-byte float32 state, 4 * sizeof(T)
@@ -108,7 +109,7 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
       float4 v4 = *reinterpret_cast<const float4*>(v + j);
       float gv[4], wv[4] = {w4.x, w4.y, w4.z, w4.w}, mv[4] = {m4.x, m4.y, m4.z, m4.w},
                    vv[4] = {v4.x, v4.y, v4.z, v4.w};
-      if constexpr (sizeof(T) == 2) {
+      if constexpr (sizeof(G) == 2) {
         const uint2 gr = *reinterpret_cast<const uint2*>(g + j);
         gv[0] = bf16_to_float((bf16_t)(gr.x & 0xffff)); gv[1] = bf16_to_float((bf16_t)(gr.x >> 16));
         gv[2] = bf16_to_float((bf16_t)(gr.y & 0xffff)); gv[3] = bf16_to_float((bf16_t)(gr.y >> 16));
@@ -135,7 +136,7 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   }
   for (i += threadIdx.x; i < end; i += OPT_THREADS) {
     float wi = w[i], mi = m[i], vi = v[i];
-    update(Elem<T>::load(g, i), wi, mi, vi);
+    update(Elem<G>::load(g, i), wi, mi, vi);
     m[i] = mi;
     v[i] = vi;
     w[i] = wi;
@@ -165,18 +166,26 @@ extern "C" int alodlm_adamw(void* const* params, float* const* master, float* co
                             const int64_t* numels, const float* weight_decay, int64_t n_chunks,
                             int64_t chunk_size, const float* total_norm, float max_norm, float lr,
                             float beta1, float beta2, float eps, int64_t step, int dtype,
-                            void* stream) {
+                            int grad_dtype, void* stream) {
   ALODLM_CHECK_ARG(n_chunks > 0 && chunk_size > 0, "adamw: empty tensor list");
   ALODLM_CHECK_ARG(step >= 1, "adamw: step must be >= 1");
   const double bc1 = 1.0 - pow((double)beta1, (double)step);
   const double bc2 = 1.0 - pow((double)beta2, (double)step);
   const float step_size = (float)((double)lr / bc1);
   const float bc2_sqrt = (float)sqrt(bc2);
+  ALODLM_CHECK_ARG(grad_dtype == dtype || grad_dtype == ALODLM_F32,
+                   "adamw: gradients are float32 or of the parameter dtype");
   ALODLM_DISPATCH(dtype, T, {
-    adamw_kernel<T><<<(unsigned)n_chunks, OPT_THREADS, 0, as_stream(stream)>>>(
-        params, master, exp_avg, exp_avg_sq, grads, chunk_tensor, chunk_start, numels,
-        weight_decay, chunk_size, total_norm, max_norm, lr, beta1, beta2, eps, step_size,
-        bc2_sqrt);
+    if (grad_dtype == ALODLM_F32)
+      adamw_kernel<T, float><<<(unsigned)n_chunks, OPT_THREADS, 0, as_stream(stream)>>>(
+          params, master, exp_avg, exp_avg_sq, grads, chunk_tensor, chunk_start, numels,
+          weight_decay, chunk_size, total_norm, max_norm, lr, beta1, beta2, eps, step_size,
+          bc2_sqrt);
+    else
+      adamw_kernel<T, T><<<(unsigned)n_chunks, OPT_THREADS, 0, as_stream(stream)>>>(
+          params, master, exp_avg, exp_avg_sq, grads, chunk_tensor, chunk_start, numels,
+          weight_decay, chunk_size, total_norm, max_norm, lr, beta1, beta2, eps, step_size,
+          bc2_sqrt);
   });
   ALODLM_CHECK_LAUNCH("adamw");
   return ALODLM_OK;

@@ -31,7 +31,7 @@ import math
 import torch
 
 from . import _lib
-from ._lib import EPI_ACCUM, call, ptr, query
+from ._lib import EPI_ACCUM, EPI_STORE_F32, call, ptr, query
 from .batch import build_batch
 from .layers import Kernels, LayerGrads, LayerWeights, Rope
 
@@ -65,24 +65,32 @@ class Dims:
         return (self.heads + 2 * self.kv_heads) * self.head_dim
 
 
-_LAYER_ORDER = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
-                "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
-                "mlp.down_proj.weight", "input_layernorm.weight",
-                "post_attention_layernorm.weight", "self_attn.q_norm.weight",
-                "self_attn.k_norm.weight")
+_LAYER_MATRICES = ("self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                   "self_attn.v_proj.weight", "self_attn.o_proj.weight", "mlp.gate_proj.weight",
+                   "mlp.up_proj.weight", "mlp.down_proj.weight")
+_LAYER_NORMS = ("input_layernorm.weight", "post_attention_layernorm.weight",
+                "self_attn.q_norm.weight", "self_attn.k_norm.weight")
 _ALIGN = 64  # elements
 
 
 class Arena:
-    """Parameters re-homed into one flat buffer, in a fixed order."""
+    """Parameters re-homed into one flat buffer, in a fixed order: the word
+    embedding, every layer's projection matrices, the LM head, then one block
+    of all the small tensors (norm weights, gate).  The float32 gradient arena
+    has the same layout: its matrices receive their first contribution by
+    overwriting, so only the embedding (sparse rows) and the small block are
+    zeroed before a backward (``zero_spans``)."""
 
     def __init__(self, named_params, dims, device, dtype):
         self.dims, self.device, self.dtype = dims, device, dtype
         order = ["backbone.model.embed_tokens.weight"]
         for i in range(dims.layers):
-            order += [f"backbone.model.layers.{i}.{s}" for s in _LAYER_ORDER]
-        order += ["backbone.model.norm.weight", "backbone.lm_head.weight",
-                  "exit_gate.net.weight", "exit_gate.net.bias", "exit_gate.depth_bias"]
+            order += [f"backbone.model.layers.{i}.{s}" for s in _LAYER_MATRICES]
+        order += ["backbone.lm_head.weight"]
+        small = [f"backbone.model.layers.{i}.{s}" for i in range(dims.layers) for s in _LAYER_NORMS]
+        small += ["backbone.model.norm.weight", "exit_gate.net.weight", "exit_gate.net.bias",
+                  "exit_gate.depth_bias"]
+        order += small
         params = dict(named_params)
         missing = set(order) ^ set(params)
         if missing:
@@ -97,6 +105,11 @@ class Arena:
             self.offsets[name] = total
             total += numel
         self.total = (total + _ALIGN - 1) // _ALIGN * _ALIGN
+        embed_end = params["backbone.model.embed_tokens.weight"].numel()
+        self.zero_spans = [(0, embed_end), (self.offsets[small[0]], self.total)]
+        self.lm_span = (self.offsets["backbone.lm_head.weight"],
+                        self.offsets["backbone.lm_head.weight"]
+                        + params["backbone.lm_head.weight"].numel())
         self.flat = torch.empty(self.total, dtype=dtype, device=device)
         self.params = []
         for name in order:
@@ -204,6 +217,13 @@ class StepEngine(Kernels):
         self._keep_rows = 0
         self._step_alloc = None
         self._step_peak = None
+        # float32 gradients of the step in the arena layout (kept across steps)
+        self.grads = None
+        # a FusedAdamW that reads self.grads directly (see model._Step), and
+        # whether self.grads holds gradients not yet consumed by its step
+        self.fused_optimizer = None
+        self.grads_pending = False
+        self._written = None
 
     # ------------------------------------------------------------------ memory policy
     KEEP_FRACTION = 0.95  # of the device memory a step may plan to use
@@ -213,8 +233,10 @@ class StepEngine(Kernels):
         keeps neither and measures how far its forward and backward raise the
         allocated memory (the device's peak statistics are reset at its start);
         the second step decides once, keeping each set only if the allocations
-        live at its start (the optimizer state included by then) plus that
-        growth plus the set's bytes stay under KEEP_FRACTION of the device."""
+        live at its start, plus that growth, plus optimizer state still to be
+        allocated (the decision can precede the first optimizer step under
+        gradient accumulation), plus the set's bytes stay under KEEP_FRACTION
+        of the device."""
         dev = self.device
         if self._keep is not None:
             # a pack with more rows than the one the decision was made for
@@ -223,6 +245,7 @@ class StepEngine(Kernels):
         if self._step_alloc is None:
             torch.cuda.reset_peak_memory_stats(dev)
             self._step_alloc = torch.cuda.memory_allocated(dev)
+            self._grads_existed = self.grads is not None
             return (False, False)
         if self._step_peak is None:  # the first step ran no backward
             return (False, False)
@@ -233,12 +256,27 @@ class StepEngine(Kernels):
         elem = 2 if self.dtype == torch.bfloat16 else 4
         rotary = apps * N * (d.heads + d.kv_heads) * d.head_dim * elem
         norms = apps * N * 2 * d.hidden * elem
-        used = torch.cuda.memory_allocated(dev) + growth
+        used = torch.cuda.memory_allocated(dev) + growth + self._optimizer_state_to_come()
+        if not self._grads_existed and self.grads is not None:
+            # the float32 gradient arena was allocated during the first step:
+            # it is in both the growth and the memory now allocated
+            used -= self.grads.numel() * 4
         keep_rot = used + rotary <= budget
         keep_norm = keep_rot and used + rotary + norms <= budget
         self._keep = (keep_rot, keep_norm)
         self._keep_rows = N
         return self._keep
+
+    def _optimizer_state_to_come(self):
+        """Bytes of optimizer state that may still be allocated after the
+        keep decision (with gradient accumulation the decision can come
+        before the first optimizer step): the bound FusedAdamW's state not yet
+        allocated, or - with no FusedAdamW bound - AdamW's float32 master and
+        moments for every parameter (12 bytes each), counted conservatively
+        because another optimizer's allocations are not visible here."""
+        if self.fused_optimizer is not None:
+            return self.fused_optimizer.state_bytes_to_come()
+        return 12 * sum(p.numel() for p in self.arena.params)
 
     # ------------------------------------------------------------------ layer fwd/bwd
     def _layer_fwd(self, li, x, b, save):
@@ -247,8 +285,13 @@ class StepEngine(Kernels):
 
     def _layer_bwd(self, dy, saved, b, g):
         li = saved[0]
+        # a layer's first backward application writes its matrices' gradients
+        # (the arena is not zeroed there); later ones accumulate
+        first = self._written is not None and li not in self._written
+        if first:
+            self._written.add(li)
         return self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li], b.kernel_mask,
-                              self._rope)
+                              self._rope, first=first)
 
     # ------------------------------------------------------------------ shared pieces
     def _carry(self, core_out, b, exits, depth):
@@ -344,8 +387,10 @@ class StepEngine(Kernels):
              self._stream())
         return out, dgate
 
-    def _readout_bwd(self, rec, depth, dgate, grad_scale, g_lm, g_norm, g_gw, g_gb, g_db):
-        """Backward of pass ``depth``'s readout: LM head dX/dW, gate head, final
+    def _readout_bwd(self, rec, depth, dgate, grad_scale, g_lm, g_norm, g_gw, g_gb, g_db,
+                     first_lm=False):
+        """Backward of pass ``depth``'s readout: LM head dX/dW (``first_lm``:
+        the LM head's gradient is written, not accumulated), gate head, final
         norm; returns d final_in."""
         d = self.dims
         N, H = rec["readout"].shape
@@ -359,7 +404,8 @@ class StepEngine(Kernels):
             self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
                        alpha=grad_scale)
             self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H,
-                       rec["xsel"].shape[0], alpha=grad_scale, epi=EPI_ACCUM)
+                       rec["xsel"].shape[0], alpha=grad_scale,
+                       epi=EPI_STORE_F32 if first_lm else EPI_ACCUM)
             call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
                  c, st)
             del dsel
@@ -441,21 +487,33 @@ class StepEngine(Kernels):
                  "prelude": saves, "depths": depths}
         return out, state
 
-    def backward(self, state, grad_scale):
-        """Backward of the step; returns float32 gradients in the arena layout."""
+    def backward(self, state, grad_scale, accumulate=False):
+        """Backward of the step into the float32 gradient arena ``self.grads``
+        (returned).  Without ``accumulate`` the arena's previous contents are
+        replaced: each matrix's first contribution is written, the embedding
+        and the small tensors are zeroed first; with it every contribution is
+        added (gradient accumulation)."""
         cfg, d = self.cfg, self.dims
         K, st, c = cfg.max_depth, self._stream(), self.code
         b = state["batch"]
         N, H, V = b.ids.numel(), d.hidden, d.vocab
-        grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
+        if self.grads is None:
+            self.grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
+        grads = self.grads
+        self._written = None if accumulate else set()
+        if not accumulate:
+            for lo, hi in self.arena.zero_spans:
+                grads[lo:hi].zero_()
         self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
         g_embed, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
         dnext = None  # gradient at the core input of depth+1
+        lm_written = accumulate
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
             dr = self._readout_bwd(rec, depth, state["dgate"][depth], grad_scale, g_lm, g_norm,
-                                   g_gw, g_gb, g_db)
+                                   g_gw, g_gb, g_db, first_lm=not lm_written)
+            lm_written = lm_written or rec["R"] > 0
             for saved in reversed(rec["coda_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             if dnext is not None:
@@ -470,9 +528,18 @@ class StepEngine(Kernels):
             dx = self._layer_bwd(dx, saved, b, grads)
         call("alodlm_embed_scatter_add", ptr(dx), ptr(b.ids), None, 0, ptr(g_embed), N, H, V, c,
              st)
+        if not lm_written:
+            # no pass had a loss-bearing row: the LM head's gradient is zero
+            lo, hi = self.arena.lm_span
+            grads[lo:hi].zero_()
+        self._written = None
+        return grads
+
+    def note_step_peak(self):
+        """Record the first step's memory peak (forward, backward and the
+        gradients handed to autograd) for the keep decision."""
         if self._step_alloc is not None and self._step_peak is None:
             self._step_peak = torch.cuda.max_memory_allocated(self.device)
-        return grads
 
     # ------------------------------------------------------------------ stages
     def core_forward(self, x0, batch, need_grad=True, exit_uniforms=None, generator=None):
@@ -523,6 +590,7 @@ class StepEngine(Kernels):
         b = state["batch"]
         grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
         self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
+        self._written = None
         g_embed, g_norm, _, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
         dnext = None

@@ -11,6 +11,7 @@ hand-scheduled backward and fills every parameter's ``.grad``.
 
 import json
 import math
+import weakref
 from dataclasses import asdict
 from pathlib import Path
 
@@ -45,7 +46,14 @@ class GateHead(nn.Module):
 
 
 class _Step(torch.autograd.Function):
-    """One autograd node for the whole step; inputs are the arena parameters."""
+    """One autograd node for the whole step; inputs are the arena parameters.
+
+    The backward fills the engine's float32 gradient arena.  With a bound
+    FusedAdamW (``engine.fused_optimizer``) the parameters' ``.grad`` stay
+    unset: the optimizer reads the float32 arena itself (no rounding to the
+    parameter dtype, no second arena; ``ALoDLM.materialize_grads`` fills
+    ``.grad`` on request) and consecutive backward calls accumulate there.
+    Otherwise the gradients are handed to autograd in the parameter dtype."""
 
     @staticmethod
     def forward(ctx, engine, inputs, need_grad, *params):
@@ -53,6 +61,7 @@ class _Step(torch.autograd.Function):
         out, state = engine.forward(ids, labels, boundaries, need_grad, **extra)
         ctx.engine = engine
         ctx.state = state if need_grad else None
+        ctx.nparams = len(params)
         metrics = out[1:].clone()
         ctx.mark_non_differentiable(metrics)
         return out[0].clone(), metrics
@@ -62,22 +71,41 @@ class _Step(torch.autograd.Function):
         engine, state = ctx.engine, ctx.state
         if state is None:
             raise RuntimeError("the step was run without gradient tracking")
+        ctx.state = None
+        if engine.fused_optimizer is not None:
+            # the upstream gradient scales the LM head and gate products
+            # (everything else is linear in them); one read of the scalar
+            engine.backward(state, float(grad_loss), accumulate=engine.grads_pending)
+            del state
+            engine.grads_pending = True
+            engine.note_step_peak()
+            return (None, None, None, *([None] * ctx.nparams))
         # The backward is linear in the loss's upstream gradient: it runs for a
         # unit seed and the seed (a device scalar, never read on the host, so
-        # the host does not wait for the forward here) scales the result.
+        # the host does not wait for the forward here) scales the result while
+        # it is cast to the parameter dtype.
         seed = grad_loss.detach().to(device=engine.device, dtype=torch.float32).reshape(1)
         grads = engine.backward(state, 1.0)
-        ctx.state = None
-        stream = _lib.stream_handle(engine.device)
-        if engine.dtype == torch.float32:
-            flat = grads
-            _lib.call("alodlm_scale_f32", _lib.ptr(flat), _lib.ptr(seed), flat.numel(), stream)
-        else:
-            flat = torch.empty(engine.arena.total, dtype=engine.dtype, device=engine.device)
-            _lib.call("alodlm_cast_f32", _lib.ptr(grads), _lib.ptr(seed), _lib.ptr(flat),
-                      grads.numel(), engine.code, stream)
+        del state
+        flat = torch.empty(engine.arena.total, dtype=engine.dtype, device=engine.device)
+        _lib.call("alodlm_cast_f32", _lib.ptr(grads), _lib.ptr(seed), _lib.ptr(flat),
+                  grads.numel(), engine.code, _lib.stream_handle(engine.device))
+        engine.note_step_peak()
         views = [engine.arena.view(flat, name) for name in engine.arena.names]
         return (None, None, None, *views)
+
+
+_MODELS = weakref.WeakSet()
+
+
+def model_of(params):
+    """The ALoDLM whose parameters are exactly ``params`` (by identity), or None."""
+    ids = {id(p) for p in params}
+    for model in list(_MODELS):
+        mine = list(model.parameters())
+        if len(mine) == len(ids) and all(id(p) in ids for p in mine):
+            return model
+    return None
 
 
 class ALoDLM(nn.Module):
@@ -89,6 +117,8 @@ class ALoDLM(nn.Module):
         self.exit_gate = GateHead(backbone.config.hidden_size, config.gate_init_pi)
         self.exit_gate.to(dtype=backbone.dtype, device=backbone.device)
         self._engine = None
+        self._fused_optimizer = None
+        _MODELS.add(self)
 
     @classmethod
     def from_pretrained(cls, directory, config=None, dtype=torch.float32, require_gate=True):
@@ -137,9 +167,42 @@ class ALoDLM(nn.Module):
 
     def engine(self):
         """The step engine bound to the current parameter storage."""
-        if self._engine is None or not self._engine.arena.valid():
+        if self._engine is not None and not self._engine.arena.valid():
+            if self._fused_optimizer is not None:
+                raise RuntimeError("the model's parameters were moved after a FusedAdamW was "
+                                   "bound to them; build the optimizer after moving the model")
+            self._engine = None
+        if self._engine is None:
             self._engine = StepEngine(self)
+            self._engine.fused_optimizer = self._fused_optimizer
         return self._engine
+
+    def bind_optimizer(self, optimizer):
+        """Let ``optimizer`` (a FusedAdamW over exactly this model's
+        parameters) read the step's float32 gradients directly; called by
+        FusedAdamW itself."""
+        self._fused_optimizer = optimizer
+        if self._engine is not None:
+            self._engine.fused_optimizer = optimizer
+
+    def float32_grads(self):
+        """name -> float32 gradient of the last backward(s) since zero_grad when
+        a FusedAdamW reads them from the step's arena, else None."""
+        e = self._engine
+        if e is None or e.fused_optimizer is None or not e.grads_pending:
+            return None
+        return {name: e.arena.view(e.grads, name) for name in e.arena.names}
+
+    def materialize_grads(self):
+        """Fill every parameter's ``.grad`` (parameter dtype) from the float32
+        gradients a bound FusedAdamW reads, for code that inspects ``.grad``;
+        a no-op when autograd already filled them."""
+        grads = self.float32_grads()
+        if grads is None:
+            return
+        named = dict(self.named_parameters())
+        for name, g in grads.items():
+            named[name].grad = g.to(named[name].dtype)
 
     def forward(self, ids, labels, boundaries, exit_uniforms=None, draws=None, generator=None):
         """The training step's forward (alodlm/model.py:171-187).

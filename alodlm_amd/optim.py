@@ -7,8 +7,13 @@ max_norm)``.  Differences by design: bf16 parameters keep a float32 master copy
 and float32 moments (the reference's plain bf16 run keeps bf16 parameters and
 moments; its ZeRO-2 run keeps float32 masters), and the clip coefficient is
 applied inside the AdamW kernel from a device-side norm, so no host sync is
-needed.
+needed.  Over exactly the parameters of an ALoDLM model the optimizer reads
+the step's float32 gradient arena itself (no rounding of the gradients to
+bf16, no bf16 gradient copy); ``.grad`` then stays unset unless
+``ALoDLM.materialize_grads()`` is called.
 """
+
+import weakref
 
 import torch
 
@@ -56,6 +61,51 @@ class FusedAdamW(torch.optim.Optimizer):
         self.last_grad_norm = None
         self._tables = None
         self._norm_ready = False
+        # Over exactly the parameters of an ALoDLM, read the step's float32
+        # gradient arena directly instead of .grad (see model._Step).
+        from .model import model_of
+        model = model_of(self._params())
+        self._model = None
+        if model is not None:
+            self._model = weakref.ref(model)
+            self._names = {id(p): name for name, p in model.named_parameters()}
+            model.bind_optimizer(self)
+
+    def _bound_engine(self):
+        model = self._model() if self._model is not None else None
+        engine = model._engine if model is not None else None
+        return engine if engine is not None and engine.fused_optimizer is self else None
+
+    def state_bytes_to_come(self):
+        """Bytes of float32 master / moment state not allocated yet (allocated
+        at the first step): 8 per element, 12 when the parameter is not float32."""
+        total = 0
+        for p in self._params():
+            if not self.state.get(p):
+                total += p.numel() * (8 if p.dtype == torch.float32 else 12)
+        return total
+
+    def _grads(self, params):
+        """(gradient tensors, dtype code) for ``params``: the bound model's
+        float32 arena views, or ``.grad`` (zeros where unset).  None when the
+        bound model holds no gradients since the last zero_grad."""
+        engine = self._bound_engine()
+        if engine is not None:
+            if not engine.grads_pending:
+                return None, None
+            return ([engine.arena.view(engine.grads, self._names[id(p)]) for p in params],
+                    _lib.F32_CODE)
+        grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in params]
+        for g in grads:
+            if g.dtype != self._dtype or not g.is_contiguous():
+                raise ValueError("gradients must be contiguous and of the parameter dtype")
+        return grads, self._code
+
+    def _check_tables(self):
+        """(Re)build the pointer tables when parameters were moved or re-homed
+        since they were built."""
+        if self._tables is None or [p.data_ptr() for p in self._params()] != self._ptrs:
+            self._prepare()
 
     def _params(self):
         return [p for g in self.param_groups for p in g["params"]]
@@ -79,6 +129,11 @@ class FusedAdamW(torch.optim.Optimizer):
                                    else p.detach().float().clone())
                 state["exp_avg"] = torch.zeros(p.shape, dtype=torch.float32, device=device)
                 state["exp_avg_sq"] = torch.zeros(p.shape, dtype=torch.float32, device=device)
+            elif p.dtype == torch.float32 and state["master"].data_ptr() != p.data_ptr():
+                # a float32 parameter is its own master: follow it to its new
+                # storage (the step engine re-homes parameters into its arena)
+                p.data.copy_(state["master"])
+                state["master"] = p.detach()
         self._tables = []
         for group in self.param_groups:
             ps = group["params"]
@@ -96,9 +151,13 @@ class FusedAdamW(torch.optim.Optimizer):
         self._all = _Table(params, device)
         self._partial = torch.empty(self._all.n_chunks, dtype=torch.float32, device=device)
         self._norm = torch.zeros(1, dtype=torch.float32, device=device)
+        self._ptrs = [p.data_ptr() for p in params]
 
     def zero_grad(self, set_to_none=True):
         self._norm_ready = False
+        engine = self._bound_engine()
+        if engine is not None:
+            engine.grads_pending = False
         super().zero_grad(set_to_none)
 
     def load_state_dict(self, state_dict):
@@ -141,18 +200,18 @@ class FusedAdamW(torch.optim.Optimizer):
 
         The next ``step()`` clips with this norm instead of computing it again,
         so the gradients must not change in between."""
-        if self._tables is None:
-            self._prepare()
+        self._check_tables()
         params = self._params()
-        grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in params]
-        for g in grads:
-            if g.dtype != self._dtype or not g.is_contiguous():
-                raise ValueError("gradients must be contiguous and of the parameter dtype")
-        gptr = _Table.pointers(grads, self._device)
-        _lib.call("alodlm_grad_norm", _lib.ptr(gptr), _lib.ptr(self._all.chunk_tensor),
-                  _lib.ptr(self._all.chunk_start), _lib.ptr(self._all.numels),
-                  self._all.n_chunks, CHUNK, self._code, _lib.ptr(self._partial),
-                  _lib.ptr(self._norm), _lib.stream_handle(self._device))
+        grads, code = self._grads(params)
+        if grads is None:
+            self._norm.zero_()
+            grads = []
+        else:
+            gptr = _Table.pointers(grads, self._device)
+            _lib.call("alodlm_grad_norm", _lib.ptr(gptr), _lib.ptr(self._all.chunk_tensor),
+                      _lib.ptr(self._all.chunk_start), _lib.ptr(self._all.numels),
+                      self._all.n_chunks, CHUNK, code, _lib.ptr(self._partial),
+                      _lib.ptr(self._norm), _lib.stream_handle(self._device))
         self.last_grad_norm = self._norm[0]
         self._norm_ready = True
         return self._norm[0], grads
@@ -160,8 +219,11 @@ class FusedAdamW(torch.optim.Optimizer):
     @torch.no_grad()
     def step(self, closure=None):
         loss = closure() if closure is not None else None
-        if self._tables is None:
-            self._prepare()
+        self._check_tables()
+        if self._bound_engine() is not None and not self._bound_engine().grads_pending:
+            # no gradients since zero_grad: nothing to update (torch's AdamW
+            # skips parameters whose .grad is None)
+            return loss
         norm_ptr = None
         if self.max_grad_norm is not None:
             if not self._norm_ready:
@@ -172,7 +234,7 @@ class FusedAdamW(torch.optim.Optimizer):
             if table is None:
                 continue
             ps = group["params"]
-            grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in ps]
+            grads, gcode = self._grads(ps)
             steps = {self.state[p]["step"] for p in ps}
             if len(steps) != 1:
                 raise RuntimeError("parameters of one group must share their step count")
@@ -186,7 +248,7 @@ class FusedAdamW(torch.optim.Optimizer):
                       _lib.ptr(table.chunk_tensor), _lib.ptr(table.chunk_start),
                       _lib.ptr(table.numels), _lib.ptr(table.wd), table.n_chunks, CHUNK,
                       norm_ptr, float(self.max_grad_norm or 0.0), float(group["lr"]),
-                      float(beta1), float(beta2), float(group["eps"]), step, self._code,
+                      float(beta1), float(beta2), float(group["eps"]), step, self._code, gcode,
                       _lib.stream_handle(self._device))
         return loss
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 1
+#define ALODLM_ABI_VERSION 2
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -177,13 +177,16 @@ int alodlm_rotary_bwd(const void* dout, const void* cos_tab, const void* sin_tab
  * epilogue: ALODLM_EPI_STORE    C = alpha*acc                (C in dtype)
  *           ALODLM_EPI_RESIDUAL C = R + cast(alpha*acc)       (C, R in dtype; may alias)
  *           ALODLM_EPI_ACCUM    Cf32 += alpha*acc             (C is float)
+ *           ALODLM_EPI_STORE_F32 Cf32 = alpha*acc            (C is float: the first
+ *                               contribution to a gradient, which then needs no zeroing)
  * workspace: float scratch of alodlm_gemm_workspace(M, N, K, epilogue, dtype)
  * floats for split-K partials: ALODLM_EPI_ACCUM products with few output
  * tiles, and bf16 ALODLM_EPI_STORE products with K >= 16384 and few output
  * tiles (summed in split order, then rounded once).  May be NULL (the
  * product then runs unsplit); unused when the query returns 0.
  * ------------------------------------------------------------------------ */
-enum { ALODLM_EPI_STORE = 0, ALODLM_EPI_RESIDUAL = 1, ALODLM_EPI_ACCUM = 2 };
+enum { ALODLM_EPI_STORE = 0, ALODLM_EPI_RESIDUAL = 1, ALODLM_EPI_ACCUM = 2,
+       ALODLM_EPI_STORE_F32 = 3 };
 int64_t alodlm_gemm_workspace(int64_t M, int64_t N, int64_t K, int epilogue, int dtype);
 int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t ldb,
                 int b_kmajor, void* C, int64_t ldc, const void* R, int64_t ldr, int64_t M,
@@ -381,7 +384,9 @@ int alodlm_gate_bwd(const float* dgate, const void* readout, float scale, float*
  * for `step` (>= 1) on the float master; m and v float; the dtype param is
  * rewritten from the master when it is a separate tensor.  If total_norm is
  * not NULL the gradient is scaled by min(1, max_norm/(total_norm+1e-6)),
- * read on the device.
+ * read on the device.  grad_dtype is the gradients' storage type: `dtype`,
+ * or ALODLM_F32 for float32 gradients of bf16 parameters (the step's
+ * float32 gradient arena, read without a rounding to bf16).
  * ------------------------------------------------------------------------ */
 int alodlm_grad_norm(const void* const* grads, const int32_t* chunk_tensor,
                      const int64_t* chunk_start, const int64_t* numels, int64_t n_chunks,
@@ -392,7 +397,7 @@ int alodlm_adamw(void* const* params, float* const* master, float* const* exp_av
                  const int32_t* chunk_tensor, const int64_t* chunk_start, const int64_t* numels,
                  const float* weight_decay, int64_t n_chunks, int64_t chunk_size,
                  const float* total_norm, float max_norm, float lr, float beta1, float beta2,
-                 float eps, int64_t step, int dtype, void* stream);
+                 float eps, int64_t step, int dtype, int grad_dtype, void* stream);
 
 /* Elementwise helpers. */
 /* dst = cast(src * scale[0]); scale is a device scalar or null (no scaling).

@@ -89,3 +89,118 @@ def test_fused_adamw_bf16_parameters_keep_float32_masters():
         gi = p.grad.double().cpu() * clip
         want = w0 * (1 - lr * 0.01) - lr * gi / (gi.abs() + 1e-8)
         torch.testing.assert_close(master.double().cpu(), want, atol=1e-6, rtol=1e-5)
+
+
+def _tiny_bf16(seed):
+    from oracle import step as O
+    from tests.helpers import make_model
+    dims = O.Dims(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=768, vocab=1024,
+                  layers=4, eps=1e-6, theta=1e6)
+    obj = O.Objective(loop_start=1, loop_end=3, mask_token_id=3, block_size=32)
+    params = O.init_params(dims, obj.gate_init_pi, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    params["exit_gate.net.weight"] = 0.02 * torch.randn(1, dims.hidden, generator=g)
+    model = make_model(dims, obj, params, dtype=torch.bfloat16)
+    ids = torch.randint(0, dims.vocab, (512,), generator=g)
+    return model, obj, ids, torch.tensor([0, 128, 256, 384, 512])
+
+
+def _step_inputs(obj, ids, bounds, seed):
+    from tests.helpers import cpu_draws
+    draws, uniforms = cpu_draws(ids, bounds, obj.block_size, seed, obj.max_depth)
+    return dict(draws=draws, exit_uniforms=[u.to(DEV) for u in uniforms])
+
+
+def test_fused_optimizer_reads_float32_gradients():
+    """Over exactly a model's parameters FusedAdamW binds to the model: the
+    backward leaves .grad unset and keeps float32 gradients whose bf16
+    rounding equals the .grad an unbound model gets for the same step
+    (materialize_grads fills .grad with them); two backward calls without
+    zero_grad accumulate (to float32 rounding of the two separate
+    gradients); the first AdamW step equals its closed form on those float32
+    gradients."""
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    plain, obj, ids, bounds = _tiny_bf16(seed=6)
+    fused, _, _, _ = _tiny_bf16(seed=6)
+    opt = FusedAdamW(param_groups(fused, 0.01), lr=1e-3, max_grad_norm=1.0)
+    kw = _step_inputs(obj, ids, bounds, 6)
+    loss_a, _ = plain(ids.to(DEV), ids.to(DEV), bounds, **kw)
+    loss_a.backward()
+    loss_b, _ = fused(ids.to(DEV), ids.to(DEV), bounds, **kw)
+    loss_b.backward()
+    assert loss_a.item() == loss_b.item()
+    assert all(p.grad is None for p in fused.parameters())
+    f32 = {k: v.clone() for k, v in fused.float32_grads().items()}
+    for name, p in plain.named_parameters():
+        if name == "backbone.model.embed_tokens.weight":  # float atomics: summation order varies
+            torch.testing.assert_close(f32[name].to(torch.bfloat16), p.grad, rtol=1e-2, atol=1e-6)
+        else:
+            assert torch.equal(f32[name].to(torch.bfloat16), p.grad), name
+    fused.materialize_grads()
+    for name, p in fused.named_parameters():
+        assert torch.equal(p.grad, f32[name].to(torch.bfloat16)), name
+    # the first AdamW step on the float32 gradients
+    masters0 = {n: p.detach().float().clone() for n, p in fused.named_parameters()}
+    opt.step()
+    torch.cuda.synchronize()
+    norm = float(torch.sqrt(sum((g.double() ** 2).sum() for g in f32.values())))
+    assert float(opt.last_grad_norm) == pytest.approx(norm, rel=1e-5)
+    clip = min(1.0, 1.0 / (norm + 1e-6))
+    groups = {id(p): grp["weight_decay"] for grp in opt.param_groups for p in grp["params"]}
+    for name, p in fused.named_parameters():
+        gi = f32[name].double() * clip
+        wd = groups[id(p)]
+        want = masters0[name].double() * (1 - 1e-3 * wd) - 1e-3 * gi / (gi.abs() + 1e-8)
+        torch.testing.assert_close(opt.state[p]["master"].double(), want, atol=2e-6, rtol=1e-5,
+                                   msg=name)
+    # accumulation: two halves of two steps without zero_grad
+    opt.zero_grad(set_to_none=True)
+    assert fused.float32_grads() is None
+    kw2 = _step_inputs(obj, ids, bounds, 7)
+    parts = []
+    for k in (kw, kw2):
+        loss, _ = fused(ids.to(DEV), ids.to(DEV), bounds, **k)
+        (loss / 2).backward()
+        parts.append({n: g.clone() for n, g in fused.float32_grads().items()})
+        opt.zero_grad(set_to_none=True)
+    for k in (kw, kw2):
+        loss, _ = fused(ids.to(DEV), ids.to(DEV), bounds, **k)
+        (loss / 2).backward()
+    acc = fused.float32_grads()
+    for name, g in acc.items():
+        want = parts[0][name] + parts[1][name]
+        torch.testing.assert_close(g, want, rtol=1e-5, atol=1e-5 * want.abs().max().item(),
+                                   msg=name)
+
+
+def test_moving_bound_parameters_is_refused():
+    """After a FusedAdamW bound the model's parameters, re-homing a parameter
+    (which would leave the optimizer's tables pointing at freed memory) makes
+    the next step raise instead of silently building a new arena."""
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    model, obj, ids, bounds = _tiny_bf16(seed=8)
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-3)
+    kw = _step_inputs(obj, ids, bounds, 8)
+    loss, _ = model(ids.to(DEV), ids.to(DEV), bounds, **kw)
+    loss.backward()
+    opt.step()
+    w = model.exit_gate.net.weight
+    w.data = w.data.clone()
+    with pytest.raises(RuntimeError, match="moved"):
+        model(ids.to(DEV), ids.to(DEV), bounds, **kw)
+
+
+def test_unbound_optimizer_rebuilds_tables_when_parameters_move():
+    """An optimizer over standalone tensors follows a parameter given new
+    storage: the update lands in the parameter's current storage."""
+    from alodlm_amd.optim import FusedAdamW
+    p = torch.nn.Parameter(torch.ones(1000, device=DEV, dtype=torch.bfloat16))
+    opt = FusedAdamW([{"params": [p], "weight_decay": 0.0}], lr=0.1)
+    p.grad = torch.ones_like(p)
+    opt.step()
+    first = p.detach().clone()
+    p.data = p.data.clone()
+    p.grad = torch.ones_like(p)
+    opt.step()
+    torch.cuda.synchronize()
+    assert not torch.equal(p.detach(), first)

@@ -230,7 +230,12 @@ def test_tiny_step_without_masked_rows_or_targets():
     ids, _, bounds = _tiny_inputs(seed=2)
     labels = torch.full_like(ids, -100)
     engine = model.engine()
+    # a step with loss-bearing rows first, so the gradient arena holds values
+    # the M = 0 step must overwrite (its matrices are written, not zeroed)
     gen = torch.Generator(device="cuda").manual_seed(2)
+    out, state = engine.forward(ids.cuda(), ids.cuda(), bounds, True, generator=gen)
+    engine.backward(state, 1.0)
+    assert float(engine.grads.abs().sum()) > 0
     out, state = engine.forward(ids.cuda(), labels.cuda(), bounds, True, generator=gen)
     grads = engine.backward(state, 1.0)
     torch.cuda.synchronize()

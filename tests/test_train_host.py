@@ -187,3 +187,72 @@ def test_config_errors(tmp_path):
         path.write_text(yaml.safe_dump(dict(base, **change)))
         with pytest.raises(ValueError):
             TrainConfig.load(path)
+
+
+class _FakeProps:
+    total_memory = 100 * 2**30
+
+
+def _engine_for_keep(monkeypatch, alloc, peak, fused_state):
+    """A StepEngine shell for the keep decision with mocked memory figures
+    (GiB): `alloc` is what memory_allocated reports at each call, `peak` the
+    first step's peak."""
+    import types
+    from alodlm_amd import engine as E
+    e = E.StepEngine.__new__(E.StepEngine)
+    e.dims = E.Dims(hidden=1024, heads=8, kv_heads=4, head_dim=128, intermediate=4096, vocab=1000,
+                    layers=4, eps=1e-6, theta=1e6)
+    e.cfg = types.SimpleNamespace(loop_start=0, max_depth=4)
+    e.dtype, e.device = __import__("torch").bfloat16, "cuda:0"
+    e.arena = types.SimpleNamespace(params=[types.SimpleNamespace(numel=lambda: 2**30)])
+    e.grads = None
+    e.fused_optimizer = (None if fused_state is None else
+                         types.SimpleNamespace(state_bytes_to_come=lambda: fused_state * 2**30))
+    e._keep, e._keep_rows, e._step_alloc, e._step_peak = None, 0, None, None
+    values = iter(alloc)
+    monkeypatch.setattr("torch.cuda.memory_allocated", lambda dev=None: next(values) * 2**30)
+    monkeypatch.setattr("torch.cuda.max_memory_allocated", lambda dev=None: peak * 2**30)
+    monkeypatch.setattr("torch.cuda.reset_peak_memory_stats", lambda dev=None: None)
+    monkeypatch.setattr("torch.cuda.get_device_properties", lambda dev=None: _FakeProps())
+    return e
+
+
+def test_keep_decision_counts_optimizer_state_not_yet_allocated(monkeypatch):
+    """The keep decision at the second forward of an accumulated step (before
+    any optimizer step) adds the bound FusedAdamW's state still to come; a
+    decision after the first optimizer step has none to add.  With N = 262144
+    rows and 16 layer applications the rotary q/k take 12 GiB and the norm
+    outputs 16 GiB; the budget is 95 GiB."""
+    N = 262144
+    # first forward: 20 GiB allocated; the step peaks at 50 GiB (growth 30)
+    e = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=30)
+    assert e._decide_keep(N) == (False, False)
+    e._step_peak = 50 * 2**30
+    # 30 GiB of optimizer state to come: 20 + 30 + 30 = 80, so q/k (92) fit
+    # and the norm outputs (108) do not; without counting it both would
+    assert e._decide_keep(N) == (True, False)
+    # the same decision once the state exists: 50 GiB allocated, nothing to come
+    e2 = _engine_for_keep(monkeypatch, [20, 50], 50, fused_state=0)
+    e2._decide_keep(N)
+    e2._step_peak = 50 * 2**30
+    assert e2._decide_keep(N) == (True, False)
+    # a smaller pack keeps both: 80 + 6 + 8 <= 95
+    e3 = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=30)
+    e3._decide_keep(N // 2)
+    e3._step_peak = 50 * 2**30
+    assert e3._decide_keep(N // 2) == (True, True)
+
+
+def test_keep_decision_without_fused_optimizer_reserves_adam_state(monkeypatch):
+    """With no FusedAdamW bound the decision reserves AdamW's float32 master and
+    moments (12 bytes per parameter: 12 GiB for 2^30 parameters): 20 + 30 + 12
+    = 62 GiB, so q/k (74) and the norm outputs (90) fit at N = 262144; at three
+    times the rows q/k alone (98) do not."""
+    e = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=None)
+    e._decide_keep(262144)
+    e._step_peak = 50 * 2**30
+    assert e._decide_keep(262144) == (True, True)
+    e = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=None)
+    e._decide_keep(3 * 262144)
+    e._step_peak = 50 * 2**30
+    assert e._decide_keep(3 * 262144) == (False, False)
