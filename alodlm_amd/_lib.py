@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -30,9 +30,13 @@ SIGNATURES = {
     "alodlm_mask_draws": [U64, U64, P, I64, P, I64, I64, P, P, P, P, P, P, P, P],
     "alodlm_batch_build": [P, P, P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P, P, P],
     "alodlm_embed_gather": [P, P, P, I64, I64, I64, I32, P],
-    "alodlm_embed_scatter_add": [P, P, P, I64, P, I64, I64, I64, I32, P],
+    "alodlm_embed_plan": [P, I64, I64, P, P],
+    "alodlm_embed_scatter_add": [P, P, P, I64, P, P, I64, I64, I64, I32, P],
     "alodlm_rmsnorm_fwd": [P, P, P, P, I64, I64, F32, I32, P],
     "alodlm_rmsnorm_bwd_workspace": [I64, I64],
+    "alodlm_embed_plan_size": [I64],
+    "alodlm_embed_scatter_workspace": [I64, I64],
+    "alodlm_carry_select_bwd_workspace": [I64, I64],
     "alodlm_rmsnorm_bwd": [P, P, P, P, P, P, P, P, I64, I64, I32, P],
     "alodlm_rmsnorm_bwd_noalloc": [P, P, P, P, P, P, P, I64, I64, I32, P],
     "alodlm_qknorm_rope_fwd": [P, P, P, P, P, P, P, I64, I64, I64, I64, F32, I32, P],
@@ -80,6 +84,9 @@ SIGNATURES = {
 _RESTYPE = {
     "alodlm_last_error": ctypes.c_char_p,
     "alodlm_rmsnorm_bwd_workspace": I64,
+    "alodlm_embed_plan_size": I64,
+    "alodlm_embed_scatter_workspace": I64,
+    "alodlm_carry_select_bwd_workspace": I64,
     "alodlm_qknorm_rope_bwd_workspace": I64,
     "alodlm_gemm_workspace": I64,
     "alodlm_attention_bwd_workspace": I64,

@@ -1,4 +1,4 @@
-// Embedding gather / scatter-add, SwiGLU, and small elementwise helpers.
+// Embedding gather, SwiGLU, and small elementwise helpers.
 #include "common.h"
 
 // out[r] = table[ids[r]]   ([tf] modeling_qwen3.py:352; alodlm/model.py:133,149)
@@ -12,23 +12,6 @@ __global__ void embed_gather_kernel(const T* __restrict__ table, const int64_t* 
   const int64_t id = ids[r];
   if (id < 0 || id >= vocab) Elem<T>::store(out, i, NAN);
   else out[i] = table[id * H + c];
-}
-
-// dtable[ids[r]] += dout[r] (float accumulate) for rows with
-// row_exits == NULL or row_exits[r] <= max_exit.  One wavefront per row.
-template <typename T>
-__global__ void embed_scatter_kernel(const T* __restrict__ dout, const int64_t* __restrict__ ids,
-                                     const int32_t* __restrict__ row_exits, int64_t max_exit,
-                                     float* __restrict__ dtable, int64_t rows, int64_t H,
-                                     int64_t vocab) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (r >= rows) return;
-  if (row_exits && row_exits[r] > max_exit) return;
-  if (ids[r] < 0 || ids[r] >= vocab) return;
-  float* dst = dtable + ids[r] * H;
-  const T* src = dout + r * H;
-  for (int64_t c = lane; c < H; c += 64) atomicAdd(dst + c, Elem<T>::load(src, c));
 }
 
 // act = cast(cast(silu(gate)) * up)   ([tf] modeling_qwen3.py:81-83).
@@ -196,19 +179,6 @@ extern "C" int alodlm_embed_gather(const void* table, const int64_t* ids, void* 
         (const T*)table, ids, (T*)out, rows, hidden, vocab);
   });
   ALODLM_CHECK_LAUNCH("embed_gather");
-  return ALODLM_OK;
-}
-
-extern "C" int alodlm_embed_scatter_add(const void* dout, const int64_t* ids,
-                                        const int32_t* row_exits, int64_t max_exit, float* dtable,
-                                        int64_t rows, int64_t hidden, int64_t vocab, int dtype,
-                                        void* stream) {
-  if (rows == 0) return ALODLM_OK;
-  ALODLM_DISPATCH(dtype, T, {
-    embed_scatter_kernel<T><<<ceil_div_u(rows, 4), 256, 0, as_stream(stream)>>>(
-        (const T*)dout, ids, row_exits, max_exit, dtable, rows, hidden, vocab);
-  });
-  ALODLM_CHECK_LAUNCH("embed_scatter_add");
   return ALODLM_OK;
 }
 

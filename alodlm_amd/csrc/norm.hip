@@ -7,6 +7,7 @@
 // true for Qwen3 shapes), otherwise scalar.
 #include "common.h"
 #include "norm.h"
+#include "embed.h"
 
 #define NORM_WAVES 4
 
@@ -467,17 +468,29 @@ extern "C" int alodlm_rmsnorm_bwd(const void* dy, const void* x, const float* rs
                             nullptr, 0, as_stream(stream));
 }
 
+// The rmsnorm part of the workspace, rounded to 64 floats so the scatter's
+// part keeps 256-byte alignment.
+static int64_t carry_norm_workspace(int64_t rows, int64_t hidden) {
+  return (alodlm_rmsnorm_bwd_workspace(rows, hidden) + 63) / 64 * 64;
+}
+
+extern "C" int64_t alodlm_carry_select_bwd_workspace(int64_t rows, int64_t hidden) {
+  return carry_norm_workspace(rows, hidden) + alodlm_embed_scatter_workspace(rows, hidden);
+}
+
 extern "C" int alodlm_carry_select_bwd(const void* dy, const void* x, const float* rstd,
                                        const void* wf, const int32_t* exits, int64_t depth,
-                                       const int64_t* original, const void* dres, void* dx,
+                                       const int32_t* plan, const void* dres, void* dx,
                                        float* dwf_accum, float* dtable, float* workspace,
                                        int64_t rows, int64_t hidden, int64_t vocab, int dtype,
                                        void* stream) {
+  const hipStream_t st = as_stream(stream);
   // re-embedded rows (exits <= depth) send their gradient to the embedding table
-  int rc = alodlm_embed_scatter_add(dy, original, exits, depth, dtable, rows, hidden, vocab, dtype,
-                                    stream);
+  int rc = embed_scatter_launch(dy, plan, exits, depth, dtable,
+                                workspace + carry_norm_workspace(rows, hidden), rows, hidden,
+                                vocab, dtype, st);
   if (rc) return rc;
   // carried rows go back through the carry norm into the previous depth's core output
   return rmsnorm_bwd_launch(dy, x, rstd, wf, dres, dx, dwf_accum, workspace, rows, hidden, dtype,
-                            exits, depth, as_stream(stream));
+                            exits, depth, st);
 }

@@ -306,15 +306,16 @@ class StepEngine(Kernels):
              self.code, self._stream())
         return xin, rstd
 
-    def _carry_bwd(self, dnext, core_out, rstd, b, exits, depth, dres, g_norm, g_embed):
+    def _carry_bwd(self, dnext, core_out, rstd, plan, exits, depth, dres, g_norm, g_embed):
         """Backward of ``_carry`` at ``depth``: carried rows go back through the
         carry norm into the previous core output (plus ``dres``), re-embedded
-        rows into the embedding table."""
+        rows into the embedding table (``plan``: the embed plan of the
+        original tokens)."""
         N, H = core_out.shape
         dcore = self._empty(N, H)
-        ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        ws = self._workspace(query("alodlm_carry_select_bwd_workspace", N, H))
         call("alodlm_carry_select_bwd", ptr(dnext), ptr(core_out), ptr(rstd),
-             ptr(self.final_norm), ptr(exits), depth, ptr(b.original), ptr(dres), ptr(dcore),
+             ptr(self.final_norm), ptr(exits), depth, ptr(plan), ptr(dres), ptr(dcore),
              ptr(g_norm), ptr(g_embed), ptr(ws), N, H, self.dims.vocab, self.code, self._stream())
         return dcore
 
@@ -507,6 +508,7 @@ class StepEngine(Kernels):
         self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
         g_embed, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
+        plan_original = self.embed_plan(b.original) if K > 1 else None
         dnext = None  # gradient at the core input of depth+1
         lm_written = accumulate
         for depth in reversed(range(K)):
@@ -518,16 +520,15 @@ class StepEngine(Kernels):
                 dr = self._layer_bwd(dr, saved, b, grads)
             if dnext is not None:
                 # x_in(depth+1) = exits <= depth+1 ? E[original] : norm(core_out(depth))
-                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], b, exits,
-                                     depth + 1, dr, g_norm, g_embed)
+                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], plan_original,
+                                     exits, depth + 1, dr, g_norm, g_embed)
             for saved in reversed(rec["core_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             dnext = dr
         dx = dnext
         for saved in reversed(state["prelude"]):
             dx = self._layer_bwd(dx, saved, b, grads)
-        call("alodlm_embed_scatter_add", ptr(dx), ptr(b.ids), None, 0, ptr(g_embed), N, H, V, c,
-             st)
+        self.embed_scatter(dx, self.embed_plan(b.ids), g_embed)
         if not lm_written:
             # no pass had a loss-bearing row: the LM head's gradient is zero
             lo, hi = self.arena.lm_span
@@ -593,6 +594,7 @@ class StepEngine(Kernels):
         self._written = None
         g_embed, g_norm, _, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
+        plan_original = self.embed_plan(b.original) if K > 1 else None
         dnext = None
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
@@ -604,8 +606,8 @@ class StepEngine(Kernels):
                 call("alodlm_gate_bwd", ptr(g), ptr(rec["readout"]), 1.0, ptr(g_gw), ptr(g_gb),
                      ptr(g_db), depth, N, H, ptr(ws), self.code, self._stream())
             if dnext is not None:
-                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], b, exits,
-                                     depth + 1, dr, g_norm, g_embed)
+                dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], plan_original,
+                                     exits, depth + 1, dr, g_norm, g_embed)
             for saved in reversed(rec["core_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             dnext = dr

@@ -289,6 +289,23 @@ class Kernels:
             self._ws = torch.empty(max(n, 1), dtype=torch.float32, device=self.device)
         return self._ws
 
+    def embed_plan(self, ids):
+        """The sorted-row plan of the int64 token ids ``ids`` that the
+        deterministic embedding scatters take (one per id array and step)."""
+        n = ids.numel()
+        plan = self._empty(query("alodlm_embed_plan_size", n), dtype=torch.int32)
+        call("alodlm_embed_plan", ptr(ids), n, self.dims.vocab, ptr(plan), self._stream())
+        return plan
+
+    def embed_scatter(self, dout, plan, dtable, row_exits=None, max_exit=0):
+        """dtable[ids[r]] += dout[r] (float32 table) over the rows of ``plan``
+        (those with row_exits[r] <= max_exit when ``row_exits`` is given), in
+        a fixed order."""
+        N, H = dout.shape
+        ws = self._workspace(query("alodlm_embed_scatter_workspace", N, H))
+        call("alodlm_embed_scatter_add", ptr(dout), ptr(plan), ptr(row_exits), max_exit,
+             ptr(dtable), ptr(ws), N, H, dtable.shape[0], self.code, self._stream())
+
     def _gemm(self, A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=EPI_STORE, R=None,
               ldr=0):
         ws = None

@@ -39,8 +39,7 @@ class _Embedding(torch.autograd.Function):
     def backward(ctx, dout):
         k, (V, H) = ctx.kernels, ctx.shape
         dtable = _f32_zeros(V, H, device=k.device)
-        call("alodlm_embed_scatter_add", ptr(dout.contiguous()), ptr(ctx.ids), None, 0,
-             ptr(dtable), ctx.ids.numel(), H, V, k.code, k._stream())
+        k.embed_scatter(dout.contiguous(), k.embed_plan(ctx.ids), dtable)
         return None, None, dtable.to(k.dtype)
 
 
@@ -71,10 +70,10 @@ class _CarrySelect(torch.autograd.Function):
         dx = k._empty(N, H)
         dwf = _f32_zeros(H, device=k.device)
         dtable = _f32_zeros(V, H, device=k.device)
-        ws = k._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
+        ws = k._workspace(query("alodlm_carry_select_bwd_workspace", N, H))
         call("alodlm_carry_select_bwd", ptr(dy.contiguous()), ptr(core_out), ptr(rstd), ptr(wf),
-             ptr(ctx.exits), ctx.depth, ptr(ctx.original), None, ptr(dx), ptr(dwf), ptr(dtable),
-             ptr(ws), N, H, V, k.code, k._stream())
+             ptr(ctx.exits), ctx.depth, ptr(k.embed_plan(ctx.original)), None, ptr(dx), ptr(dwf),
+             ptr(dtable), ptr(ws), N, H, V, k.code, k._stream())
         return None, None, None, None, dx, dwf.to(k.dtype), dtable.to(k.dtype)
 
 

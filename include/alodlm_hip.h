@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 2
+#define ALODLM_ABI_VERSION 3
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -84,16 +84,28 @@ int alodlm_batch_build(const int64_t* ids, const int64_t* labels, const int64_t*
 
 /* ---------------------------------------------------------------------------
  * Embedding ([tf] modeling_qwen3.py:352; alodlm/model.py:133,149).
- * gather: out[r] = table[ids[r]].  scatter_add (backward): dtable[ids[r]] +=
- * dout[r] (float32 accumulate) for rows with row_exits == NULL or
- * row_exits[r] <= max_exit.  Ids outside [0, vocab) give NaN rows (gather)
- * or are skipped (scatter); they are never dereferenced.
+ * gather: out[r] = table[ids[r]].  Ids outside [0, vocab) give NaN rows
+ * (gather) or no gradient (scatter); they are never dereferenced.
+ *
+ * The backward is deterministic: embed_plan sorts the rows by id (stable,
+ * one workgroup) into runs of equal ids cut into chunks of at most 32 rows;
+ * plan holds alodlm_embed_plan_size(rows) int32 and serves every later
+ * scatter over the same ids (rows < 2^24).  scatter_add: dtable[ids[r]] +=
+ * dout[r] (float32) for rows with row_exits == NULL or row_exits[r] <=
+ * max_exit, each chunk summed in row order and the chunks of a run in chunk
+ * order, so the result does not depend on scheduling (the reference's
+ * nn.Embedding backward accumulates with atomics).  workspace holds
+ * alodlm_embed_scatter_workspace(rows, hidden) floats.
  * ------------------------------------------------------------------------ */
 int alodlm_embed_gather(const void* table, const int64_t* ids, void* out, int64_t rows,
                         int64_t hidden, int64_t vocab, int dtype, void* stream);
-int alodlm_embed_scatter_add(const void* dout, const int64_t* ids, const int32_t* row_exits,
-                             int64_t max_exit, float* dtable, int64_t rows, int64_t hidden,
-                             int64_t vocab, int dtype, void* stream);
+int64_t alodlm_embed_plan_size(int64_t rows);
+int alodlm_embed_plan(const int64_t* ids, int64_t rows, int64_t vocab, int32_t* plan,
+                      void* stream);
+int64_t alodlm_embed_scatter_workspace(int64_t rows, int64_t hidden);
+int alodlm_embed_scatter_add(const void* dout, const int32_t* plan, const int32_t* row_exits,
+                             int64_t max_exit, float* dtable, float* workspace, int64_t rows,
+                             int64_t hidden, int64_t vocab, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * RMSNorm ([tf] modeling_qwen3.py:59-64): y = w * cast(x * rsqrt(mean(x^2) + eps)).
@@ -256,11 +268,13 @@ int alodlm_carry_select(const void* x, const void* wf, const void* table,
                         void* out, float* rstd, int64_t rows, int64_t hidden, int64_t vocab,
                         float eps, int dtype, void* stream);
 /* Backward of carry_select at depth d: rows with exits <= d add dy into
- * dtable[original] (float); the others go through the carry norm:
- * dx = dres + norm'(x) . dy, dwf_accum += ... (workspace as rmsnorm_bwd);
- * re-embedded rows get dx = dres. */
+ * dtable[original] (float; plan = alodlm_embed_plan of original); the others
+ * go through the carry norm: dx = dres + norm'(x) . dy, dwf_accum += ...;
+ * re-embedded rows get dx = dres.  workspace holds
+ * alodlm_carry_select_bwd_workspace(rows, hidden) floats. */
+int64_t alodlm_carry_select_bwd_workspace(int64_t rows, int64_t hidden);
 int alodlm_carry_select_bwd(const void* dy, const void* x, const float* rstd, const void* wf,
-                            const int32_t* exits, int64_t depth, const int64_t* original,
+                            const int32_t* exits, int64_t depth, const int32_t* plan,
                             const void* dres, void* dx, float* dwf_accum, float* dtable,
                             float* workspace, int64_t rows, int64_t hidden, int64_t vocab,
                             int dtype, void* stream);

@@ -90,3 +90,21 @@ def test_no_alloc_rmsnorm_bwd_rejects_oversize_on_the_host():
     with pytest.raises(ValueError, match="scratch"):
         _lib.call("alodlm_rmsnorm_bwd_noalloc", None, None, None, None, None, None, None,
                   65536, 2048, _lib.BF16_CODE, None)
+
+
+def test_embed_plan_limits_on_the_host():
+    """The embedding plan and scatter reject row counts of 2^24 and more (one
+    256-thread workgroup per chunk) before any launch; the plan and workspace
+    sizes are linear in the rows."""
+    from alodlm_amd import _lib
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    assert _lib.query("alodlm_embed_plan_size", 1000) == 8 + 13 * 1000
+    assert _lib.query("alodlm_embed_scatter_workspace", 3200, 64) == (200 + 1) * 64
+    with pytest.raises(ValueError, match="rows"):
+        _lib.call("alodlm_embed_plan", None, 1 << 24, 151936, None, None)
+    with pytest.raises(ValueError, match="shape"):
+        _lib.call("alodlm_embed_scatter_add", None, None, None, 0, None, None, 1 << 24, 64,
+                  151936, _lib.BF16_CODE, None)
+    # zero rows is a no-op that touches nothing
+    _lib.call("alodlm_embed_plan", None, 0, 151936, None, None)

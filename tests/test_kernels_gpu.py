@@ -575,3 +575,110 @@ def test_gate_bwd(dtype, rows, hidden):
     torch.testing.assert_close(gw.cpu().double(), want_w, atol=1e-4, rtol=1e-5)
     assert abs(float(gb) - (0.25 + want_b)) < 1e-4
     assert abs(float(gdb[2]) - want_b) < 1e-4 and float(gdb[0]) == 0.0
+
+
+def _embed_ids(rows, vocab, seed):
+    """Token ids with runs of every length class the plan distinguishes: one
+    row, exactly one chunk (32), just over (33), two full chunks (64), a long
+    run (the mask token's), and ids outside [0, vocab)."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, vocab, (rows,), generator=g)
+    perm = torch.randperm(rows, generator=g)
+    start = 0
+    for token, count in ((7, 32), (8, 33), (9, 64), (vocab - 1, rows // 10), (-1, 5), (vocab, 5)):
+        ids[perm[start:start + count]] = token
+        start += count
+    return ids
+
+
+def _embed_fixed_order(dout, ids, keep, table, vocab, chunk=32):
+    """float32 sums in the kernels' fixed order: rows of one id in ascending
+    row order, summed in chunks of 32 rows; a one-chunk run is added to the
+    table row, a longer run's chunk sums are added up in chunk order first."""
+    out = table.copy()
+    for token in np.unique(ids):
+        if token < 0 or token >= vocab:
+            continue
+        rows = np.nonzero(ids == token)[0]
+        partial = []
+        for lo in range(0, len(rows), chunk):
+            acc = np.zeros(dout.shape[1], np.float32)
+            used = False
+            for r in rows[lo:lo + chunk]:
+                if keep[r]:
+                    acc = acc + dout[r]
+                    used = True
+            partial.append((acc, used))
+        if len(partial) == 1:
+            if partial[0][1]:
+                out[token] = out[token] + partial[0][0]
+        else:
+            acc = np.zeros(dout.shape[1], np.float32)
+            for p, _ in partial:
+                acc = acc + p
+            out[token] = out[token] + acc
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,hidden,filtered", [(5000, 512, False), (3001, 264, True),
+                                                  (40, 8, False)])
+def test_embed_scatter_is_deterministic_and_exact(dtype, rows, hidden, filtered):
+    """Embedding backward (alodlm/model.py:133,149-151 through nn.Embedding):
+    dtable[id] += sum of dout over the rows with that id, ids outside [0, V)
+    contributing nothing, rows with row_exits > max_exit skipped.  The plan
+    is a stable sort of the rows by id; the sums are bit-identical to float32
+    additions in the plan's fixed order and within float32 rounding of the
+    float64 sums."""
+    L = lib()
+    vocab = 1000
+    log(f"embed scatter rows={rows} hidden={hidden} {dtype} filtered={filtered}")
+    ids = _embed_ids(rows, vocab, rows + hidden)
+    g = torch.Generator().manual_seed(rows)
+    dout = torch.randn(rows, hidden, generator=g).to(dtype)
+    table = torch.randn(vocab, hidden, generator=g)
+    exits = torch.randint(0, 4, (rows,), generator=g, dtype=torch.int32)
+    max_exit = 1
+    keep = (exits <= max_exit).numpy() if filtered else np.ones(rows, bool)
+    ids_d = ids.to(DEV)
+    plan = torch.empty(L.query("alodlm_embed_plan_size", rows), dtype=torch.int32, device=DEV)
+    L.call("alodlm_embed_plan", L.ptr(ids_d), rows, vocab, L.ptr(plan), st())
+    ws = torch.empty(L.query("alodlm_embed_scatter_workspace", rows, hidden), dtype=torch.float32,
+                     device=DEV)
+    exits_d = exits.to(DEV) if filtered else None
+    results = []
+    for _ in range(2):
+        dt = table.to(DEV)
+        L.call("alodlm_embed_scatter_add", L.ptr(dout.to(DEV)), L.ptr(plan), L.ptr(exits_d),
+               max_exit, L.ptr(dt), L.ptr(ws), rows, hidden, vocab, L.dtype_code(dtype), st())
+        results.append(dt.cpu())
+    torch.cuda.synchronize()
+    assert torch.equal(results[0], results[1])
+    # the plan: keys sorted (out-of-range ids as V), rows stable within a key
+    p = plan.cpu().numpy()
+    key, row = p[8:8 + rows], p[8 + rows:8 + 2 * rows]
+    want_key = np.where((ids.numpy() >= 0) & (ids.numpy() < vocab), ids.numpy(), vocab)
+    order = np.argsort(want_key, kind="stable")
+    np.testing.assert_array_equal(row, order)
+    np.testing.assert_array_equal(key, want_key[order])
+    runs = np.unique(want_key, return_counts=True)[1]
+    chunks = (runs + 31) // 32
+    assert p[0] == len(runs) and p[1] == chunks.sum()
+    assert p[2] == chunks[runs > 32].sum() and p[3] == (runs > 32).sum()
+    dout32 = dout.float().numpy()
+    want = _embed_fixed_order(dout32, ids.numpy(), keep, table.numpy(), vocab)
+    np.testing.assert_array_equal(results[0].numpy(), want)
+    exact = table.double().numpy().copy()
+    valid = (ids.numpy() >= 0) & (ids.numpy() < vocab) & keep
+    np.add.at(exact, ids.numpy()[valid], dout32.astype(np.float64)[valid])
+    np.testing.assert_allclose(results[0].numpy(), exact, rtol=0, atol=2e-4 * np.sqrt(rows / 10))
+
+
+def test_embed_scatter_without_rows_is_a_no_op():
+    L = lib()
+    table = torch.ones(10, 8, device=DEV)
+    L.call("alodlm_embed_plan", None, 0, 10, None, st())
+    L.call("alodlm_embed_scatter_add", None, None, None, 0, L.ptr(table), None, 0, 8, 10,
+           L.F32_CODE, st())
+    torch.cuda.synchronize()
+    assert torch.equal(table.cpu(), torch.ones(10, 8))

@@ -176,14 +176,15 @@ def test_core_block_full_size_properties():
                  "backbone.model.layers.0.mlp.down_proj.weight", "backbone.model.norm.weight",
                  "backbone.model.embed_tokens.weight", "exit_gate.net.weight"):
         assert engine.arena.view(grads, name).norm().item() > 0, name
-    # the autograd wrapper gives the same gradients (deterministic kernels;
-    # the table's re-embedded rows are summed by atomics, so close, not equal)
+    # the autograd wrapper gives the same input gradient bit for bit (every
+    # kernel sums in a fixed order; the gate-logit cotangents, rounded to the
+    # parameter dtype on this path, reach only the gate parameters)
     x = x0.to(DEV).requires_grad_(True)
     outs2, gates2, _ = recurrent_core(model, x, batch, exit_uniforms=uniforms)
     loss = sum((o.float() * c.to(DEV).float()).sum() for o, c in zip(outs2, cot))
     loss = loss + (gates2.float() * gcot.to(DEV)).sum()
     gx = torch.autograd.grad(loss, x)[0]
-    assert cosine(gx.float(), dx0.float()) >= 0.9999
+    assert torch.equal(gx, dx0)
     log(f"core block full size: masked rows {int(batch.masked.sum())}")
 
 
