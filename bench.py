@@ -162,9 +162,12 @@ def device_info():
 
 def gemm_bytes(A, lda, a_k, B, ldb, b_k, C, ldc, M, N, K, alpha=1.0, epi=0, R=None, ldr=0):
     """Algorithmic HBM bytes of one GEMM launch: A and B read once (bf16), C
-    written once (bf16 store), plus R read (residual) or the float32 C read and
-    written back (accumulate)."""
-    c_bytes = {0: 2 * M * N, 1: 4 * M * N, 2: 8 * M * N}[epi]
+    written once (bf16 store, or float32 for the first contribution to a
+    gradient), plus R read (residual) or the float32 C read and written back
+    (accumulate)."""
+    from alodlm_amd._lib import EPI_ACCUM, EPI_RESIDUAL, EPI_STORE, EPI_STORE_F32
+    c_bytes = {EPI_STORE: 2 * M * N, EPI_RESIDUAL: 4 * M * N, EPI_ACCUM: 8 * M * N,
+               EPI_STORE_F32: 4 * M * N}[epi]
     return 2 * (M * K + N * K) + c_bytes
 
 

@@ -31,3 +31,20 @@ def test_cpu_only_machine_is_refused():
 def test_model_choices():
     out = run("--model", "70b")
     assert out.returncode == 2 and "invalid choice" in out.stderr
+
+
+def test_gemm_bytes_covers_every_epilogue():
+    """Every epilogue code the library exports has an algorithmic byte count:
+    A and B read once in bf16, C written in its store type, plus the residual
+    read or the float32 read-modify-write of an accumulated gradient."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from alodlm_amd import _lib
+    M, N, K = 256, 512, 1024
+    ab = 2 * (M * K + N * K)
+    want = {_lib.EPI_STORE: ab + 2 * M * N, _lib.EPI_RESIDUAL: ab + 4 * M * N,
+            _lib.EPI_ACCUM: ab + 8 * M * N, _lib.EPI_STORE_F32: ab + 4 * M * N}
+    codes = {v for k, v in vars(_lib).items() if k.startswith("EPI_")}
+    assert codes == set(want)
+    for epi, nbytes in want.items():
+        assert bench.gemm_bytes(None, 0, 0, None, 0, 0, None, 0, M, N, K, epi=epi) == nbytes
