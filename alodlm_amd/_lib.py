@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -66,6 +66,9 @@ SIGNATURES = {
     "alodlm_cross_entropy": [P, P, P, P, I64, I64, P, P, I32, P],
     "alodlm_scatter_ce": [P, P, P, I64, P, I64, P],
     "alodlm_decode_readout": [P, I64, I64, P, P, I32, P],
+    "alodlm_decode_plan": [P, P],
+    "alodlm_decode_begin": [P, P, I64, I64, P],
+    "alodlm_decode_commit": [P, P, I64, I64, I32, P],
     "alodlm_objective_workspace": [I64, I64, I64],
     "alodlm_objective": [P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P],
     "alodlm_outcome_loss": [P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P, P],

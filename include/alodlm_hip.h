@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 3
+#define ALODLM_ABI_VERSION 4
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -323,6 +323,79 @@ int alodlm_cross_entropy(void* logits, const int32_t* target, const float* coef,
  * among equal maxima) and entropy[rows] (float). */
 int alodlm_decode_readout(const void* logits, int64_t rows, int64_t vocab, int64_t* argmax,
                           float* entropy, int dtype, void* stream);
+/* ---------------------------------------------------------------------------
+ * Adaptive decoding's window bookkeeping (alodlm/inference.py:71-246) on the
+ * device.  The state is a set of caller-allocated device arrays:
+ *   ledger   the pending tail of the text in logical order (capacity slots):
+ *            slot_token, slot_open (1 = still a mask token), slot_depth and
+ *            slot_halt (exit depth and first-pass halt probability of a
+ *            committed slot);
+ *   output   out_token / out_depth / out_halt (max_new_tokens entries);
+ *   window   row_token / row_position (window rows: committed slots, then
+ *            open slots, each in logical order; position = cache rows +
+ *            slot), and per mask row j: mask_row (window row), mask_slot,
+ *            mask_offset (position penalty: (slot_j - slot_0) * penalty),
+ *            mask_token / mask_exit / mask_committed / mask_fresh (committed
+ *            at the current depth), mask_survival, mask_first_hazard;
+ *   readout  predicted / entropy of the mask rows at the current depth
+ *            (alodlm_decode_readout writes them);
+ *   carry    replace_token / replace_depth of the window rows: the next
+ *            depth's alodlm_carry_select table (rows committed at depth d
+ *            restart from their token's embedding at depth d + 1);
+ *   header   ALODLM_DECODE_HEADER int64 fields, indices below.
+ * One workgroup per call; the caller reads the header after a commit.
+ * ------------------------------------------------------------------------ */
+#define ALODLM_DECODE_HEADER 16
+enum {
+  ALODLM_DECODE_LEDGER = 0,     /* ledger slots in use */
+  ALODLM_DECODE_GENERATED = 1,  /* tokens in the output stream */
+  ALODLM_DECODE_CACHE = 2,      /* cached prefix rows (retired tokens + prompt) */
+  ALODLM_DECODE_DONE = 3,       /* 1 once decoding has ended */
+  ALODLM_DECODE_REASON = 4,     /* ALODLM_DECODE_LENGTH or ALODLM_DECODE_EOS */
+  ALODLM_DECODE_WINDOW = 5,     /* rows of the planned window */
+  ALODLM_DECODE_OBSERVED = 6,   /* committed rows at its start (mask rows follow) */
+  ALODLM_DECODE_PREFIX = 7,     /* leading committed slots it retires when it ends */
+  ALODLM_DECODE_STOP = 8        /* 1 when the last committed depth ended the window */
+};
+enum { ALODLM_DECODE_LENGTH = 0, ALODLM_DECODE_EOS = 1 };
+enum { ALODLM_DECODE_ENTROPY = 0, ALODLM_DECODE_LEFT1 = 1 };
+typedef struct {
+  int64_t* slot_token; int32_t* slot_open; int32_t* slot_depth; float* slot_halt;
+  int64_t* out_token; int32_t* out_depth; float* out_halt;
+  int64_t* row_token; int64_t* row_position;
+  int32_t* mask_row; int32_t* mask_slot; float* mask_offset;
+  int64_t* mask_token; int32_t* mask_exit; int32_t* mask_committed; int32_t* mask_fresh;
+  float* mask_survival; float* mask_first_hazard;
+  int64_t* predicted; float* entropy;
+  int64_t* replace_token; int32_t* replace_depth;
+  int64_t* header;
+  const int64_t* stop_ids; int64_t n_stop;
+  int64_t capacity;        /* rows of the window and mask arrays, slots of the ledger */
+  int64_t max_new_tokens, window_size, mask_token_id, max_depth;
+  float tau, q, penalty;   /* DecodeConfig.tau, .q and the position penalty */
+  int32_t mode;            /* ALODLM_DECODE_ENTROPY or ALODLM_DECODE_LEFT1 */
+} alodlm_decode_state;
+/* The top of the decoding loop (inference.py:185-210) from the header's
+ * ledger, output and cache counts: ends decoding (emitting the committed
+ * run up to a stop token) or grows the ledger to the window size and lays
+ * out the window.  capacity >= 2 * window_size. */
+int alodlm_decode_plan(const alodlm_decode_state* state, void* stream);
+/* Fresh mask-row state for a window given by the caller (rows rows, the
+ * count mask rows at logical positions logical[count]); replace_depth of
+ * every row = max_depth.  alodlm_decode_plan does this itself. */
+int alodlm_decode_begin(const alodlm_decode_state* state, const int64_t* logical, int64_t rows,
+                        int64_t count, void* stream);
+/* One depth's commitments (inference.py:109-142): hazard = sigmoid(gate[row])
+ * of each mask row, survival, the entropy (tau) or left-to-right agreement,
+ * the stop rule (last depth, nothing left, or mean (1 - survival) of the
+ * uncommitted rows >= q) and its fallback (least adjusted entropy commits),
+ * and the next depth's carry table; header[STOP] says whether the window
+ * ended.  With `finish`, an ended window is retired (inference.py:227-238:
+ * the committed run it started with is emitted and stays cached, its
+ * commitments go to their slots) and the next one planned. */
+int alodlm_decode_commit(const alodlm_decode_state* state, const float* gate, int64_t count,
+                         int64_t depth, int finish, void* stream);
+
 /* Scatter ce of the selected rows into ce_full[depth, rows]. */
 int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n_rows,
                       int64_t max_rows, float* ce_full, int64_t rows, void* stream);

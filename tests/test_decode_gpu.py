@@ -164,17 +164,8 @@ def _cache_matches_fresh_prefill(model, prompt, cfg, atol, rtol):
     prefill of the same tokens computes (tests/test_inference.py:51-84)."""
     from alodlm_amd.inference import Decoder, PrefixCache
     decoder = Decoder(model, tokenizer())
-    caches = []
-    inner = decoder._window
-
-    def recording(ids, positions, cache, mask_rows, config, logical):
-        caches.append(cache)
-        return inner(ids, positions, cache, mask_rows, config, logical)
-
-    decoder._window = recording
     out = decoder.generate(prompt, cfg)
-    decoder._window = inner
-    cache = caches[-1]
+    cache = decoder.cache
     tokens = torch.tensor(list(prompt) + out["token_ids"], device=DEV)[:cache.length]
     fresh = PrefixCache(model.config)
     empty = torch.empty(0, dtype=torch.long, device=DEV)
@@ -263,3 +254,155 @@ def test_decode_readout(dtype, rows, vocab):
     torch.testing.assert_close(ent.cpu().double(), ref, atol=1e-4, rtol=1e-5)
     if rows > 2:
         assert abs(float(ent[2]) - math.log(vocab)) < 1e-4
+
+
+def _ledger_state(n, ws, gen, cache_rows, seed, max_new=100000, stop=(2,), mode="entropy",
+                  tau=0.4, q=0.5):
+    """A decode state whose ledger holds n slots with a random committed/open
+    pattern (committed slots carry tokens >= 5, open slots the mask id 3)."""
+    from alodlm_amd.inference import (CACHE, GENERATED, HEADER, LEDGER, DecodeConfig,
+                                      _DeviceState)
+    cfg = DecodeConfig(window_size=ws, max_new_tokens=max_new, mode=mode, tau=tau, q=q)
+    st = _DeviceState(DEV, 2 * ws, cfg, 4, 3, list(stop))
+    g = torch.Generator().manual_seed(seed)
+    lead = int(torch.randint(0, max(n, 1), (1,), generator=g)) if n else 0
+    is_open = (torch.rand(n, generator=g) < 0.4).to(torch.int32)
+    is_open[:lead] = 0
+    tokens = torch.randint(5, 50, (n,), generator=g)
+    tokens[is_open.bool()] = 3
+    depth = torch.randint(1, 5, (n,), generator=g, dtype=torch.int32) * (1 - is_open)
+    halt = torch.rand(n, generator=g) * (1 - is_open)
+    for name, t in (("slot_token", tokens), ("slot_open", is_open), ("slot_depth", depth),
+                    ("slot_halt", halt)):
+        st[name][:n].copy_(t)
+    h = torch.zeros(HEADER, dtype=torch.int64)
+    h[LEDGER], h[GENERATED], h[CACHE] = n, gen, cache_rows
+    st["header"].copy_(h)
+    return st, cfg, tokens, is_open, depth, halt
+
+
+def _expected_plan(tokens, is_open, ws, gen, cache_rows, max_new, penalty):
+    import numpy as np
+    n = len(tokens)
+    opened = np.nonzero(is_open.numpy())[0]
+    p = int(opened[0]) if len(opened) else n
+    n2 = max(n, p + min(ws, max_new - gen - p))
+    tok = np.concatenate([tokens.numpy(), np.full(n2 - n, 3)])
+    op = np.concatenate([is_open.numpy(), np.ones(n2 - n, dtype=np.int32)])
+    closed, masks = np.nonzero(op == 0)[0], np.nonzero(op == 1)[0]
+    order = np.concatenate([closed, masks])
+    offset = (masks - p).astype(np.float32) * np.float32(penalty)
+    return dict(p=p, n2=n2, n_obs=len(closed), row_token=tok[order], row_position=cache_rows + order,
+                mask_slot=masks, mask_offset=offset)
+
+
+@pytest.mark.parametrize("n,ws,gen,seed", [(0, 4, 0, 0), (5, 8, 3, 1), (600, 700, 10, 2),
+                                           (300, 256, 0, 3), (1000, 513, 7, 4)])
+def test_decode_plan_lays_out_the_window(n, ws, gen, seed):
+    """alodlm_decode_plan (inference.py:185-210) against numpy: the committed
+    run, ledger growth, committed-first row order, positions, mask slots and
+    position penalties, across several 256-slot chunks."""
+    from alodlm_amd import _lib
+    from alodlm_amd.inference import DONE, LEDGER, OBSERVED, PREFIX, WINDOW
+    log(f"plan n={n} ws={ws} gen={gen}")
+    n = min(n, ws)  # a ledger never holds more than window_size slots
+    st, cfg, tokens, is_open, _, _ = _ledger_state(n, ws, gen, 77, seed)
+    _lib.call("alodlm_decode_plan", st.ref, _lib.stream_handle(DEV))
+    h = st.read_header()
+    want = _expected_plan(tokens, is_open, ws, gen, 77, cfg.max_new_tokens, cfg.penalty)
+    n2, n_obs = want["n2"], want["n_obs"]
+    assert (h[DONE], h[LEDGER], h[WINDOW], h[OBSERVED], h[PREFIX]) == (0, n2, n2, n_obs, want["p"])
+    assert st["row_token"][:n2].cpu().tolist() == want["row_token"].tolist()
+    assert st["row_position"][:n2].cpu().tolist() == want["row_position"].tolist()
+    assert st["mask_row"][:n2 - n_obs].cpu().tolist() == list(range(n_obs, n2))
+    assert st["mask_slot"][:n2 - n_obs].cpu().tolist() == want["mask_slot"].tolist()
+    assert torch.equal(st["mask_offset"][:n2 - n_obs].cpu(), torch.from_numpy(want["mask_offset"]))
+    assert st["replace_depth"][:n2].cpu().tolist() == [4] * n2
+    assert st["mask_survival"][:n2 - n_obs].cpu().tolist() == [1.0] * (n2 - n_obs)
+
+
+@pytest.mark.parametrize("budget_left", [False, True])
+def test_decode_plan_ends_on_stop_token_or_budget(budget_left):
+    """A stop token inside the committed run ends decoding with the run up to
+    it emitted (reason eos); a run that reaches the budget is emitted whole
+    (reason length)."""
+    from alodlm_amd import _lib
+    from alodlm_amd.inference import DONE, GENERATED, REASON, REASON_EOS
+    ws, n, gen = 300, 300, 5
+    max_new = gen + 40 if budget_left else 100000
+    st, _, tokens, is_open, depth, halt = _ledger_state(n, ws, gen, 0, 11, max_new=max_new)
+    st["slot_open"][:60].zero_()
+    run = 60 if budget_left else 59
+    if budget_left:
+        st["slot_open"][40] = 1  # the committed run is 40 slots = the budget left
+        run = 40
+    else:
+        st["slot_token"][59] = 2  # a stop token at slot 59 of a 60-slot run
+    tok = st["slot_token"][:run].cpu().clone()
+    dep, hal = st["slot_depth"][:run].cpu().clone(), st["slot_halt"][:run].cpu().clone()
+    _lib.call("alodlm_decode_plan", st.ref, _lib.stream_handle(DEV))
+    h = st.read_header()
+    emitted = 40 if budget_left else 59
+    assert h[DONE] == 1 and h[GENERATED] == gen + emitted
+    assert (h[REASON] == REASON_EOS) == (not budget_left)
+    assert st["out_token"][gen:gen + emitted].cpu().tolist() == tok[:emitted].tolist()
+    assert st["out_depth"][gen:gen + emitted].cpu().tolist() == dep[:emitted].tolist()
+    assert torch.equal(st["out_halt"][gen:gen + emitted].cpu(), hal[:emitted])
+
+
+def test_decode_commit_fallback_retires_and_replans():
+    """At the last depth with nothing agreed (tau = 0) the mask row of least
+    adjusted entropy commits (first of equal minima); with `finish` the
+    window is retired - its committed run emitted, the commitment written to
+    its slot, the ledger shifted across chunks - and the next window planned."""
+    from alodlm_amd import _lib
+    from alodlm_amd.inference import (CACHE, DONE, GENERATED, LEDGER, OBSERVED, PREFIX, STOP,
+                                      WINDOW)
+    ws, n, gen, cache_rows = 400, 400, 3, 50
+    st, cfg, tokens, is_open, depth, halt = _ledger_state(n, ws, gen, cache_rows, 5, tau=0.0)
+    sh = _lib.stream_handle(DEV)
+    _lib.call("alodlm_decode_plan", st.ref, sh)
+    h = st.read_header()
+    rows, n_obs, p = h[WINDOW], h[OBSERVED], h[PREFIX]
+    count = rows - n_obs
+    assert count > 256 and p > 0
+    ledger = st["slot_token"][:rows].cpu().clone()
+    opened = st["slot_open"][:rows].cpu().clone()
+    g = torch.Generator().manual_seed(9)
+    entropy = torch.rand(count, generator=g) + 1.0
+    pick = count - 3
+    entropy[pick] = 0.0
+    entropy[pick + 1] = 0.0  # equal minimum after the pick: the first wins
+    st["mask_offset"][:count].zero_()
+    predicted = torch.randint(100, 200, (count,), generator=g)
+    st["entropy"][:count].copy_(entropy)
+    st["predicted"][:count].copy_(predicted)
+    gate = torch.randn(rows, generator=g).to(DEV)
+    # without `finish` the window's state stays for inspection
+    _lib.call("alodlm_decode_commit", st.ref, _lib.ptr(gate), count, 3, 0, sh)
+    h1 = st.read_header()
+    assert h1[STOP] == 1 and h1[GENERATED] == gen and h1[WINDOW] == rows
+    committed = st["mask_committed"][:count].cpu()
+    assert committed.nonzero().flatten().tolist() == [pick]
+    assert int(st["mask_token"][pick]) == int(predicted[pick])
+    assert int(st["mask_exit"][pick]) == 4
+    hazard = torch.sigmoid(gate.cpu()[st["mask_row"][:count].cpu().long()])
+    torch.testing.assert_close(st["mask_first_hazard"][:count].cpu(), torch.zeros(count))
+    torch.testing.assert_close(st["mask_survival"][:count].cpu(), 1 - hazard, rtol=1e-6, atol=1e-7)
+    slot = int(st["mask_slot"][pick])  # (the next plan rewrites the mask rows)
+    # again with `finish`: the row committed above is kept (no second fallback)
+    _lib.call("alodlm_decode_commit", st.ref, _lib.ptr(gate), count, 3, 1, sh)
+    h2 = st.read_header()
+    assert h2[STOP] == 1 and h2[DONE] == 0
+    assert h2[GENERATED] == gen + p and h2[CACHE] == cache_rows + p
+    assert st["out_token"][gen:gen + p].cpu().tolist() == ledger[:p].tolist()
+    # the ledger after retirement, then the next plan from it
+    after_tok, after_open = ledger.clone(), opened.clone()
+    after_tok[slot], after_open[slot] = int(predicted[pick]), 0
+    after_tok, after_open = after_tok[p:], after_open[p:]
+    want = _expected_plan(after_tok, after_open, ws, gen + p, cache_rows + p, cfg.max_new_tokens,
+                          cfg.penalty)
+    assert (h2[LEDGER], h2[WINDOW], h2[OBSERVED], h2[PREFIX]) == (
+        want["n2"], want["n2"], want["n_obs"], want["p"])
+    assert st["row_token"][:want["n2"]].cpu().tolist() == want["row_token"].tolist()
+    assert st["row_position"][:want["n2"]].cpu().tolist() == want["row_position"].tolist()

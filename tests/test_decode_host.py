@@ -83,3 +83,52 @@ def test_cache_growth_keeps_prefix():
     torch.testing.assert_close(cache.values[(0, 0)][0][2:], more[[0, 2]])
     with pytest.raises(ValueError):
         cache._bind(2, 4, torch.float32, torch.device("cpu"))
+
+
+def test_decode_state_struct_matches_header(tmp_path):
+    """The ctypes mirror of alodlm_decode_state has the C struct's field
+    order, offsets and size (a gcc-compiled probe prints them)."""
+    import ctypes
+    import shutil
+    import subprocess
+    from pathlib import Path
+    from alodlm_amd.inference import DecodeState
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    include = Path(__file__).resolve().parents[1] / "include"
+    fields = [name for name, _ in DecodeState._fields_]
+    src = tmp_path / "probe.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"alodlm_hip.h\"\n"
+                   "int main(void) {\n" + "".join(
+                       f'  printf("%zu\\n", offsetof(alodlm_decode_state, {f}));\n'
+                       for f in fields) +
+                   '  printf("%zu\\n", sizeof(alodlm_decode_state));\n  return 0;\n}\n')
+    exe = tmp_path / "probe"
+    subprocess.run([gcc, "-I", str(include), str(src), "-o", str(exe)], check=True)
+    out = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    assert out[:-1] == [getattr(DecodeState, f).offset for f in fields]
+    assert out[-1] == ctypes.sizeof(DecodeState)
+
+
+def test_stop_tokens_and_penalty():
+    """EOS id(s) plus the chat end markers the vocabulary holds
+    (alodlm/inference.py:158-163); the default position penalty is tau / 20."""
+    from alodlm_amd.inference import DecodeConfig, stop_token_ids
+
+    class Tok:
+        def __init__(self, eos, vocab):
+            self.eos_token_id, self.vocab = eos, vocab
+
+        def get_vocab(self):
+            return self.vocab
+
+        def convert_tokens_to_ids(self, t):
+            return self.vocab[t]
+
+    assert stop_token_ids(Tok(7, {"<|im_end|>": 9, "x": 1})) == [7, 9]
+    assert stop_token_ids(Tok([5, 2], {"</s>": 2})) == [2, 5]
+    assert stop_token_ids(Tok(None, {})) == []
+    assert DecodeConfig(tau=0.4).penalty == pytest.approx(0.02)
+    assert DecodeConfig(tau=0.4, position_penalty=0.0).penalty == 0.0
