@@ -390,6 +390,66 @@ def run_readout(device, steps, warmup, kernel_timing):
     return record
 
 
+def run_attention(spec, device, steps, warmup):
+    """The attention kernels alone at a step configuration's layer shape: one
+    pack of the configuration's segments under the training mask, random
+    bf16 q/k/v/dO; forward, then backward (dQ pass, dK/dV pass), each timed
+    with HIP events on the launch stream.  For kernel profiling; not a line
+    of the benchmark's metric."""
+    from alodlm_amd import _lib
+    from alodlm_amd.layers import DualStreamMask
+    nq, nkv, dh = spec["num_attention_heads"], spec["num_key_value_heads"], 128
+    offsets = [0]
+    for L in spec["segments"]:
+        offsets.append(offsets[-1] + L)
+    mask = DualStreamMask(offsets, 32, device)
+    N = mask.rows
+    g = torch.Generator(device=device).manual_seed(5)
+    q, do = (torch.randn(N, nq * dh, generator=g, device=device).to(torch.bfloat16)
+             for _ in range(2))
+    k, v = (torch.randn(N, nkv * dh, generator=g, device=device).to(torch.bfloat16)
+            for _ in range(2))
+    o = torch.empty_like(q)
+    lse = torch.empty(nq, N, dtype=torch.float32, device=device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    n_tiles = mask.tiles.shape[0]
+    ws = torch.empty(_lib.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, n_tiles),
+                     dtype=torch.float32, device=device)
+    st = _lib.stream_handle(device)
+    P = _lib.ptr
+    code = _lib.BF16_CODE
+
+    def fwd():
+        _lib.call("alodlm_attention_fwd", P(q), P(k), P(v), nkv * dh, P(mask.boundaries),
+                  P(mask.row_segment), P(mask.tiles), n_tiles, P(o), P(lse), N, nq, nkv, dh, 32,
+                  code, st)
+
+    def bwd():
+        _lib.call("alodlm_attention_bwd", P(q), P(k), P(v), nkv * dh, P(o), P(lse), P(do),
+                  P(mask.boundaries), P(mask.row_segment), P(mask.tiles), n_tiles, P(dq), P(dk),
+                  P(dv), nkv * dh, P(ws), N, nq, nkv, dh, 32, code, st)
+
+    out = {}
+    for name, fn, per_pair in (("attention_fwd", fwd, 4), ("attention_bwd", bwd, 8)):
+        for _ in range(warmup):
+            fn()
+        stream = torch.cuda.current_stream(device)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            fn()
+        t1.record(stream)
+        t1.synchronize()
+        us = 1000.0 * t0.elapsed_time(t1) / steps
+        flops = per_pair * dh * nq * mask.pairs
+        out[name] = {"us_per_call": round(us, 1), "tflops": round(flops / us / 1e6, 1),
+                     "frac": round(flops / (us / 1e6) / PEAK_BF16, 4)}
+    print(json.dumps({"kernel": "attention", "workload": f"{spec['name']} layer shape: "
+                      f"{len(spec['segments'])} x {spec['segments'][0]} tokens ({N} dual-stream "
+                      f"rows), {nq}/{nkv} heads, head_dim 128", "pairs_per_head": mask.pairs,
+                      "steps": steps, **out}), flush=True)
+
+
 def cpu_baseline(spec, cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     """Time the CPU oracle (float32, torch eager on this host) on a bounded
     sample: `layer_reps` decoder-layer fwd+bwd passes of the model's layer
@@ -451,6 +511,9 @@ def main():
     parser.add_argument("--traffic-calibration", action="store_true",
                         help="first run one plain 1 GiB device copy (read 1 GiB, write "
                              "1 GiB) so that HBM byte counters can be scaled against it")
+    parser.add_argument("--kernel", choices=["attention"],
+                        help="time one kernel class alone at the --model layer shape "
+                             "(for profiling) instead of the step")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -468,6 +531,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     spec = MODELS[args.model]
+    if args.kernel == "attention":
+        run_attention(spec, device, args.steps, args.warmup)
+        return
     timing = not args.no_kernel_timing
     head, facts = run_step(spec, device, args.steps, args.warmup, timing)
     line = {

@@ -17,6 +17,10 @@ numpy, loadable with ``allow_pickle=False``).  Cases:
   1/2/1, 4 q / 2 kv heads of 64, SwiGLU 768, vocab 1024, 4 x 128 tokens,
   seed 0) - loss, metrics, gates, exits, CE, and per-gradient summaries
   (norm, a fixed random projection, a strided sample).
+* ``step_tiny_bf16``: the same model and inputs cast to bfloat16, as the
+  reference runs with ``precision: bf16`` (its eager bf16 rounding sequence
+  on the CPU): the same outputs, gates and gradient summaries as float64 of
+  the bf16 values.
 """
 
 import argparse
@@ -58,7 +62,7 @@ def step_case(model, ids, labels, boundaries, seed, lr, full_grads, capture):
     def rollout(self, batch):
         logits, gates, exits = original_rollout(self, batch)
         captured["batch"] = batch
-        captured["gates"] = torch.stack([g.detach() for g in gates])
+        captured["gates"] = torch.stack([g.detach() for g in gates]).float()
         captured["exits"] = exits.clone()
         return logits, gates, exits
 
@@ -178,6 +182,12 @@ def main():
     ids = torch.randint(0, 1024, (512,), generator=g)
     cases["step_tiny"] = step_case(model, ids, ids.clone(), torch.tensor([0, 128, 256, 384, 512]),
                                    0, 1e-4, False, None)
+    model = ALoDLM(Qwen3ForCausalLM(backbone.config), cfg)
+    model.load_state_dict({(k if k.startswith("exit_gate.") else "backbone." + k): v
+                           for k, v in params.items()}, strict=True)
+    model = model.to(torch.bfloat16)
+    cases["step_tiny_bf16"] = step_case(model, ids, ids.clone(),
+                                        torch.tensor([0, 128, 256, 384, 512]), 0, 1e-4, False, None)
 
     meta = {"torch": torch.__version__}
     import transformers
