@@ -161,12 +161,14 @@ class FusedAdamW(torch.optim.Optimizer):
         super().zero_grad(set_to_none)
 
     def load_state_dict(self, state_dict):
-        """Restore a ``state_dict()`` of this optimizer.
+        """Restore a ``state_dict()`` of this optimizer or of a
+        ``torch.optim.AdamW`` over the same parameter groups.
 
         The float32 masters and moments are restored as float32 whatever the
         parameter dtype (``torch.optim.Optimizer.load_state_dict`` would cast
         them to it).  Float32 parameters take their master's values and share
-        its storage again.
+        its storage again.  A state without masters (torch's AdamW keeps
+        none) takes them from the parameters' current values.
         """
         saved_groups = state_dict["param_groups"]
         if len(saved_groups) != len(self.param_groups):
@@ -185,7 +187,7 @@ class FusedAdamW(torch.optim.Optimizer):
                 if not entry:
                     continue
                 f32 = lambda t: t.to(device=p.device, dtype=torch.float32).clone()
-                master = f32(entry["master"])
+                master = f32(entry["master"] if "master" in entry else p.detach())
                 if p.dtype == torch.float32:
                     p.data.copy_(master)
                     master = p.detach()

@@ -13,11 +13,12 @@ What differs by design:
 * one process on one GPU; no accelerate or DeepSpeed wrapper (``use_deepspeed``
   is accepted and only enters the run identity);
 * the optimizer is ``FusedAdamW`` with float32 masters and moments whatever
-  the parameter dtype, and ``training_state/`` holds this implementation's
-  state: ``optimizer.json`` (hyperparameters, step counts, shard list) with
-  float32 tensors in ``optimizer-*.safetensors`` shards of at most 4 GiB,
-  ``scheduler.json`` and ``random_states.json`` (Python, NumPy, torch CPU and
-  every GPU generator).  Nothing in it is a pickle;
+  the parameter dtype; ``training_state/`` keeps accelerate's layout
+  (``model.safetensors``, ``optimizer.bin`` as a torch AdamW state dict with
+  the float32 masters as an extra per-parameter entry,
+  ``custom_checkpoint_0.pkl`` for the scheduler, ``random_states_0.pkl``), so
+  checkpoints resume across the two
+  implementations; it is read back with ``torch.load(weights_only=True)``;
 * the loss finiteness check reads the loss after the backward has been
   queued, so the GPU does not idle between forward and backward; a non-finite
   loss still raises ``FloatingPointError`` before any parameter changes.
@@ -41,8 +42,6 @@ from .model import ALoDLM
 from .optim import FusedAdamW, param_groups
 
 WORLD_SIZE = 1
-SHARD_BYTES = 4 << 30
-STATE_KEYS = ("master", "exp_avg", "exp_avg_sq")
 
 
 def set_seed(seed):
@@ -126,88 +125,104 @@ def _param_names(model):
     return {id(p): name for name, p in model.named_parameters()}
 
 
-def save_training_state(directory, model, optimizer, scheduler):
-    """Write optimizer, schedule and generator state to ``directory``."""
+# torch.load of the training state's tensors and plain containers only; the
+# NumPy generator state additionally needs these (accelerate allows the same)
+_NUMPY_SAFE = ("numpy.core.multiarray._reconstruct", "numpy._core.multiarray._reconstruct",
+               "numpy.ndarray", "numpy.dtype", "numpy.dtypes.UInt32DType")
+
+
+def _safe_load(path):
+    import importlib
+    allowed = []
+    for qualified in _NUMPY_SAFE:
+        module, _, attr = qualified.rpartition(".")
+        try:
+            allowed.append(getattr(importlib.import_module(module), attr))
+        except (ImportError, AttributeError):
+            pass
+    with torch.serialization.safe_globals(allowed):
+        return torch.load(path, map_location="cpu", weights_only=True)
+
+
+def _adamw_group_defaults(lr):
+    """The parameter-group fields torch.optim.AdamW(groups, lr) records in its
+    state dict (this torch version's), so that a torch AdamW restores them."""
+    probe = torch.optim.AdamW([torch.zeros(1, requires_grad=True)], lr=lr)
+    fields = dict(probe.param_groups[0])
+    fields.pop("params")
+    return fields
+
+
+def save_training_state(directory, model, optimizer, scheduler, loader_position=0):
+    """Write ``directory`` in the layout accelerate's ``save_state`` gives a
+    one-process run without DeepSpeed (alodlm/train.py:94; accelerate
+    checkpointing.save_accelerator_state):
+
+    * ``model.safetensors``: the model's state dict;
+    * ``optimizer.bin``: a ``torch.optim.AdamW`` state dict - per parameter
+      index (groups in order) ``step`` (float tensor), ``exp_avg`` and
+      ``exp_avg_sq``, plus ``master``, the float32 master weight, which a torch
+      AdamW carries along unused; group fields as torch.optim.AdamW records;
+    * ``custom_checkpoint_0.pkl``: the LR scheduler's state dict (the
+      reference registers its scheduler for checkpointing,
+      alodlm/train.py:58);
+    * ``random_states_0.pkl``: Python, NumPy, torch CPU and GPU generator
+      states and accelerate's step counter (micro-batches since the epoch
+      started, ``loader_position``).
+    """
     from safetensors.torch import save_file
     directory = Path(directory)
     directory.mkdir(parents=True)
-    names = _param_names(model)
-    groups, steps, shards = [], {}, []
-    pending, pending_bytes = {}, 0
-
-    def flush():
-        nonlocal pending, pending_bytes
-        if pending:
-            name = f"optimizer-{len(shards):05d}.safetensors"
-            save_file(pending, str(directory / name))
-            shards.append(name)
-            pending, pending_bytes = {}, 0
-
+    weights = {k: v.detach().to("cpu").contiguous() for k, v in model.state_dict().items()}
+    save_file(weights, str(directory / "model.safetensors"), metadata={"format": "pt"})
+    index = {}
+    state, groups = {}, []
     for group in optimizer.param_groups:
-        groups.append({**{k: v for k, v in group.items() if k != "params"},
-                       "params": [names[id(p)] for p in group["params"]]})
+        defaults = _adamw_group_defaults(group["lr"])
+        fields = {**defaults, **{k: v for k, v in group.items() if k in defaults}}
+        ids = []
         for p in group["params"]:
-            state = optimizer.state.get(p)
-            if not state:
+            i = index.setdefault(id(p), len(index))
+            ids.append(i)
+            entry = optimizer.state.get(p)
+            if not entry:
                 continue
-            name = names[id(p)]
-            steps[name] = int(state["step"])
-            for key in STATE_KEYS:
-                tensor = state[key]
-                pending[f"{name}/{key}"] = tensor.detach().to("cpu", copy=True)
-                pending_bytes += tensor.numel() * tensor.element_size()
-            if pending_bytes >= SHARD_BYTES:
-                flush()
-    flush()
-    (directory / "optimizer.json").write_text(json.dumps(
-        {"param_groups": groups, "step": steps, "shards": shards}, indent=1) + "\n")
-    (directory / "scheduler.json").write_text(json.dumps(scheduler.state_dict()) + "\n")
-    version, mt, gauss = random.getstate()
-    np_state = np.random.get_state()
-    rng = {
-        "python": [version, list(mt), gauss],
-        "numpy": [np_state[0], np_state[1].tolist(), *(float(v) if isinstance(v, float) else int(v)
-                                                        for v in np_state[2:])],
-        "torch_cpu": torch.get_rng_state().tolist(),
-        "torch_gpu": [s.tolist() for s in torch.cuda.get_rng_state_all()],
-    }
-    (directory / "random_states.json").write_text(json.dumps(rng) + "\n")
+            state[i] = {"step": torch.tensor(float(entry["step"]))}
+            for key in ("exp_avg", "exp_avg_sq", "master"):
+                state[i][key] = entry[key].detach().to("cpu", copy=True)
+        groups.append({**fields, "params": ids})
+    torch.save({"state": state, "param_groups": groups}, directory / "optimizer.bin")
+    torch.save(scheduler.state_dict(), directory / "custom_checkpoint_0.pkl")
+    rng = {"step": int(loader_position), "random_state": random.getstate(),
+           "numpy_random_seed": np.random.get_state(), "torch_manual_seed": torch.get_rng_state()}
+    if torch.cuda.is_available():
+        rng["torch_cuda_manual_seed"] = torch.cuda.get_rng_state_all()
+    torch.save(rng, directory / "random_states_0.pkl")
 
 
 def load_training_state(directory, model, optimizer, scheduler):
-    """Restore what ``save_training_state`` wrote."""
+    """Restore a training state in accelerate's layout: one written by
+    ``save_training_state`` or by the reference's ``accelerator.save_state``
+    (float32 masters taken from the parameters when the state has none, as a
+    torch AdamW keeps no master).  Returns accelerate's step counter."""
     from safetensors.torch import load_file
     directory = Path(directory)
-    meta = json.loads((directory / "optimizer.json").read_text())
-    tensors = {}
-    for shard in meta["shards"]:
-        tensors.update(load_file(str(directory / shard)))
-    by_name = dict(model.named_parameters())
-    index_of, saved_groups, state, index = {}, [], {}, 0
-    for group in meta["param_groups"]:
-        ids = []
-        for name in group["params"]:
-            if name not in by_name:
-                raise ValueError(f"training state names an unknown parameter {name}")
-            index_of[name] = index
-            ids.append(index)
-            if name in meta["step"]:
-                state[index] = {"step": meta["step"][name],
-                                **{key: tensors[f"{name}/{key}"] for key in STATE_KEYS}}
-            index += 1
-        saved_groups.append({**{k: v for k, v in group.items() if k != "params"}, "params": ids})
-    for group in saved_groups:
-        if "betas" in group:
-            group["betas"] = tuple(group["betas"])
-    optimizer.load_state_dict({"state": state, "param_groups": saved_groups})
-    scheduler.load_state_dict(json.loads((directory / "scheduler.json").read_text()))
-    rng = json.loads((directory / "random_states.json").read_text())
-    version, mt, gauss = rng["python"]
-    random.setstate((version, tuple(mt), gauss))
-    np.random.set_state((rng["numpy"][0], np.asarray(rng["numpy"][1], dtype=np.uint32),
-                         *rng["numpy"][2:]))
-    torch.set_rng_state(torch.tensor(rng["torch_cpu"], dtype=torch.uint8))
-    torch.cuda.set_rng_state_all([torch.tensor(s, dtype=torch.uint8) for s in rng["torch_gpu"]])
+    weights = load_file(str(directory / "model.safetensors"))
+    with torch.no_grad():
+        missing, unexpected = model.load_state_dict(weights, strict=False)
+    if missing or unexpected:
+        raise ValueError(f"training state does not fit the model (missing {missing[:3]}, "
+                         f"unexpected {unexpected[:3]})")
+    optimizer.load_state_dict(_safe_load(directory / "optimizer.bin"))
+    scheduler.load_state_dict(_safe_load(directory / "custom_checkpoint_0.pkl"))
+    rng = _safe_load(directory / "random_states_0.pkl")
+    random.setstate(rng["random_state"])
+    np.random.set_state(rng["numpy_random_seed"])
+    torch.set_rng_state(rng["torch_manual_seed"])
+    cuda = rng.get("torch_cuda_manual_seed")
+    if cuda is not None and torch.cuda.is_available() and len(cuda) == torch.cuda.device_count():
+        torch.cuda.set_rng_state_all(cuda)
+    return int(rng.get("step", 0))
 
 
 def load_checkpoint_weights(model, directory):
@@ -272,7 +287,8 @@ def train(config):
             raise FileExistsError("Checkpoint already exists")
         model.save_pretrained(destination)
         tokenizer.save_pretrained(destination)
-        save_training_state(destination / "training_state", model, optimizer, scheduler)
+        save_training_state(destination / "training_state", model, optimizer, scheduler,
+                            next_batch)
         record = {"step": step, "epoch": epoch, "next_batch": next_batch,
                   "identity": identity, "epoch_rng": epoch_rng}
         # written last: its presence marks the checkpoint complete

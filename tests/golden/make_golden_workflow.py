@@ -21,6 +21,8 @@ inputs and outputs are stored, under ``tests/golden/workflow/``:
   accumulation over 2 packs and no step cap (2 epochs): the printed header,
   the pack index each step consumed, every ``metrics.jsonl`` record, each
   checkpoint's ``trainer_state.json`` and file names.
+* ``reference_checkpoint-2/``: the run's ``checkpoint-2`` as the reference
+  wrote it, ``training_state/`` in accelerate's layout included.
 """
 
 import argparse
@@ -134,6 +136,10 @@ def main():
                     "trainer_state": json.loads((ckpt / "trainer_state.json").read_text()),
                     "files": sorted(p.name for p in ckpt.iterdir()),
                 }
+            if name == "run":
+                # a complete reference checkpoint (weights, tokenizer,
+                # accelerate training state, trainer state) to resume from
+                shutil.copytree(output / "checkpoint-2", OUT / "reference_checkpoint-2")
             result[name] = {
                 "steps": steps,
                 "header": lines[0],

@@ -116,6 +116,32 @@ def test_resume_is_exact(workflow):
     assert again == straight
 
 
+def test_resume_from_reference_checkpoint(tmp_path):
+    """A checkpoint the reference wrote (its recorded run's checkpoint-2, with
+    training_state/ saved by accelerate) resumes here: the interrupted epoch's
+    remaining packs in the reference's order, the reference resumption's
+    learning rates and metric names, and its final trainer state."""
+    shutil.copy(FIXTURE / "training.jsonl", tmp_path / "training.jsonl")
+    consumed = []
+    print("[train] resume from the reference's checkpoint-2", file=sys.stderr, flush=True)
+    steps = run_train(write_config(tmp_path, "resumed", resume=str(
+        GOLDEN / "workflow" / "reference_checkpoint-2")), consumed)
+    want = RUN["resumed"]
+    assert steps == want["steps"]
+    # the remaining packs of the interrupted epoch (later epochs draw their
+    # order after this run's masks, which come from the GPU generator here)
+    assert consumed[:2] == want["consumed"][:2]
+    records = [json.loads(l) for l in (tmp_path / "resumed" / "metrics.jsonl").read_text().splitlines()]
+    assert [r["step"] for r in records] == [r["step"] for r in want["metrics"]]
+    for got, ref in zip(records, want["metrics"]):
+        assert list(got) == list(ref)
+        assert got["learning_rate"] == pytest.approx(ref["learning_rate"], rel=1e-12, abs=1e-18)
+    for name, ref in want["checkpoints"].items():
+        state = json.loads((tmp_path / "resumed" / name / "trainer_state.json").read_text())
+        for key in ("step", "epoch", "next_batch", "identity"):
+            assert state[key] == ref["trainer_state"][key], (name, key)
+
+
 def test_resume_requires_same_identity(workflow):
     tmp, _, _ = workflow
     path = write_config(tmp, "mismatch", learning_rate=2e-5, resume=str(tmp / "run" / "checkpoint-2"))

@@ -162,8 +162,101 @@ def test_training_state_round_trip(tmp_path):
     assert sched2.get_last_lr() == sched.get_last_lr()
     assert (random.random(), np.random.rand(), torch.rand(1).item()) == expect
     files = sorted(p.name for p in (tmp_path / "state").iterdir())
-    assert files == ["optimizer-00000.safetensors", "optimizer.json", "random_states.json",
-                     "scheduler.json"]
+    assert files == sorted(p.name for p in (REFERENCE_CHECKPOINT / "training_state").iterdir())
+
+
+REFERENCE_CHECKPOINT = GOLDEN / "workflow" / "reference_checkpoint-2"
+
+
+def _reference_side(model):
+    """The reference's optimizer and scheduler over ``model``
+    (alodlm/train.py:42-56): torch.optim.AdamW over the two decay groups and
+    transformers' cosine schedule with warmup."""
+    from transformers import get_cosine_schedule_with_warmup
+    no_decay = ("bias", "LayerNorm.weight", "layer_norm.weight")
+    groups = [
+        {"params": [p for n, p in model.named_parameters() if not any(s in n for s in no_decay)],
+         "weight_decay": 0.01},
+        {"params": [p for n, p in model.named_parameters() if any(s in n for s in no_decay)],
+         "weight_decay": 0.0},
+    ]
+    optimizer = torch.optim.AdamW(groups, lr=1e-5)
+    return optimizer, get_cosine_schedule_with_warmup(optimizer, 0, 4)
+
+
+def test_reference_training_state_loads():
+    """A training state the reference wrote through accelerate (checkpoint-2
+    of its recorded run) restores into this implementation: moments and step
+    counts equal the reference's, float32 masters are the parameters, the
+    schedule continues from the same learning rate, the generators and
+    accelerate's step counter are the reference's."""
+    from alodlm_amd.model import ALoDLM
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    from alodlm_amd.train import _safe_load, cosine_schedule, load_training_state
+    state_dir = REFERENCE_CHECKPOINT / "training_state"
+    model = ALoDLM.from_pretrained(REFERENCE_CHECKPOINT)
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-5, max_grad_norm=1.0)
+    sched = cosine_schedule(opt, RUN["run"]["steps"], 0.03)  # the fixture run's warmup ratio
+    position = load_training_state(state_dir, model, opt, sched)
+    ref = _safe_load(state_dir / "optimizer.bin")
+    params = [p for g in opt.param_groups for p in g["params"]]
+    assert len(params) == len(ref["state"])
+    for index, p in enumerate(params):
+        entry = ref["state"][index]
+        assert opt.state[p]["step"] == int(entry["step"]) == 2
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(opt.state[p][key], entry[key].float())
+        assert torch.equal(opt.state[p]["master"], p.detach().float())
+    assert [g["lr"] for g in opt.param_groups] == [g["lr"] for g in ref["param_groups"]]
+    assert sched.get_last_lr() == _safe_load(state_dir / "custom_checkpoint_0.pkl")["_last_lr"]
+    rng = _safe_load(state_dir / "random_states_0.pkl")
+    assert torch.equal(torch.get_rng_state(), rng["torch_manual_seed"])
+    assert random.getstate() == rng["random_state"]
+    assert position == 2
+
+
+def test_training_state_restores_into_the_reference(tmp_path):
+    """A training state written here restores through accelerate's own
+    loaders into the reference's objects (model, torch.optim.AdamW, the
+    registered scheduler): weights, moments, step counts, learning rates and
+    generators."""
+    from accelerate import PartialState
+    from accelerate.checkpointing import load_accelerator_state, load_custom_state
+    PartialState(cpu=True)  # accelerate's loaders log through its process state
+    from alodlm_amd.model import ALoDLM
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    from alodlm_amd.train import cosine_schedule, save_training_state
+    model = ALoDLM.from_pretrained(REFERENCE_CHECKPOINT)
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-5, max_grad_norm=1.0)
+    sched = cosine_schedule(opt, 4, 0.0)
+    g = torch.Generator().manual_seed(3)
+    for p in model.parameters():
+        opt.state[p] = {"step": 2, "master": p.detach().float().clone(),
+                        "exp_avg": torch.randn(p.shape, generator=g),
+                        "exp_avg_sq": torch.rand(p.shape, generator=g)}
+    for _ in range(2):
+        sched.step()
+    torch.manual_seed(11)
+    save_training_state(tmp_path / "state", model, opt, sched, loader_position=2)
+    expect = torch.rand(3)
+
+    target = ALoDLM.from_pretrained(REFERENCE_CHECKPOINT)
+    with torch.no_grad():
+        for p in target.parameters():
+            p.zero_()
+    ref_opt, ref_sched = _reference_side(target)
+    torch.manual_seed(0)
+    load_accelerator_state(str(tmp_path / "state"), [target], [ref_opt], [], [], 0)
+    load_custom_state(ref_sched, str(tmp_path / "state"), 0)
+    for (name, p), q in zip(model.named_parameters(), target.parameters()):
+        assert torch.equal(p.detach(), q.detach()), name
+        entry = ref_opt.state[q]
+        assert int(entry["step"]) == 2
+        assert torch.equal(entry["exp_avg"], opt.state[p]["exp_avg"])
+        assert torch.equal(entry["exp_avg_sq"], opt.state[p]["exp_avg_sq"])
+    assert ref_sched.get_last_lr() == sched.get_last_lr()
+    assert [g["lr"] for g in ref_opt.param_groups] == [g["lr"] for g in opt.param_groups]
+    assert torch.equal(torch.rand(3), expect)
 
 
 def test_train_needs_gpu(tmp_path):
