@@ -450,6 +450,58 @@ def run_attention(spec, device, steps, warmup):
                       "steps": steps, **out}), flush=True)
 
 
+def run_gemm(spec, device, steps, warmup):
+    """The bf16 GEMM alone on the products of one layer application of a step
+    configuration (forward on the out-contiguous weight copies, dX on the
+    weights, dW into the float32 gradient arena), each timed with HIP events
+    over ``steps`` calls.  For kernel profiling; not a line of the benchmark's
+    metric."""
+    from alodlm_amd import _lib
+    H, I = spec["hidden_size"], spec["intermediate_size"]
+    nq, nkv, dh = spec["num_attention_heads"], spec["num_key_value_heads"], 128
+    N = 2 * sum(spec["segments"])
+    QW, QD = (nq + 2 * nkv) * dh, nq * dh
+    E = (_lib.EPI_STORE, _lib.EPI_RESIDUAL, _lib.EPI_ACCUM)
+    # name, M, N, K, A k-major, B k-major, epilogue
+    shapes = [("qkv_fwd", N, QW, H, 1, 0, E[0]), ("o_fwd", N, H, QD, 1, 0, E[1]),
+              ("gate_up_fwd", N, 2 * I, H, 1, 0, E[0]), ("down_fwd", N, H, I, 1, 0, E[1]),
+              ("dx_gate_up", N, H, 2 * I, 1, 0, E[0]), ("dx_down", N, I, H, 1, 0, E[0]),
+              ("dw_gate_up", 2 * I, H, N, 0, 0, E[2]), ("dw_down", H, I, N, 0, 0, E[2])]
+    g = torch.Generator(device=device).manual_seed(7)
+    st = _lib.stream_handle(device)
+    stream = torch.cuda.current_stream(device)
+    out = {}
+    for name, M, Nn, K, ak, bk, epi in shapes:
+        A = torch.randn(M * K, generator=g, device=device).to(torch.bfloat16)
+        B = torch.randn(Nn * K, generator=g, device=device).to(torch.bfloat16)
+        cdt = torch.float32 if epi == _lib.EPI_ACCUM else torch.bfloat16
+        C = torch.zeros(M * Nn, dtype=cdt, device=device)
+        R = torch.randn(M * Nn, generator=g, device=device).to(torch.bfloat16) \
+            if epi == _lib.EPI_RESIDUAL else None
+        need = _lib.query("alodlm_gemm_workspace", M, Nn, K, epi, _lib.BF16_CODE)
+        ws = torch.empty(max(need, 1), dtype=torch.float32, device=device) if need else None
+        lda, ldb = (K if ak else M), (K if bk else Nn)
+
+        def call():
+            _lib.call("alodlm_gemm", _lib.ptr(A), lda, ak, _lib.ptr(B), ldb, bk, _lib.ptr(C), Nn,
+                      _lib.ptr(R), Nn, M, Nn, K, 1.0, epi, _lib.BF16_CODE, _lib.ptr(ws), st)
+
+        for _ in range(warmup):
+            call()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            call()
+        t1.record(stream)
+        t1.synchronize()
+        us = 1000.0 * t0.elapsed_time(t1) / steps
+        out[name] = {"mnk": [M, Nn, K], "us": round(us, 1),
+                     "tflops": round(2.0 * M * Nn * K / us / 1e6, 1)}
+        del A, B, C, R, ws
+    print(json.dumps({"kernel": "gemm", "workload": f"{spec['name']} layer products "
+                      f"({N} dual-stream rows)", "steps": steps, "products": out}), flush=True)
+
+
 def cpu_baseline(spec, cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=None):
     """Time the CPU oracle (float32, torch eager on this host) on a bounded
     sample: `layer_reps` decoder-layer fwd+bwd passes of the model's layer
@@ -511,7 +563,7 @@ def main():
     parser.add_argument("--traffic-calibration", action="store_true",
                         help="first run one plain 1 GiB device copy (read 1 GiB, write "
                              "1 GiB) so that HBM byte counters can be scaled against it")
-    parser.add_argument("--kernel", choices=["attention"],
+    parser.add_argument("--kernel", choices=["attention", "gemm"],
                         help="time one kernel class alone at the --model layer shape "
                              "(for profiling) instead of the step")
     args = parser.parse_args()
@@ -533,6 +585,9 @@ def main():
     spec = MODELS[args.model]
     if args.kernel == "attention":
         run_attention(spec, device, args.steps, args.warmup)
+        return
+    if args.kernel == "gemm":
+        run_gemm(spec, device, args.steps, args.warmup)
         return
     timing = not args.no_kernel_timing
     head, facts = run_step(spec, device, args.steps, args.warmup, timing)
