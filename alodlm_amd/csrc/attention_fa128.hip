@@ -33,6 +33,8 @@
 // The host lists tiles by decreasing in-stream start; forward and dQ take
 // them in that order and dK/dV in reverse, so the heaviest tiles of each pass
 // are dispatched first.
+#include <type_traits>
+
 #include "attention_common.h"
 #include "lds_dma.h"
 
@@ -83,6 +85,33 @@ __device__ __forceinline__ bf16x8_t tr_frag(const char* tile, int r0, int cb, in
 
 __device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc += a * b with the accumulator held in AGPRs.  The register allocator
+// otherwise moves long-lived accumulators between AGPRs and VGPRs around
+// every use when the VGPRs are full.  gfx950 needs no wait states between
+// MFMAs chained on one accumulator; a VALU read of `acc` needs 12 after the
+// last such MFMA (mfma_acc_settle).
+__device__ __forceinline__ void mfma_acc(f32x16_t& acc, bf16x8_t a, bf16x8_t b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_acc_settle() { asm volatile("s_nop 15" ::: "memory"); }
+// A zero accumulator made in AGPRs (0 * 0 + 0), so that the register
+// allocator keeps the accumulator's home there from the start.
+__device__ __forceinline__ void mfma_acc_zero(f32x16_t& acc) {
+  const bf16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
+}
+
+// d = a * b (d0: first k step, zero accumulator) / d += a * b with d in VGPRs
+// for the VALU work that follows and b held in AGPRs.  A VALU read of d needs
+// 12 wait states after the MFMA; callers place at least a block of other
+// MFMAs in between, or mfma_acc_settle.
+__device__ __forceinline__ void mfma_v0(f32x16_t& d, bf16x8_t a, bf16x8_t b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "a"(b));
+}
+__device__ __forceinline__ void mfma_v(f32x16_t& d, bf16x8_t a, bf16x8_t b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
 }
 
 struct QTile {  // a 128-row query tile (forward / dQ)
@@ -245,7 +274,8 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                 const bf16_t* __restrict__ o, float* __restrict__ delta,
                 const bf16_t* __restrict__ dout, const int64_t* __restrict__ bounds,
                 const int32_t* __restrict__ tiles, bf16_t* __restrict__ dq, int64_t N, int nq,
-                int nkv, int B, float scale) {
+                int nkv, int B, float scale, int* __restrict__ counter) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *counter = 0;  // for dK/dV
   __shared__ __attribute__((aligned(1024))) char lds[2][2][KT * ROWB];  // [stage][K | V]
   const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -364,27 +394,60 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 // ---------------------------------------------------------------------------
 // dV = P^T dO,  dK = scale * dS^T Q.  lse2[h, r] = lse[h, r] * log2(e), as the
 // dQ pass writes it next to delta.
+//
+// One wavefront per SIMD (one workgroup per CU, so each lane may hold up to
+// 512 registers).  K and V of the wavefront's 32 keys stay in registers as B
+// operands.  Query tiles (32 rows of Q and dO with their lse2 and delta)
+// stream through a ring of DK_STAGES LDS stages.  The loop is
+// software-pipelined; iteration i runs:
+//   A  S and dP of tile i+1 (16 MFMAs), with the VALU work of tile i (P, dS,
+//      bf16 packing) placed between them;
+//   -  a barrier: tile i+2 has landed and the stage of tile i-1 is free;
+//   -  the direct loads of tile i + DK_STAGES - 1 into that stage;
+//   B  dV and dK of tile i (16 MFMAs), with the LDS reads of tile i+2's first
+//      operands and of tile i+1's lse2/delta placed between them.
+// Every instruction group is fenced with sched_barrier, so the compiler keeps
+// this order.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256, 2)
+constexpr int DK_STAGES = 5;
+constexpr int DK_LOADS = 5;  // direct-load instructions per wavefront per query tile
+
+__global__ void __launch_bounds__(256, 1)
 fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                   const bf16_t* __restrict__ v, int64_t ldv, const float* __restrict__ lse2,
                   const float* __restrict__ delta, const bf16_t* __restrict__ dout,
                   const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
                   int n_tiles, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv,
-                  float* __restrict__ partial, int64_t N, int nq, int nkv, int B, float scale) {
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][QT * ROWB];  // [stage][Q | dO]
-  __shared__ __attribute__((aligned(1024))) char lds_v[128 * ROWB];     // V of the key tile
-  __shared__ __attribute__((aligned(16))) float lds_ld[2][2 * QT];      // [stage][lse2 | delta]
+                  float* __restrict__ partial, int64_t N, int nq, int nkv, int B, float scale,
+                  int* __restrict__ counter) {
+  constexpr int S = DK_STAGES;
+  static_assert(S >= 4, "the ring holds tiles i-1 .. i+2 and the one being loaded");
+  __shared__ __attribute__((aligned(1024))) char lds[S][2][QT * ROWB];  // [stage][Q | dO]
+  __shared__ __attribute__((aligned(16))) float lds_ld[S][4][2 * QT];   // [stage][wave][lse2 | delta]
+  __shared__ int s_item;
   const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // One workgroup per (kv head, key tile) walking the group's query heads, or,
-  // with `partial`, one per (query head, key tile) writing float32 partials
-  // that fa128_dkdv_reduce_kernel sums over the group.
+  // Work items: (kv head, key tile), each walking the group's query heads,
+  // or, with `partial`, (query head, key tile) writing float32 partials that
+  // fa128_dkdv_reduce_kernel sums over the group.  Items differ by more than
+  // 30x in work (the first key tiles of a segment see most of its queries)
+  // and the hardware hands workgroups to CUs round-robin, so the grid is one
+  // workgroup per CU taking items from a counter, heaviest first.  An item's
+  // results do not depend on which workgroup takes it.
   const int group = nq / nkv;
-  const int hk = partial ? (int)blockIdx.x / group : (int)blockIdx.x;
-  const int h_first = partial ? (int)blockIdx.x : hk * group;
+  const int heads = partial ? nq : nkv;
+  const int n_work = heads * n_tiles;
+  for (;;) {
+  if (threadIdx.x == 0) s_item = atomicAdd(counter, 1);
+  __syncthreads();
+  const int item = __builtin_amdgcn_readfirstlane(s_item);
+  __syncthreads();  // every lane has read s_item before the next item overwrites it
+  if (item >= n_work) break;
+  const int bx = item % heads, by = item / heads;
+  const int hk = partial ? bx / group : bx;
+  const int h_first = partial ? bx : hk * group;
   const int h_end = partial ? h_first + 1 : (hk + 1) * group;
-  const int t = n_tiles - 1 - (int)blockIdx.y;
+  const int t = n_tiles - 1 - by;
   const int seg = tiles[2 * t], start = tiles[2 * t + 1];
   const int64_t base = bounds[seg];
   const int L = (int)((bounds[seg + 1] - base) / 2);
@@ -393,101 +456,266 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const int ki = start + wave * 32 + col;
   const bool k_valid = ki < k1;
   const int64_t ldq = (int64_t)nq * HD, ldk = (int64_t)nkv * HD;
+  const uint32_t qrow_bytes = (uint32_t)(ldq * 2);
   const float c = scale * FA_LOG2E;
 
-  // K of this wavefront's 32 keys as B operands in registers (lane = key, 8 of
-  // head_dim per k step); V of the tile's 128 keys in LDS (same operand reads).
-  bf16x8_t kf[HD / 16];
-  {
-    const int64_t kr = base + (k_valid ? ki : k1 - 1);
-#pragma unroll
-    for (int kk = 0; kk < HD / 16; ++kk) kf[kk] = load_frag(k + kr * ldk + hk * HD + kk * 16 + half * 8);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dload4(lds_v, wave * 32 + i * 4, v + hk * HD, ldv, base + start, base + k1 - 1, lane);
-  }
   f32x16_t dkacc[HD / 32], dvacc[HD / 32];
 #pragma unroll
-  for (int i = 0; i < HD / 32; ++i) { dkacc[i] = zero16(); dvacc[i] = zero16(); }
+  for (int i = 0; i < HD / 32; ++i) {
+    mfma_acc_zero(dkacc[i]);
+    mfma_acc_zero(dvacc[i]);
+  }
 
   const Interval2 mine = queries_of_key(ki, k_valid, L, B);
   const Interval2 R = query_ranges(start, k1, L, B);
   // queries allowed for every key of the tile
   const Interval2 first = queries_of_key(start, true, L, B), last = queries_of_key(k1 - 1, true, L, B);
-  auto issue = [&](int stg, int hh, int rr, int qq) {
-    const int64_t gmax = base + (rr ? R.hi1 : R.hi0) - 1;
+  const bool whole = k1 - start == 128;
+
+  // Cursor (query head h, range r, first row q0) over the query tiles that see
+  // this key tile; `more` turns false past the last one.
+  // Cursor (query head h, range r, first row q0) over the query tiles that see
+  // this key tile, head by head, range 0 then range 1; `more` turns false
+  // past the last one.  Branch-free: an exhausted range moves to range 1 of
+  // the same head, or to the first range of the next head.
+  const bool has1 = R.lo1 < R.hi1;
+  const int r_first = R.lo0 < R.hi0 ? 0 : 1, q_first = r_first ? R.lo1 : R.lo0;
+  int h = h_first, r = r_first, q0 = q_first;
+  bool more = r_first == 0 || has1;
+  if (more) {
+    // (th, tr, tq): the tile last taken from the cursor.  Past the end it is
+    // loaded again, into a stage that is never read, so that every iteration
+    // issues DK_LOADS loads and the vmcnt waits stay fixed.
+    int th = h, tr = r, tq = q0;
+    // Tile descriptors of tiles i .. i+S-1: bit 0 a real tile, bit 1 every key
+    // of the key tile sees every row, bit 2 the range; and the first row.
+    int fl[S], fr[S];
+    auto take = [&](int& f, int& row) {
+      f = 0;
+      if (more) {
+        th = h; tr = r; tq = q0;
+        const bool full = whole && q0 >= (r ? last.lo1 : last.lo0) &&
+                          q0 + QT <= (r ? first.hi1 : first.hi0);
+        f = 1 | (full ? 2 : 0) | (r << 2);
+        q0 += QT;
+        if (q0 >= (r ? R.hi1 : R.hi0)) {
+          const bool to1 = r == 0 && has1;
+          h = to1 ? h : h + 1;
+          q0 = to1 ? R.lo1 : q_first;
+          r = to1 ? 1 : r_first;
+          more = h < h_end;
+        }
+      }
+      row = tq;
+    };
+    // One tile's direct loads: this wavefront's 8 rows of Q and of dO (rows
+    // past the range re-read its last row; their products are masked) and its
+    // own copy of the tile's 32 lse2 and 32 delta values.  Global addresses are
+    // a wave-uniform base plus a 32-bit lane offset; M0 (the LDS destination)
+    // is saved once around the five loads.
+    const uint32_t lds0 = lds_addr(lds);
+    const uint32_t lse_dist = (uint32_t)((const char*)lse2 - (const char*)delta);
+    const int rows0 = wave * 8 + (lane >> 4), rows1 = rows0 + 4;
+    const uint32_t chunk0 = (uint32_t)((lane & 15) ^ swz(rows0)) << 4;
+    const uint32_t chunk1 = (uint32_t)((lane & 15) ^ swz(rows1)) << 4;
+    auto issue = [&](int st) {
+      const int rel_max = (tr ? R.hi1 : R.hi0) - 1 - tq;
+      const int64_t row0 = base + tq;
+      const bf16_t* qb = q + row0 * ldq + th * HD;
+      const bf16_t* db = dout + row0 * ldq + th * HD;
+      const float* lb = delta + (int64_t)th * N + row0;
+      const uint32_t off0 = (uint32_t)(rows0 < rel_max ? rows0 : rel_max) * qrow_bytes + chunk0;
+      const uint32_t off1 = (uint32_t)(rows1 < rel_max ? rows1 : rel_max) * qrow_bytes + chunk1;
+      const uint32_t offl = (uint32_t)(col < rel_max ? col : rel_max) * 4u + (half ? 0u : lse_dist);
+      const uint32_t lq = lds0 + (uint32_t)st * (2 * QT * ROWB) + (uint32_t)wave * (8 * ROWB);
+      const uint32_t ll = lds_addr(lds_ld) + (uint32_t)(st * 4 + wave) * (2 * QT * 4);
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %[sv], m0\n\t"
+          "s_mov_b32 m0, %[lq]\n\t"
+          "global_load_lds_dwordx4 %[o0], %[qb]\n\t"
+          "s_add_u32 m0, %[lq], %[dq]\n\t"
+          "global_load_lds_dwordx4 %[o0], %[db]\n\t"
+          "s_add_u32 m0, %[lq], %[r4]\n\t"
+          "global_load_lds_dwordx4 %[o1], %[qb]\n\t"
+          "s_add_u32 m0, %[lq], %[d4]\n\t"
+          "global_load_lds_dwordx4 %[o1], %[db]\n\t"
+          "s_mov_b32 m0, %[ll]\n\t"
+          "global_load_lds_dword %[ol], %[lb]\n\t"
+          "s_mov_b32 m0, %[sv]"
+          : [sv] "=&s"(saved)
+          : [lq] "s"(lq), [ll] "s"(ll), [o0] "v"(off0), [o1] "v"(off1), [ol] "v"(offl),
+            [qb] "s"(qb), [db] "s"(db), [lb] "s"(lb), [dq] "n"(QT * ROWB), [r4] "n"(4 * ROWB),
+            [d4] "n"(QT * ROWB + 4 * ROWB)
+          : "memory");
+    };
+    // lse2 and delta of the two elements of S that group kk of the VALU work
+    // handles (elements 2kk, 2kk+1 belong to query rows
+    // 8 (kk / 2) + 4 half + 2 (kk % 2) + {0, 1} of the tile).
+    auto read_pair = [&](int st, int kk, float2& ls, float2& dl) {
+      const float* p = lds_ld[st][wave] + 8 * (kk >> 1) + 4 * half + 2 * (kk & 1);
+      ls = *reinterpret_cast<const float2*>(p);
+      dl = *reinterpret_cast<const float2*>(p + QT);
+    };
+
+    // Prologue: tiles 0 .. S-2 into stages 0 .. S-2; K and V fragments.
+    bf16x8_t kf[HD / 16], vf[HD / 16];
+    take(fl[0], fr[0]);
+    issue(0);
+    {
+      const int64_t kr = base + (k_valid ? ki : k1 - 1);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r0 = wave * 8 + i * 4;
-      dload4(lds[stg][0], r0, q + hh * HD, ldq, base + qq, gmax, lane);
-      dload4(lds[stg][1], r0, dout + hh * HD, ldq, base + qq, gmax, lane);
+      for (int kk = 0; kk < HD / 16; ++kk) {
+        kf[kk] = load_frag(k + kr * ldk + hk * HD + kk * 16 + half * 8);
+        vf[kk] = load_frag(v + kr * ldv + hk * HD + kk * 16 + half * 8);
+      }
     }
-    if (wave == 0) {  // lse2 (lanes 0-31) and delta (lanes 32-63) of the tile's rows
-      int64_t row = base + qq + col;
-      row = row < gmax ? row : gmax;
-      const float* src = (half ? delta : lse2) + (int64_t)hh * N + row;
-      dma4_v(src, lds_addr(lds_ld[stg]));
+    __builtin_amdgcn_s_waitcnt(0);  // K, V and this wavefront's share of tile 0
+#pragma unroll
+    for (int s = 1; s < S - 1; ++s) {
+      take(fl[s], fr[s]);
+      issue(s);
     }
-  };
-  int r = 0, q0 = 0, h = h_first;
-  bool more = range_first(R, r, q0);
-  __builtin_amdgcn_s_waitcnt(0);
-  if (more) issue(0, h, r, q0);
-  int stg = 0;
-  while (more) {
-    wait_vmem();
-    __syncthreads();
-    const int cur_q0 = q0;
-    const int qlo = r ? mine.lo1 : mine.lo0, qhi = r ? mine.hi1 : mine.hi0;
-    const bool full = k1 - start == 128 && cur_q0 >= (r ? last.lo1 : last.lo0) &&
-                      cur_q0 + QT <= (r ? first.hi1 : first.hi0);
-    more = range_next(R, QT, r, q0);
-    if (!more && h + 1 < h_end) {
-      ++h;
-      more = range_first(R, r, q0);
-    }
-    if (more) issue(stg ^ 1, h, r, q0);
-    const char* qt = lds[stg][0];
-    const char* dt = lds[stg][1];
-    f32x16_t sacc = zero16(), pacc = zero16();
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DK_LOADS * (S - 3)) : "memory");
+    f32x16_t sacc, pacc;
 #pragma unroll
     for (int kk = 0; kk < HD / 16; ++kk) {
-      sacc = mfma(row_frag(qt, col, kk * 2 + half), kf[kk], sacc);
-      pacc = mfma(row_frag(dt, col, kk * 2 + half), row_frag(lds_v, wave * 32 + col, kk * 2 + half), pacc);
-    }
-    // S[q, key]: lane owns the key column; element e is query row 8(e/4) + 4*half + e%4.
-    // Query qq is allowed iff (unsigned)(qq - qlo) < qhi - qlo; for a tile every
-    // key sees whole the bound is set so that the test always passes (one add,
-    // compare and select per element, no second copy of the loop body).
-    const int q_off = full ? 0 : cur_q0 + half * 4 - qlo;
-    const unsigned q_width = full ? 0xffffffffu : (unsigned)(qhi - qlo);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int qo = j * 8 + half * 4;
-      const float4 ls = *reinterpret_cast<const float4*>(&lds_ld[stg][qo]);
-      const float4 dl = *reinterpret_cast<const float4*>(&lds_ld[stg][QT + qo]);
-      const float lsv[4] = {ls.x, ls.y, ls.z, ls.w}, dlv[4] = {dl.x, dl.y, dl.z, dl.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = j * 4 + i;
-        float p = fast_exp2(fmaf(sacc[e], c, -lsv[i]));
-        if ((unsigned)(q_off + j * 8 + i) >= q_width) p = 0.f;
-        sacc[e] = p;
-        pacc[e] = p * (pacc[e] - dlv[i]);
+      const bf16x8_t a = row_frag(lds[0][0], col, kk * 2 + half);
+      const bf16x8_t b = row_frag(lds[0][1], col, kk * 2 + half);
+      if (kk == 0) {
+        mfma_v0(sacc, a, kf[kk]);
+        mfma_v0(pacc, b, vf[kk]);
+      } else {
+        mfma_v(sacc, a, kf[kk]);
+        mfma_v(pacc, b, vf[kk]);
       }
     }
+    bf16x8_t aq[HD / 16], ad[HD / 16];  // S / dP A operands of the next tile
+    aq[0] = row_frag(lds[1][0], col, half);
+    ad[0] = row_frag(lds[1][1], col, half);
+    aq[1] = row_frag(lds[1][0], col, 2 + half);
+    ad[1] = row_frag(lds[1][1], col, 2 + half);
+    float2 lsa, dla;
+    read_pair(0, 0, lsa, dla);
+    mfma_acc_settle();  // the first VALU group reads sacc / pacc
+    __builtin_amdgcn_sched_barrier(0);
+
+    int cs = 0;  // stage of tile i
+    // One iteration: S / dP of tile i in (sacc, pacc) and the lse2 / delta of
+    // its first VALU group in (ls0, dl0); leaves tile i+1's in (sn, pn) and
+    // (ls1, dl1).  Returns false after the last tile.  The loop alternates
+    // the two register sets.
+    auto step = [&](f32x16_t& sacc, f32x16_t& pacc, f32x16_t& sn, f32x16_t& pn, float2& ls0,
+                    float2& dl0, float2& ls1, float2& dl1) -> bool {
+      const int ns = cs + 1 == S ? 0 : cs + 1;
+      const int ns2 = ns + 1 == S ? 0 : ns + 1;
+      const int ls_stage = cs == 0 ? S - 1 : cs - 1;  // stage of tile i-1 = i+S-1
+      const char* qc = lds[cs][0];
+      const char* dc = lds[cs][1];
+      uint32_t pw[8], sw[8];
+      bf16x8_t tv[8], tk[8];  // dO^T / Q^T fragments of dV / dK, index st * 4 + db
+
+      // A: S, dP of tile i+1; P, dS of tile i.
+      auto block_a = [&](auto masked_tag) {
+        constexpr bool masked = decltype(masked_tag)::value;
+        int q_off = 0;
+        unsigned q_width = 0;
+        if constexpr (masked) {
+          const int rr = (fl[0] >> 2) & 1;
+          const int qlo = rr ? mine.lo1 : mine.lo0, qhi = rr ? mine.hi1 : mine.hi0;
+          q_off = fr[0] + half * 4 - qlo;
+          q_width = (unsigned)(qhi - qlo);
+        }
+        const char* qn = lds[ns][0];
+        const char* dn = lds[ns][1];
+        float2 lsg = ls0, dlg = dl0;
 #pragma unroll
-    for (int st = 0; st < QT / 16; ++st) {
-      const bf16x8_t pb = pack8(sacc, st * 8);
-      const bf16x8_t sb = pack8(pacc, st * 8);
+        for (int kk = 0; kk < HD / 16; ++kk) {
+          float2 lsn, dln;
+          if (kk + 1 < HD / 16) read_pair(cs, kk + 1, lsn, dln);
+          if (kk + 2 < HD / 16) aq[kk + 2] = row_frag(qn, col, (kk + 2) * 2 + half);
+          if (kk == 0) mfma_v0(sn, aq[kk], kf[kk]);
+          else mfma_v(sn, aq[kk], kf[kk]);
 #pragma unroll
-      for (int db = 0; db < HD / 32; ++db) {
-        dvacc[db] = mfma(tr_frag(dt, st * 16, db * 32, lane), pb, dvacc[db]);
-        dkacc[db] = mfma(tr_frag(qt, st * 16, db * 32, lane), sb, dkacc[db]);
+          for (int u = 0; u < 2; ++u) {
+            const int e = 2 * kk + u;
+            float p = fast_exp2(fmaf(sacc[e], c, -(u ? lsg.y : lsg.x)));
+            if constexpr (masked)
+              if ((unsigned)(q_off + (e >> 2) * 8 + (e & 3)) >= q_width) p = 0.f;
+            sacc[e] = p;
+            pacc[e] = p * (pacc[e] - (u ? dlg.y : dlg.x));
+            if (u == 0 && kk + 2 < HD / 16) ad[kk + 2] = row_frag(dn, col, (kk + 2) * 2 + half);
+            if (u == 0 && kk == 0) mfma_v0(pn, ad[kk], vf[kk]);
+            else if (u == 0) mfma_v(pn, ad[kk], vf[kk]);
+          }
+          pw[kk] = pack2(sacc[2 * kk], sacc[2 * kk + 1]);
+          sw[kk] = pack2(pacc[2 * kk], pacc[2 * kk + 1]);
+          if (kk == HD / 16 - 1) {
+            tv[0] = tr_frag(dc, 0, 0, lane);
+            tk[0] = tr_frag(qc, 0, 0, lane);
+            tv[1] = tr_frag(dc, 0, 32, lane);
+            tk[1] = tr_frag(qc, 0, 32, lane);
+          }
+          lsg = lsn;
+          dlg = dln;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      if (fl[0] & 2) block_a(std::false_type{});
+      else block_a(std::true_type{});
+
+      // Tile i+2 has landed (this wavefront's loads, then every wavefront's);
+      // the stage of tile i-1 takes tile i+S-1.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DK_LOADS * (S - 4))
+                   : "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      take(fl[S - 1], fr[S - 1]);
+      issue(ls_stage);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // B: dV, dK of tile i; first operands of tile i+2, first lse2 / delta
+      // of tile i+1.
+      const bf16x8_t pb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3])),
+                              __builtin_bit_cast(bf16x8_t, make_uint4(pw[4], pw[5], pw[6], pw[7]))};
+      const bf16x8_t sb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(sw[0], sw[1], sw[2], sw[3])),
+                              __builtin_bit_cast(bf16x8_t, make_uint4(sw[4], sw[5], sw[6], sw[7]))};
+      const char* q2 = lds[ns2][0];
+      const char* d2 = lds[ns2][1];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        if (m + 2 < 8) {
+          tv[m + 2] = tr_frag(dc, ((m + 2) >> 2) * 16, ((m + 2) & 3) * 32, lane);
+          tk[m + 2] = tr_frag(qc, ((m + 2) >> 2) * 16, ((m + 2) & 3) * 32, lane);
+        }
+        mfma_acc(dvacc[m & 3], tv[m], pb[m >> 2]);
+        mfma_acc(dkacc[m & 3], tk[m], sb[m >> 2]);
+        if (m == 5) read_pair(ns, 0, ls1, dl1);
+        if (m == 6) {
+          aq[0] = row_frag(q2, col, half);
+          ad[0] = row_frag(d2, col, half);
+        }
+        if (m == 7) {
+          aq[1] = row_frag(q2, col, 2 + half);
+          ad[1] = row_frag(d2, col, 2 + half);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (!(fl[1] & 1)) return false;
+#pragma unroll
+      for (int s = 0; s < S - 1; ++s) {
+        fl[s] = fl[s + 1];
+        fr[s] = fr[s + 1];
+      }
+      cs = ns;
+      return true;
+    };
+    f32x16_t sn, pn;
+    float2 lsb, dlb;
+    while (step(sacc, pacc, sn, pn, lsa, dla, lsb, dlb) && step(sn, pn, sacc, pacc, lsb, dlb, lsa, dla)) {
     }
-    stg ^= 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  mfma_acc_settle();  // the stores below read the accumulators
   if (k_valid && partial) {
     // [2][group][N][nkv * HD]: dK partials, then dV partials
     const int64_t plane = (int64_t)group * N * nkv * HD;
@@ -519,6 +747,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
             make_uint2(pack2(dvacc[db][j * 4], dvacc[db][j * 4 + 1]),
                        pack2(dvacc[db][j * 4 + 2], dvacc[db][j * 4 + 3]));
       }
+  }
   }
 }
 
@@ -556,11 +785,26 @@ static bool dkdv_head_split(int64_t n_tiles, int nq, int nkv) {
   return nq > nkv && (int64_t)nkv * n_tiles < 1024;
 }
 
+// delta [nq][N], lse * log2(e) [nq][N], the dK/dV work counter (one int in a
+// 64-float slot), then (head split) the float32 dK/dV partials
+// [2][group][N][nkv*128].
+constexpr int64_t COUNTER_SLOT = 64;
 int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles) {
-  // delta [nq][N], lse * log2(e) [nq][N], then (head split) the float32 dK/dV
-  // partials [2][group][N][nkv*128]
-  const int64_t delta = 2 * N * nq;
-  return dkdv_head_split(n_tiles, nq, nkv) ? delta + 2 * N * (int64_t)nq * HD : delta;
+  const int64_t head = 2 * N * nq + COUNTER_SLOT;
+  return dkdv_head_split(n_tiles, nq, nkv) ? head + 2 * N * (int64_t)nq * HD : head;
+}
+
+// Compute units of the current device (the dK/dV grid is one workgroup per CU).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev]) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
 }
 int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
@@ -578,21 +822,21 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
                      float scale, hipStream_t st) {
   // the dQ pass writes delta and lse * log2(e), which the dK/dV pass reads
   // (stream order)
+  // (and zeroes the dK/dV work counter)
+  int* counter = reinterpret_cast<int*>(delta + 2 * N * nq);
   fa128_dq_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
-      q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale);
+      q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale, counter);
   const float* lse2 = delta + N * nq;
-  if (dkdv_head_split(n_tiles, nq, nkv)) {
-    float* partial = delta + 2 * N * nq;
-    fa128_dkdv_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
-        q, k, v, ldv, lse2, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, partial, N,
-        nq, nkv, B, scale);
+  const bool split = dkdv_head_split(n_tiles, nq, nkv);
+  const int64_t items = (split ? nq : nkv) * n_tiles;
+  const unsigned grid = (unsigned)(items < device_cus() ? items : device_cus());
+  float* partial = split ? delta + 2 * N * nq + COUNTER_SLOT : nullptr;
+  fa128_dkdv_kernel<<<grid, 256, 0, st>>>(q, k, v, ldv, lse2, delta, dout, bounds, tiles,
+                                          (int)n_tiles, dk, dv, lddv, partial, N, nq, nkv, B,
+                                          scale, counter);
+  if (split)
     fa128_dkdv_reduce_kernel<<<ceil_div_u(2 * N * nkv * HD / 8, 256), 256, 0, st>>>(
         partial, nq / nkv, N, nkv, dk, dv, lddv);
-  } else {
-    fa128_dkdv_kernel<<<dim3((unsigned)nkv, (unsigned)n_tiles), 256, 0, st>>>(
-        q, k, v, ldv, lse2, delta, dout, bounds, tiles, (int)n_tiles, dk, dv, lddv, nullptr, N,
-        nq, nkv, B, scale);
-  }
   ALODLM_CHECK_LAUNCH("attention_bwd_fa128");
   return ALODLM_OK;
 }

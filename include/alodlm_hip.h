@@ -219,8 +219,9 @@ int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t
  * bwd: dq [rows, nq*dh], dk [rows, nkv*dh], dv (stride lddv) from do.
  * `workspace` holds alodlm_attention_bwd_workspace(rows, nq, nkv, dh, n_tiles)
  * floats (delta per head and row; for head_dim 128 also lse * log2(e) per
- * head and row, and with few key tiles per kv head float32 dK/dV partials
- * per query head).
+ * head and row, the dK/dV pass's work counter, and with few key tiles per kv
+ * head float32 dK/dV partials per query head).  Calls that share a workspace
+ * must not overlap.
  * ------------------------------------------------------------------------ */
 int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const int64_t* bounds, const int32_t* row_segment,
