@@ -411,6 +411,12 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 // ---------------------------------------------------------------------------
 constexpr int DK_STAGES = 5;
 constexpr int DK_LOADS = 5;  // direct-load instructions per wavefront per query tile
+#ifndef DK_AQD
+#define DK_AQD 2  // LDS reads of S / dP operands this many MFMA groups ahead
+#endif
+#ifndef DK_TRD
+#define DK_TRD 2  // LDS reads of dV / dK operands this many MFMA groups ahead
+#endif
 
 __global__ void __launch_bounds__(256, 1)
 fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
@@ -591,10 +597,11 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       }
     }
     bf16x8_t aq[HD / 16], ad[HD / 16];  // S / dP A operands of the next tile
-    aq[0] = row_frag(lds[1][0], col, half);
-    ad[0] = row_frag(lds[1][1], col, half);
-    aq[1] = row_frag(lds[1][0], col, 2 + half);
-    ad[1] = row_frag(lds[1][1], col, 2 + half);
+#pragma unroll
+    for (int kk = 0; kk < DK_AQD; ++kk) {
+      aq[kk] = row_frag(lds[1][0], col, 2 * kk + half);
+      ad[kk] = row_frag(lds[1][1], col, 2 * kk + half);
+    }
     float2 lsa, dla;
     read_pair(0, 0, lsa, dla);
     mfma_acc_settle();  // the first VALU group reads sacc / pacc
@@ -633,7 +640,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
         for (int kk = 0; kk < HD / 16; ++kk) {
           float2 lsn, dln;
           if (kk + 1 < HD / 16) read_pair(cs, kk + 1, lsn, dln);
-          if (kk + 2 < HD / 16) aq[kk + 2] = row_frag(qn, col, (kk + 2) * 2 + half);
+          if (kk + DK_AQD < HD / 16) aq[kk + DK_AQD] = row_frag(qn, col, (kk + DK_AQD) * 2 + half);
           if (kk == 0) mfma_v0(sn, aq[kk], kf[kk]);
           else mfma_v(sn, aq[kk], kf[kk]);
 #pragma unroll
@@ -644,17 +651,19 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
               if ((unsigned)(q_off + (e >> 2) * 8 + (e & 3)) >= q_width) p = 0.f;
             sacc[e] = p;
             pacc[e] = p * (pacc[e] - (u ? dlg.y : dlg.x));
-            if (u == 0 && kk + 2 < HD / 16) ad[kk + 2] = row_frag(dn, col, (kk + 2) * 2 + half);
+            if (u == 0 && kk + DK_AQD < HD / 16)
+              ad[kk + DK_AQD] = row_frag(dn, col, (kk + DK_AQD) * 2 + half);
             if (u == 0 && kk == 0) mfma_v0(pn, ad[kk], vf[kk]);
             else if (u == 0) mfma_v(pn, ad[kk], vf[kk]);
           }
           pw[kk] = pack2(sacc[2 * kk], sacc[2 * kk + 1]);
           sw[kk] = pack2(pacc[2 * kk], pacc[2 * kk + 1]);
           if (kk == HD / 16 - 1) {
-            tv[0] = tr_frag(dc, 0, 0, lane);
-            tk[0] = tr_frag(qc, 0, 0, lane);
-            tv[1] = tr_frag(dc, 0, 32, lane);
-            tk[1] = tr_frag(qc, 0, 32, lane);
+#pragma unroll
+            for (int m = 0; m < DK_TRD; ++m) {
+              tv[m] = tr_frag(dc, (m >> 2) * 16, (m & 3) * 32, lane);
+              tk[m] = tr_frag(qc, (m >> 2) * 16, (m & 3) * 32, lane);
+            }
           }
           lsg = lsn;
           dlg = dln;
@@ -683,20 +692,17 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       const char* d2 = lds[ns2][1];
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
-        if (m + 2 < 8) {
-          tv[m + 2] = tr_frag(dc, ((m + 2) >> 2) * 16, ((m + 2) & 3) * 32, lane);
-          tk[m + 2] = tr_frag(qc, ((m + 2) >> 2) * 16, ((m + 2) & 3) * 32, lane);
+        if (m + DK_TRD < 8) {
+          tv[m + DK_TRD] = tr_frag(dc, ((m + DK_TRD) >> 2) * 16, ((m + DK_TRD) & 3) * 32, lane);
+          tk[m + DK_TRD] = tr_frag(qc, ((m + DK_TRD) >> 2) * 16, ((m + DK_TRD) & 3) * 32, lane);
         }
         mfma_acc(dvacc[m & 3], tv[m], pb[m >> 2]);
         mfma_acc(dkacc[m & 3], tk[m], sb[m >> 2]);
         if (m == 5) read_pair(ns, 0, ls1, dl1);
-        if (m == 6) {
-          aq[0] = row_frag(q2, col, half);
-          ad[0] = row_frag(d2, col, half);
-        }
-        if (m == 7) {
-          aq[1] = row_frag(q2, col, 2 + half);
-          ad[1] = row_frag(d2, col, 2 + half);
+        // first operands of tile i+2, one k step per group from group 8 - DK_AQD
+        if (m >= 8 - DK_AQD) {
+          aq[m - (8 - DK_AQD)] = row_frag(q2, col, 2 * (m - (8 - DK_AQD)) + half);
+          ad[m - (8 - DK_AQD)] = row_frag(d2, col, 2 * (m - (8 - DK_AQD)) + half);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
