@@ -33,6 +33,16 @@
 // lowering the clock), so the loop is shaped for energy per FLOP as much as
 // for latency: fewer LDS bytes per MFMA and no redundant instructions.
 //
+// With one wave per SIMD every instruction of the loop takes an issue slot
+// beside the MFMAs, so the loop carries no address arithmetic: the tile loop
+// is unrolled over the STAGES stages of the ring, every fragment read is a
+// per-lane base register plus an immediate (stage, k step and 32-row block
+// are compile-time), every direct load sets M0 with one scalar add from a
+// per-wave base, and the two tile origins advance by one 64-bit add per
+// stage.  Per 32 MFMAs a stage issues 24 LDS reads, 8 direct loads and about
+// 20 scalar instructions (84 with the addresses computed in the loop, which
+// measured 3-8 % slower on every product of the step).
+//
 // Workgroup -> tile order: consecutive workgroups land on different XCDs, so
 // the tile sequence is dealt out in contiguous chunks per XCD, then swept in
 // groups of 8 tile rows.
@@ -49,30 +59,39 @@ namespace {
 constexpr int TB = 256;              // block tile (m and n)
 constexpr int KMIN = 32;             // k multiple every product must have
 
-// One direct-load instruction: 16 bytes per lane from base + off into the
-// 16-byte slot lane of `lds` (wave-uniform).
-__device__ __forceinline__ void dma16(const char* base, uint32_t off, char* lds) {
-  dma16_s(base, off, lds_addr(lds));
+// One direct-load instruction: 16 bytes per lane from the wave-uniform tile
+// origin `o` plus the lane's 32-bit offset, into the 16-byte slot lane of the
+// LDS byte address m0v (wave-uniform).  M0 is an operand of the instruction,
+// so the compiler sets it (one scalar add from a per-wave base) and knows its
+// value; the load itself is not visible to the compiler (lds_dma.h).
+__device__ __forceinline__ void dma16_m0(const char* o, uint32_t off, uint32_t m0v) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(o), "{m0}"(m0v) : "memory");
 }
 
 // Operand staging.  init() fixes this wave's lane offsets (relative to the
 // tile origin, clamped so that rows / columns past the operand re-read its
-// last valid row / chunk: they only feed outputs that are never stored);
-// issue() loads this wave's instructions of one stage; frag() reads one MFMA
-// operand.  Instruction j of a stage is issued by wave j % NW.
+// last valid row / chunk: they only feed outputs that are never stored) and
+// the byte step from one k tile's origin to the next; init_frag() fixes the
+// lane's fragment offsets within a stage, so that every fragment read is one
+// base register plus an immediate (stage, k step and 32-row block are
+// compile-time in the unrolled loop).  Instruction j of a stage is issued by
+// wave j % NW into the 1024-byte slot j of the operand's stage.
 template <bool KMAJ, int NW, int KD> struct Opnd;
 
 // P[rows][ld], k contiguous: tile [256 rows][KD k], rows of 2*KD bytes
 // (CH = KD/8 chunks), chunk' = chunk ^ f(row) with f(row) = (row / (16/CH)) % CH,
 // so the 16 rows of a fragment read cover 16 distinct 4-bank groups.
 template <int NW, int KD> struct Opnd<true, NW, KD> {
+  static_assert(KD == 32 || KD == 64, "f(row) is invariant under +32 rows for these depths");
   static constexpr int CH = KD / 8, RB = 2 * KD, RPI = 1024 / RB;  // rows per instruction
-  static constexpr int NINST = TB / RPI, PER = NINST / NW;
+  static constexpr int NINST = TB / RPI, PER = NINST / NW, OPB = TB * KD * 2;
   uint32_t off[PER];
-  int64_t ld;
+  uint32_t fo[KD / 16];  // fragment offset of 32-row block 0, per k step
+  int64_t ld, step;
   static __device__ __forceinline__ int f(int row) { return (row / (16 / CH)) % CH; }
   __device__ __forceinline__ void init(int64_t ld_, int64_t rows_left, int wave, int lane) {
     ld = ld_;
+    step = 2 * KD;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int r = RPI * (wave + NW * i) + lane / CH;
@@ -81,33 +100,33 @@ template <int NW, int KD> struct Opnd<true, NW, KD> {
       off[i] = (uint32_t)((rc * ld + 8 * c) * 2);
     }
   }
+  // fragments of rows r0 + 32 * idx + lane % 32 (r0 a multiple of 32) of the
+  // operand's stages, which start `region` bytes into the LDS array
+  __device__ __forceinline__ void init_frag(int r0, int lane, int region) {
+    const int row = r0 + (lane & 31), half = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < KD / 16; ++ks)
+      fo[ks] = (uint32_t)(region + row * RB + (((2 * ks + half) ^ f(row)) << 4));
+  }
   // tile origin: rows r0.., k from k0
   __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
     return reinterpret_cast<const char*>(P + r0 * ld + k0);
   }
-  __device__ __forceinline__ void issue(const char* o, char* stage, int wave) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
-  }
-  // instruction i (< PER) of this wave's share of a stage
-  __device__ __forceinline__ void issue_one(const char* o, char* stage, int wave, int i) const {
-    dma16(o, off[i], stage + (wave + NW * i) * 1024);
-  }
-  // row `row` (0..255) of the tile, k step ks, 8 k values at 8*half
-  static __device__ __forceinline__ bf16x8_t frag(const char* stage, int row, int ks, int half, int lane) {
-    (void)lane;
-    const int c = (2 * ks + half) ^ f(row);
-    return *reinterpret_cast<const bf16x8_t*>(stage + row * RB + c * 16);
+  // 32-row block idx, k step ks, from stage `stage` (lds: the LDS array)
+  __device__ __forceinline__ bf16x8_t frag(const char* lds, int stage, int ks, int idx) const {
+    return *reinterpret_cast<const bf16x8_t*>(lds + fo[ks] + (stage * OPB + idx * 32 * RB));
   }
 };
 
 // P[k][ld], m/n contiguous: tile [KD k][256], 512-byte rows, chunk' = chunk ^ 4*(k & 3).
 template <int NW, int KD> struct Opnd<false, NW, KD> {
-  static constexpr int NINST = KD / 2, PER = NINST / NW;  // two k rows per instruction
+  static constexpr int NINST = KD / 2, PER = NINST / NW, OPB = TB * KD * 2;  // two k rows per instruction
   uint32_t off[PER];
-  int64_t ld;
+  uint32_t fo[4];  // fragment offset of k step 0, per 32-column block
+  int64_t ld, step;
   __device__ __forceinline__ void init(int64_t ld_, int64_t cols_left, int wave, int lane) {
     ld = ld_;
+    step = 2 * KD * ld;
     const int last_chunk = (int)((cols_left < TB ? cols_left : TB) / 8) - 1;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -118,24 +137,23 @@ template <int NW, int KD> struct Opnd<false, NW, KD> {
       off[i] = (uint32_t)((row * ld + 8 * c) * 2);
     }
   }
+  // transposed fragments of columns r0 + 32 * idx + lane % 32 (r0 a multiple of
+  // 32) of the operand's stages, which start `region` bytes into the LDS
+  // array: per 16 lanes, two ds_read_b64_tr_b16 of k rows 8 half + {0..3} and
+  // {4..7} (+ 16 ks)
+  __device__ __forceinline__ void init_frag(int r0, int lane, int region) {
+    const int s = lane & 15, g = (lane >> 4) & 1, half = lane >> 5;
+#pragma unroll
+    for (int idx = 0; idx < 4; ++idx) {
+      const int c = (((r0 >> 5) + idx) * 4 + 2 * g + ((s & 3) >> 1)) ^ (4 * (s >> 2));
+      fo[idx] = (uint32_t)(region + (8 * half + (s >> 2)) * 512 + c * 16 + (s & 1) * 8);
+    }
+  }
   __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
     return reinterpret_cast<const char*>(P + k0 * ld + r0);
   }
-  __device__ __forceinline__ void issue(const char* o, char* stage, int wave) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) dma16(o, off[i], stage + (wave + NW * i) * 1024);
-  }
-  // instruction i (< PER) of this wave's share of a stage
-  __device__ __forceinline__ void issue_one(const char* o, char* stage, int wave, int i) const {
-    dma16(o, off[i], stage + (wave + NW * i) * 1024);
-  }
-  // column `row` (0..255) of the tile, k step ks: two transposed reads of
-  // k rows 16ks + 8half + {0..3} and {4..7}
-  static __device__ __forceinline__ bf16x8_t frag(const char* stage, int row, int ks, int half, int lane) {
-    const int s = lane & 15, g = (lane >> 4) & 1;
-    const int kr = 16 * ks + 8 * half + (s >> 2);
-    const int c = ((row >> 5) * 4 + 2 * g + ((s & 3) >> 1)) ^ (4 * (s >> 2));
-    const char* p0 = stage + kr * 512 + c * 16 + (s & 1) * 8;
+  __device__ __forceinline__ bf16x8_t frag(const char* lds, int stage, int ks, int idx) const {
+    const char* p0 = lds + fo[idx] + (stage * OPB + ks * 16 * 512);
     const v4s_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4s_t*)p0);
     const v4s_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4s_t*)(p0 + 4 * 512));
     return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -155,7 +173,9 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   constexpr int WAVES_N = TB / WN;
   constexpr int OPB = TB * KD * 2;   // bytes of one operand's stage
   constexpr int KS = KD / 16;         // k steps per stage
-  __shared__ __attribute__((aligned(1024))) char lds[STAGES][2][OPB];
+  // [operand][stage][OPB]: the A stages, then the B stages, so that every
+  // fragment read is a base register plus an immediate below 64 KB
+  __shared__ __attribute__((aligned(1024))) char lds[2][STAGES][OPB];
 
   const int tiles_m = (int)((M + TB - 1) / TB), tiles_n = (int)((N + TB - 1) / TB);
   const int T = tiles_m * tiles_n;
@@ -184,16 +204,10 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   Opnd<BK, NW, KD> ob;
   oa.init(lda, M - m0, wave, lane);
   ob.init(ldb, N - n0, wave, lane);
-
-  // Tile tt into stage tt % STAGES.  Tiles past the end re-load the last
-  // tile into a stage that is never read, which keeps the vmcnt waits uniform.
-  auto issue = [&](int tt) {
-    const int live = tt < ntiles ? tt : ntiles - 1;
-    const int64_t k0 = kbeg + (int64_t)live * KD;
-    char* st = lds[tt % STAGES][0];
-    oa.issue(oa.origin(A, m0, k0), st, wave);
-    ob.issue(ob.origin(B, n0, k0), st + OPB, wave);
-  };
+  oa.init_frag(wm * WM, lane, 0);
+  ob.init_frag(wn * WN, lane, STAGES * OPB);
+  (void)half;
+  (void)col;
 
   f32x16_t acc[FI][FJ];
 #pragma unroll
@@ -217,63 +231,91 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   // (tile tt+1 must have landed): whole later stages plus this tile's early ones
   constexpr int VM_LOOP = STAGES >= 3 ? (STAGES - 3) * PL + DPRE : 0;
   constexpr int VM_PRO = (STAGES - 2) * PL;
-  // load d of this wave's share of tile tt
-  auto dma_one = [&](int tt, int d) {
-    const int live = tt < ntiles ? tt : ntiles - 1;
-    const int64_t k0 = kbeg + (int64_t)live * KD;
-    char* st = lds[tt % STAGES][0];
-    if (d < PA) oa.issue_one(oa.origin(A, m0, k0), st, wave, d);
-    else ob.issue_one(ob.origin(B, n0, k0), st + OPB, wave, d - PA);
+
+  // Origins of the next k tile to load (wave-uniform), advanced once per
+  // stage.  Past the last tile they stay on it: its re-load goes to a stage
+  // that is never read, which keeps the vmcnt waits uniform.
+  const char* pa = oa.origin(A, m0, kbeg);
+  const char* pb = ob.origin(B, n0, kbeg);
+  int tl = 0;  // k tile at pa / pb
+  auto advance = [&]() {
+    if (tl + 1 < ntiles) {
+      pa += oa.step;
+      pb += ob.step;
+    }
+    ++tl;
   };
+  // LDS byte address of this wave's first 1024-byte slot
+  const uint32_t mw = lds_addr(lds) + (uint32_t)wave * 1024u;
+  // load d of this wave's share of a stage: the tile at pa / pb into stage sl
+  auto dma_one = [&](int sl, int d) {
+    if (d < PA) dma16_m0(pa, oa.off[d], mw + (uint32_t)(sl * OPB + NW * d * 1024));
+    else dma16_m0(pb, ob.off[d - PA], mw + (uint32_t)((STAGES + sl) * OPB + NW * (d - PA) * 1024));
+  };
+  const char* lds0 = lds[0][0];
   // fragment q of a k step, in the order the MFMAs consume them:
   // A0, B0, B1, B2, B3, A1, A2, A3
   auto read_one = [&](int set, int stage, int ks, int q) {
     const bool isa = q == 0 || q >= 5;
     const int idx = q == 0 ? 0 : (q >= 5 ? q - 4 : q - 1);
-    if (isa) fa[set][idx] = Opnd<AK, NW, KD>::frag(lds[stage][0], wm * WM + idx * 32 + col, ks, half, lane);
-    else fb[set][idx] = Opnd<BK, NW, KD>::frag(lds[stage][1], wn * WN + idx * 32 + col, ks, half, lane);
+    if (isa) fa[set][idx] = oa.frag(lds0, stage, ks, idx);
+    else fb[set][idx] = ob.frag(lds0, stage, ks, idx);
   };
   auto mma_one = [&](int set, int q) {
     const int i = q >> 2, j = q & 3;
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
   };
 
-  // Tile tt: k steps 0 .. KS-2, then the barrier that publishes tile tt+1
-  // (this wave's loads of it are waited for first), then k step KS-1, whose
-  // reads fetch tile tt+1's k step 0.  Every instruction group is fenced with
-  // sched_barrier so the compiler keeps this order.
+  // Tile tt (in stage s = tt % STAGES): k steps 0 .. KS-2, then the barrier
+  // that publishes tile tt+1 (this wave's loads of it are waited for first),
+  // then k step KS-1, whose reads fetch tile tt+1's k step 0; the loads of
+  // tile tt + STAGES - 1 go to the stage of tile tt - 1.  Every instruction
+  // group is fenced with sched_barrier so the compiler keeps this order.  The
+  // stage index is a compile-time constant in each unrolled copy.
+  auto tile_body = [&](const int s) {
+    const int sn = (s + 1) % STAGES, sl = (s + STAGES - 1) % STAGES;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks == KS - 1) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(VM_LOOP) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        mma_one(ks & 1, q);
+        if (q < 8) {
+          // after the last tile these reads fetch a stage that is never used
+          if (ks + 1 < KS) read_one((ks + 1) & 1, s, ks + 1, q);
+          else read_one(0, sn, 0, q);
+        } else {
+          const int slot = ks * 8 + (q - 8);
+#pragma unroll
+          for (int d = 0; d < PL; ++d)
+            if ((d * SLOTS) / PL == slot) dma_one(sl, d);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    advance();
+  };
+
   if (ntiles > 0) {  // (every split of an eligible product has k tiles)
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) issue(s);
+    for (int s = 0; s < STAGES - 1; ++s) {
+#pragma unroll
+      for (int d = 0; d < PL; ++d) dma_one(s, d);
+      advance();
+    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(VM_PRO) : "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 8; ++q) read_one(0, 0, 0, q);
-    for (int tt = 0; tt < ntiles; ++tt) {
-      const int stage = tt % STAGES;
-      const int nstage = (tt + 1) % STAGES;
+    for (int tt = 0; tt < ntiles;) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks == KS - 1) {
-          __builtin_amdgcn_sched_barrier(0);
-          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(VM_LOOP) : "memory");
-          __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          mma_one(ks & 1, q);
-          if (q < 8) {
-            // after the last tile these reads fetch a stage that is never used
-            if (ks + 1 < KS) read_one((ks + 1) & 1, stage, ks + 1, q);
-            else read_one(0, nstage, 0, q);
-          } else {
-            const int slot = ks * 8 + (q - 8);
-#pragma unroll
-            for (int d = 0; d < PL; ++d)
-              if ((d * SLOTS) / PL == slot) dma_one(tt + STAGES - 1, d);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int s = 0; s < STAGES; ++s) {
+        if (tt < ntiles) tile_body(s);
+        ++tt;
       }
     }
   }
