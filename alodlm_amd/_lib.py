@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -50,9 +50,10 @@ SIGNATURES = {
     "alodlm_gemm_workspace": [I64, I64, I64, I32, I32],
     "alodlm_gemm": [P, I64, I32, P, I64, I32, P, I64, P, I64, I64, I64, I64, F32, I32, I32, P, P],
     "alodlm_attention_fwd": [P, P, P, I64, P, P, P, I64, P, P, I64, I64, I64, I64, I64, I32, P],
-    "alodlm_attention_bwd_workspace": [I64, I64, I64, I64, I64],
-    "alodlm_attention_bwd": [P, P, P, I64, P, P, P, P, P, P, I64, P, P, P, I64, P, I64, I64, I64,
-                             I64, I64, I32, P],
+    "alodlm_attention_ds_blocks": [P, I64, I64, P],
+    "alodlm_attention_bwd_workspace": [I64, I64, I64, I64, I64, I64],
+    "alodlm_attention_bwd": [P, P, P, I64, P, P, P, P, P, P, I64, P, P, P, I64, P, P, I64, I64,
+                             I64, I64, I64, I64, I32, P],
     "alodlm_swiglu_fwd": [P, P, I64, I64, I32, P],
     "alodlm_swiglu_bwd": [P, P, P, P, I64, I64, I32, P],
     "alodlm_final_norm_gate": [P, P, P, P, P, I64, P, P, P, I64, I64, F32, I32, P],
@@ -93,6 +94,7 @@ _RESTYPE = {
     "alodlm_qknorm_rope_bwd_workspace": I64,
     "alodlm_gemm_workspace": I64,
     "alodlm_attention_bwd_workspace": I64,
+    "alodlm_attention_ds_blocks": I64,
     "alodlm_objective_workspace": I64,
     "alodlm_gate_bwd_workspace": I64,
 }

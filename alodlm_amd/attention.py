@@ -73,13 +73,14 @@ class _SparseAttention(torch.autograd.Function):
         do = do.contiguous()
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         n_tiles = mask.tiles.shape[0]
-        ws = torch.empty(_lib.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, n_tiles),
+        ws = torch.empty(_lib.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, n_tiles,
+                                    mask.ds_blocks),
                          dtype=torch.float32, device=q.device)
         _lib.call("alodlm_attention_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), nkv * dh,
                   _lib.ptr(o), _lib.ptr(lse), _lib.ptr(do), _lib.ptr(mask.boundaries),
                   _lib.ptr(mask.row_segment), _lib.ptr(mask.tiles), n_tiles, _lib.ptr(dq),
-                  _lib.ptr(dk), _lib.ptr(dv), nkv * dh, _lib.ptr(ws), N, nq, nkv, dh,
-                  mask.block_size, code, st)
+                  _lib.ptr(dk), _lib.ptr(dv), nkv * dh, _lib.ptr(ws), _lib.ptr(mask.ds_base),
+                  mask.ds_blocks, N, nq, nkv, dh, mask.block_size, code, st)
         return dq, dk, dv, None
 
 

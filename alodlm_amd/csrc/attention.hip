@@ -255,7 +255,7 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
                      const float* lse, const bf16_t* o, float* delta, const bf16_t* dout,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
                      bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
-                     float scale, hipStream_t st);
+                     float scale, const int64_t* ds_base, int64_t ds_blocks, hipStream_t st);
 
 // The MFMA kernels take bf16, head_dim 64 or 128, 16-byte aligned rows and a
 // tile table; everything else runs the reference kernels above.
@@ -296,12 +296,32 @@ extern "C" int alodlm_attention_fwd(const void* q, const void* k, const void* v,
   return ALODLM_OK;
 }
 
-int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles);
+int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles, int64_t ds_blocks);
+
+// 32x32 dS blocks per query head that the mask allows in a pack (the stored-dS
+// backward's buffer): per segment of L tokens, T (T + 1) with T = ceil(L / 32);
+// 0 unless block_size is 32.  base_out (S + 1 entries, may be NULL) receives
+// each segment's first block and the total.  Host only.
+extern "C" int64_t alodlm_attention_ds_blocks(const int64_t* token_offsets, int64_t segments,
+                                              int64_t block_size, int64_t* base_out) {
+  if (token_offsets == nullptr || segments < 0) return 0;
+  int64_t total = 0;
+  for (int64_t s = 0; s < segments; ++s) {
+    if (base_out) base_out[s] = total;
+    const int64_t L = token_offsets[s + 1] - token_offsets[s];
+    const int64_t T = (L + 31) / 32;
+    total += T * (T + 1);
+  }
+  if (base_out) base_out[segments] = total;
+  return block_size == 32 ? total : 0;
+}
 
 extern "C" int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv,
-                                                  int64_t dh, int64_t n_tiles) {
+                                                  int64_t dh, int64_t n_tiles, int64_t ds_blocks) {
   // delta [nq][rows]; the head_dim-128 kernels may also keep dK/dV partials
-  if (dh == 128 && nq > 0 && nkv > 0) return fa128_bwd_workspace(rows, (int)nq, (int)nkv, n_tiles);
+  // and the stored dS blocks
+  if (dh == 128 && nq > 0 && nkv > 0)
+    return fa128_bwd_workspace(rows, (int)nq, (int)nkv, n_tiles, ds_blocks);
   return rows * nq;
 }
 
@@ -309,7 +329,8 @@ extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v,
                                     const void* o, const float* lse, const void* dout,
                                     const int64_t* bounds, const int32_t* row_segment,
                                     const int32_t* tiles, int64_t n_tiles, void* dq, void* dk,
-                                    void* dv, int64_t lddv, float* workspace, int64_t rows,
+                                    void* dv, int64_t lddv, float* workspace,
+                                    const int64_t* ds_base, int64_t ds_blocks, int64_t rows,
                                     int64_t nq, int64_t nkv, int64_t dh, int64_t block_size,
                                     int dtype, void* stream) {
   int rc = check_attn(rows, nq, nkv, dh, block_size);
@@ -320,13 +341,13 @@ extern "C" int alodlm_attention_bwd(const void* q, const void* k, const void* v,
   float* delta = workspace;
   const bool mfma = use_mfma(dtype, dh, tiles, ldv, {q, k, v, o, dout, dq, dk, dv}) && lddv % 8 == 0;
   if (mfma && dh == 128) {
-    // the head_dim-128 dQ kernel computes delta itself
+    // the head_dim-128 kernels compute delta themselves
     if (n_tiles == 0) return ALODLM_OK;
     ALODLM_CHECK_ARG(n_tiles <= 65535, "attention: too many 128-row tiles (%lld)", (long long)n_tiles);
     return fa128_bwd_launch((const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, ldv, lse,
                             (const bf16_t*)o, delta, (const bf16_t*)dout, bounds, tiles, n_tiles,
                             (bf16_t*)dq, (bf16_t*)dk, (bf16_t*)dv, lddv, rows, (int)nq, (int)nkv,
-                            (int)block_size, scale, st);
+                            (int)block_size, scale, ds_base, ds_blocks, st);
   }
   ALODLM_DISPATCH(dtype, T, {
     attn_delta_kernel<T><<<ceil_div_u(rows * nq, 4), 256, 0, st>>>((const T*)o, (const T*)dout,

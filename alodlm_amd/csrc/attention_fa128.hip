@@ -50,6 +50,30 @@ constexpr int QT = 32;      // query rows per tile (dK/dV)
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// Stored dS (block size 32): the dK/dV pass writes dS^T in 32x32 blocks of
+// one query head - [32 keys][32 queries] bf16, 64-byte key rows - for every
+// (query tile, key tile) pair of 32-row tiles of a segment's streams that the
+// mask allows:
+//   clean query tile qt, clean key tile kt <= qt;
+//   noisy query tile qt, clean key tile kt < qt, and noisy key tile qt.
+// Blocks are numbered per segment, clean query tiles first (qt (qt + 1) / 2 +
+// kt), then noisy ones (T (T + 1) / 2 + qt (qt + 1) / 2 + kt, with kt = qt for
+// the noisy key tile), T = ceil(L / 32); ds_base[s] is the first block of
+// segment s and block b of query head h sits at (h * ds_blocks + b) * 2 KB.
+constexpr int DS_BLOCK_BYTES = 32 * 32 * 2;
+constexpr int DS_RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int DS_NT = 2;                   // cache policy of the dS stores: nt
+__device__ __forceinline__ int ds_half_blocks(int L) {
+  const int T = (L + 31) / 32;
+  return T * (T + 1) / 2;
+}
+__device__ __forceinline__ bool ds_allowed(bool qn, int qt, bool kn, int kt) {
+  return kn ? (qn && kt == qt) : (qn ? kt < qt : kt <= qt);
+}
+__device__ __forceinline__ int ds_index(bool qn, int qt, bool kn, int kt, int half_blocks) {
+  return (qn ? half_blocks : 0) + qt * (qt + 1) / 2 + (kn ? qt : kt);
+}
+
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // One wavefront instruction: tile rows [r0, r0 + 4) <- global rows
@@ -97,10 +121,13 @@ __device__ __forceinline__ void mfma_acc(f32x16_t& acc, bf16x8_t a, bf16x8_t b) 
 }
 __device__ __forceinline__ void mfma_acc_settle() { asm volatile("s_nop 15" ::: "memory"); }
 // A zero accumulator made in AGPRs (0 * 0 + 0), so that the register
-// allocator keeps the accumulator's home there from the start.
+// allocator keeps the accumulator's home there from the start.  The zero
+// operand may have been written by the instruction just before: an MFMA
+// reading a VGPR needs 2 wait states after a VALU write of it, which the
+// compiler does not insert ahead of inline assembly.
 __device__ __forceinline__ void mfma_acc_zero(f32x16_t& acc) {
   const bf16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc) : "v"(z));
 }
 
 // d = a * b (d0: first k step, zero accumulator) / d += a * b with d in VGPRs
@@ -425,8 +452,16 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                   const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
                   int n_tiles, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv,
                   float* __restrict__ partial, int64_t N, int nq, int nkv, int B, float scale,
-                  int* __restrict__ counter) {
+                  int* __restrict__ counter, bf16_t* __restrict__ ds,
+                  const int64_t* __restrict__ ds_base, int ds_blocks) {
   constexpr int S = DK_STAGES;
+  // With `ds`, every 32x32 (query tile, key tile) block of dS^T that the mask
+  // allows is stored for the dQ pass (ds_index): buffer stores, so that a
+  // block the mask rules out is dropped by the range check (offset past the
+  // buffer) rather than branched around.  The buffer is below 2 GiB.
+  const __amdgpu_buffer_rsrc_t ds_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      ds, 0, ds ? nq * ds_blocks * DS_BLOCK_BYTES : 0, DS_RSRC_WORD3);
+  const uint32_t ds_lane = (uint32_t)((threadIdx.x & 31) * 64 + ((threadIdx.x >> 5) & 1) * 8);
   static_assert(S >= 4, "the ring holds tiles i-1 .. i+2 and the one being loaded");
   __shared__ __attribute__((aligned(1024))) char lds[S][2][QT * ROWB];  // [stage][Q | dO]
   __shared__ __attribute__((aligned(16))) float lds_ld[S][4][2 * QT];   // [stage][wave][lse2 | delta]
@@ -472,6 +507,14 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     mfma_acc_zero(dvacc[i]);
   }
 
+  // dS blocks (32-bit: the buffer is below 2 GiB): this wavefront's 32-key
+  // tile in its stream, or one no query tile matches when it holds no key,
+  // and the first block of the item's first head in this segment
+  const int kn = start >= L;
+  const int kt = start + 32 * wave < k1 ? ((start - (kn ? L : 0)) >> 5) + wave : (1 << 24);
+  const uint32_t ds_item = ds ? (uint32_t)(h_first * ds_blocks + ds_base[seg]) : 0u;
+  const int half_blocks = ds_half_blocks(L);
+
   const Interval2 mine = queries_of_key(ki, k_valid, L, B);
   const Interval2 R = query_ranges(start, k1, L, B);
   // queries allowed for every key of the tile
@@ -494,7 +537,8 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     // issues DK_LOADS loads and the vmcnt waits stay fixed.
     int th = h, tr = r, tq = q0;
     // Tile descriptors of tiles i .. i+S-1: bit 0 a real tile, bit 1 every key
-    // of the key tile sees every row, bit 2 the range; and the first row.
+    // of the key tile sees every row, bit 2 the range, bits 3.. the query
+    // head's offset from h_first; and the first row.
     int fl[S], fr[S];
     auto take = [&](int& f, int& row) {
       f = 0;
@@ -502,7 +546,7 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
         th = h; tr = r; tq = q0;
         const bool full = whole && q0 >= (r ? last.lo1 : last.lo0) &&
                           q0 + QT <= (r ? first.hi1 : first.hi0);
-        f = 1 | (full ? 2 : 0) | (r << 2);
+        f = 1 | (full ? 2 : 0) | (r << 2) | ((h - h_first) << 3);
         q0 += QT;
         if (q0 >= (r ? R.hi1 : R.hi0)) {
           const bool to1 = r == 0 && has1;
@@ -672,22 +716,54 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
       };
       if (fl[0] & 2) block_a(std::false_type{});
       else block_a(std::true_type{});
+      // The packed P and dS operands of block B are fixed in their registers
+      // here, before the barrier: a VALU write of an MFMA source needs wait
+      // states that the compiler does not insert ahead of inline-asm MFMAs, so
+      // no packing or copy may be left for block B to do.
+      bf16x8_t pb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3])),
+                        __builtin_bit_cast(bf16x8_t, make_uint4(pw[4], pw[5], pw[6], pw[7]))};
+      bf16x8_t sb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(sw[0], sw[1], sw[2], sw[3])),
+                        __builtin_bit_cast(bf16x8_t, make_uint4(sw[4], sw[5], sw[6], sw[7]))};
+      asm volatile("" : "+v"(pb[0]), "+v"(pb[1]), "+v"(sb[0]), "+v"(sb[1]));
 
       // Tile i+2 has landed (this wavefront's loads, then every wavefront's);
       // the stage of tile i-1 takes tile i+S-1.
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DK_LOADS * (S - 4))
                    : "memory");
       __builtin_amdgcn_sched_barrier(0);
+      // tile i's dS^T block for this wavefront's keys (rows of 4 consecutive
+      // queries 8 j + 4 half + 0..3: dS pairs 2 j, 2 j + 1, half j % 2 of
+      // sb[j / 2]), or - when the mask rules the block out - one past the
+      // buffer, which drops the stores.  Issued before the next tile's loads,
+      // so that the vmcnt wait of the next iteration (which allows those
+      // loads to stay in flight) covers these stores as well.
+      if (ds) {
+        // (branch-free: this loop is issue-bound) the query tile's stream is
+        // noisy for a noisy key tile or range 1; ds_allowed / ds_index
+        const int qn = kn | ((fl[0] >> 2) & 1);
+        const int qt = (fr[0] - (qn ? L : 0)) >> 5;
+        const int ok = kn ? (int)(qt == kt) : (int)(kt <= qt - qn);
+        const uint32_t blk = ds_item + (uint32_t)((fl[0] >> 3) * ds_blocks) +
+                             (uint32_t)(qn ? half_blocks : 0) + (uint32_t)((qt * (qt + 1)) >> 1) +
+                             (uint32_t)(kn ? qt : kt);
+        const uint32_t ds_off = ok ? blk * DS_BLOCK_BYTES + ds_lane : 0x80000000u;
+        typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+        typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4_t w4 = __builtin_bit_cast(u32x4_t, sb[j >> 1]);
+          const u32x2_t w = (j & 1) ? u32x2_t{w4.z, w4.w} : u32x2_t{w4.x, w4.y};
+          // non-temporal: dS is read once, by the dQ pass; keeping it out of
+          // the caches' normal retention leaves them to the Q / dO tiles
+          __builtin_amdgcn_raw_buffer_store_b64(w, ds_rsrc, ds_off + 16u * j, 0, DS_NT);
+        }
+      }
       take(fl[S - 1], fr[S - 1]);
       issue(ls_stage);
       __builtin_amdgcn_sched_barrier(0);
 
       // B: dV, dK of tile i; first operands of tile i+2, first lse2 / delta
       // of tile i+1.
-      const bf16x8_t pb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3])),
-                              __builtin_bit_cast(bf16x8_t, make_uint4(pw[4], pw[5], pw[6], pw[7]))};
-      const bf16x8_t sb[2] = {__builtin_bit_cast(bf16x8_t, make_uint4(sw[0], sw[1], sw[2], sw[3])),
-                              __builtin_bit_cast(bf16x8_t, make_uint4(sw[4], sw[5], sw[6], sw[7]))};
       const char* q2 = lds[ns2][0];
       const char* d2 = lds[ns2][1];
 #pragma unroll
@@ -781,6 +857,203 @@ fa128_dkdv_reduce_kernel(const float* __restrict__ partial, int group, int64_t N
 }
 
 // ---------------------------------------------------------------------------
+// Stored-dS backward (block size 32): prep, dK/dV (storing dS), then dQ.
+// ---------------------------------------------------------------------------
+
+// delta[h, r] = sum_e dO[r, h, e] O[r, h, e] and lse2[h, r] = lse[h, r] log2(e)
+// (what the dK/dV pass reads when it runs first), and the dK/dV work counter
+// zeroed.  16 lanes per (head, row), 8 head_dim values each; items are
+// head-major so that a workgroup writes 16 consecutive rows of one head.
+__global__ void __launch_bounds__(256)
+fa128_bwd_prep_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ dout,
+                      const float* __restrict__ lse, float* __restrict__ delta, int64_t N, int nq,
+                      int* __restrict__ counter) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0;
+  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (item >= N * nq) return;
+  const int sub = threadIdx.x & 15;
+  const int h = (int)(item / N);
+  const int64_t r = item - (int64_t)h * N;
+  const int64_t off = r * nq * HD + (int64_t)h * HD + sub * 8;
+  float a[8], b[8];
+  Vec8<bf16_t>::load(o + off, a);
+  Vec8<bf16_t>::load(dout + off, b);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf(a[e], b[e], s);
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1) s += __shfl_xor(s, w, 16);
+  if (sub == 0) {
+    delta[item] = s;
+    delta[N * nq + item] = lse[item] * FA_LOG2E;
+  }
+}
+
+// dQ = scale * dS K from the stored dS^T blocks: one workgroup per (query
+// head, 128-row query tile), walking the tile's keys 32 at a time through a
+// ring of DQ_STAGES LDS stages filled by direct loads (K rows and the four
+// query tiles' dS^T blocks, both as [32 keys][128] tiles in the swizzled
+// layout), DQ_STAGES - 1 key tiles ahead.  Wavefront w accumulates dQ^T for
+// head_dim rows 64 (w / 2) .. +64 and query rows 64 (w % 2) .. +64 of the
+// tile (2 x 2 MFMA blocks), skipping every (query tile, key tile) pair the
+// mask rules out; a ruled-out block's LDS slots hold a stand-in block (the
+// head's first) that is never read.
+constexpr int DQ_STAGES = 4;
+constexpr int DQ_LOADS = 4;  // direct loads per wavefront per key tile
+
+__global__ void __launch_bounds__(256, 2)
+fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
+                   const int64_t* __restrict__ ds_base, int64_t ds_blocks,
+                   const int64_t* __restrict__ bounds, const int32_t* __restrict__ tiles,
+                   bf16_t* __restrict__ dq, int64_t N, int nq, int nkv, float scale) {
+  __shared__ __attribute__((aligned(1024))) char lds[DQ_STAGES][2][32 * ROWB];  // [stage][K | dS^T]
+  const int lane = threadIdx.x & 63, half = lane >> 5, col = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = blockIdx.x, hk = h / (nq / nkv);
+  const int seg = tiles[2 * blockIdx.y], start = tiles[2 * blockIdx.y + 1];
+  const int64_t base = bounds[seg];
+  const int L = (int)((bounds[seg + 1] - base) / 2);
+  const int stream_end = start < L ? L : 2 * L;
+  const int q1 = start + 128 < stream_end ? start + 128 : stream_end;
+  const bool qn = start >= L;
+  const int qt0 = (start - (qn ? L : 0)) >> 5;  // first 32-row query tile of the tile
+  const int nqt = (q1 - start + 31) >> 5;       // its query tiles (1..4)
+  const int half_blocks = ds_half_blocks(L);
+  // the head's blocks; every block read is checked against ds_blocks
+  const int dsb = (int)ds_blocks;
+  const bf16_t* dsh = ds + (int64_t)h * ds_blocks * (DS_BLOCK_BYTES / 2);
+  const int64_t seg_blocks = ds_base[seg];
+  const int64_t ldk = (int64_t)nkv * HD, ldq = (int64_t)nq * HD;
+  const bf16_t* kh = k + hk * HD;
+  const int dhb = (wave >> 1) * 2, qb = (wave & 1) * 2;  // first head_dim / query block
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+
+  // Query tile j of the tile (0..3) and key tile kt of range r (0: clean
+  // keys, 1: noisy keys) form an allowed block iff kt <= lim[j] (range 0:
+  // kt <= q, or kt < q for a noisy query tile q) or kt == eq[j] (range 1);
+  // the block is then tri[j] + kt of the head's blocks (ds_index).  -1 for
+  // a query tile past the stream.
+  int tri[4], lim[4], eq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = qt0 + j;
+    tri[j] = (int)seg_blocks + (qn ? half_blocks : 0) + q * (q + 1) / 2;
+    lim[j] = j < nqt ? q - (qn ? 1 : 0) : -1;
+    eq[j] = j < nqt && qn ? q : -1;
+  }
+  // this wavefront's two query tiles (qb is 0 or 2)
+  const int lim0 = qb ? lim[2] : lim[0], lim1 = qb ? lim[3] : lim[1];
+  const int eq0 = qb ? eq[2] : eq[0], eq1 = qb ? eq[3] : eq[1];
+  // The key tiles: range 0 (clean keys), then range 1 (noisy keys).
+  const Interval2 R = key_ranges(start, q1, L, 32);
+  const int n0 = R.hi0 > R.lo0 ? (R.hi0 - R.lo0 + 31) / 32 : 0;
+  const int n1 = R.hi1 > R.lo1 ? (R.hi1 - R.lo1 + 31) / 32 : 0;
+  const int n = n0 + n1;
+  auto key_tile = [&](int t, int& r, int& k0) {
+    r = t >= n0;
+    k0 = r ? R.lo1 + 32 * (t - n0) : R.lo0 + 32 * t;
+  };
+  // Per-lane parts of the direct loads, fixed for the whole walk: load i of
+  // this wavefront fills tile rows x = 8 wave + 4 i + lane / 16, 16-byte slot
+  // lane % 16, i.e. logical chunk c = slot ^ swz(x) (head_dim 8 c.. of the K
+  // row; queries 8 c.. of the tile, in query tile c / 4, in the dS^T block).
+  uint32_t k_lane[2], ds_lane[2];
+  int ds_q[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int x = wave * 8 + 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ swz(x);
+    k_lane[i] = (uint32_t)((x * ldk + c * 8) * 2);
+    ds_lane[i] = (uint32_t)((x * 32 + (c & 3) * 8) * 2);
+    ds_q[i] = c >> 2;
+  }
+  // Key tile t into stage t % DQ_STAGES: the K rows, and for each query tile
+  // of the tile its dS^T block with this key tile (byte offset from the
+  // head's first block, a scalar per query tile), or the head's first block
+  // when the mask rules the pair out.
+  auto issue = [&](int t) {
+    int r, k0;
+    key_tile(t, r, k0);
+    const int kt = (k0 - (r ? L : 0)) >> 5;
+    const int stg = t % DQ_STAGES;
+    uint32_t boff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = tri[j] + kt;
+      const int ok = (r ? (int)(kt == eq[j]) : (int)(kt <= lim[j])) & (int)(blk < dsb);
+      boff[j] = ((uint32_t)blk * DS_BLOCK_BYTES) & (uint32_t)(-ok);
+    }
+    const bool k_whole = base + k0 + 32 <= N;  // no K row to clamp
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = wave * 8 + i * 4;
+      if (k_whole) dma16_s(kh + (base + k0) * ldk, k_lane[i], lds_addr(lds[stg][0] + r0 * ROWB));
+      else dload4(lds[stg][0], r0, kh, ldk, base + k0, N - 1, lane);
+      const uint32_t b01 = ds_q[i] & 1 ? boff[1] : boff[0];
+      const uint32_t b23 = ds_q[i] & 1 ? boff[3] : boff[2];
+      dma16_s_nt(dsh, (ds_q[i] & 2 ? b23 : b01) + ds_lane[i], lds_addr(lds[stg][1] + r0 * ROWB));
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < DQ_STAGES - 1; ++t)
+    if (t < n) issue(t);
+  for (int t = 0; t < n; ++t) {
+    // key tile t has landed (this wavefront's loads, then every
+    // wavefront's); later tiles' loads may stay in flight
+    const int later = (n - 1 - t) < (DQ_STAGES - 2) ? (n - 1 - t) : (DQ_STAGES - 2);
+    if (later >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DQ_LOADS) : "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DQ_LOADS) : "memory");
+    else wait_vmem();
+    __syncthreads();
+    // the stage of key tile t - 1 is free: key tile t + DQ_STAGES - 1 goes there
+    if (t + DQ_STAGES - 1 < n) issue(t + DQ_STAGES - 1);
+    int r, k0;
+    key_tile(t, r, k0);
+    const int kt = (k0 - (r ? L : 0)) >> 5;
+    const char* kt_lds = lds[t % DQ_STAGES][0];
+    const char* st_lds = lds[t % DQ_STAGES][1];
+    const bool ok0 = r ? kt == eq0 : kt <= lim0, ok1 = r ? kt == eq1 : kt <= lim1;
+    if (!ok0 && !ok1) continue;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int rk = st * 16;
+      const bf16x8_t a0 = tr_frag(kt_lds, rk, dhb * 32, lane);
+      const bf16x8_t a1 = tr_frag(kt_lds, rk, dhb * 32 + 32, lane);
+      if (ok0) {
+        const bf16x8_t b = tr_frag(st_lds, rk, qb * 32, lane);
+        acc[0][0] = mfma(a0, b, acc[0][0]);
+        acc[1][0] = mfma(a1, b, acc[1][0]);
+      }
+      if (ok1) {
+        const bf16x8_t b = tr_frag(st_lds, rk, qb * 32 + 32, lane);
+        acc[0][1] = mfma(a0, b, acc[0][1]);
+        acc[1][1] = mfma(a1, b, acc[1][1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int qi = start + (qb + j) * 32 + col;
+    if (qi >= q1) continue;
+    bf16_t* row = dq + (base + qi) * ldq + (int64_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int d = (dhb + i) * 32 + jj * 8 + half * 4;
+        *reinterpret_cast<uint2*>(row + d) =
+            make_uint2(pack2(acc[i][j][jj * 4] * scale, acc[i][j][jj * 4 + 1] * scale),
+                       pack2(acc[i][j][jj * 4 + 2] * scale, acc[i][j][jj * 4 + 3] * scale));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Launchers (head_dim 128)
 // ---------------------------------------------------------------------------
 
@@ -793,9 +1066,23 @@ static bool dkdv_head_split(int64_t n_tiles, int nq, int nkv) {
 
 // delta [nq][N], lse * log2(e) [nq][N], the dK/dV work counter (one int in a
 // 64-float slot), then (head split) the float32 dK/dV partials
-// [2][group][N][nkv*128].
+// [2][group][N][nkv*128], then (stored dS) nq * ds_blocks dS^T blocks,
+// 256-byte aligned.
 constexpr int64_t COUNTER_SLOT = 64;
-int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles) {
+static int64_t fa128_ds_offset(int64_t N, int nq, int nkv, int64_t n_tiles) {
+  const int64_t head = 2 * N * nq + COUNTER_SLOT;
+  const int64_t end = dkdv_head_split(n_tiles, nq, nkv) ? head + 2 * N * (int64_t)nq * HD : head;
+  return (end + 63) / 64 * 64;
+}
+// The stored-dS path needs the block size 32 and a dS buffer below 2 GiB (its
+// buffer stores take 32-bit offsets).
+static bool fa128_ds_path(int64_t nq, int64_t ds_blocks, int64_t block_size) {
+  return block_size == 32 && ds_blocks > 0 && nq * ds_blocks * DS_BLOCK_BYTES < (int64_t(1) << 31);
+}
+int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles, int64_t ds_blocks) {
+  const int64_t off = fa128_ds_offset(N, nq, nkv, n_tiles);
+  if (ds_blocks > 0 && nq * ds_blocks * DS_BLOCK_BYTES < (int64_t(1) << 31))
+    return off + (int64_t)nq * ds_blocks * (DS_BLOCK_BYTES / 4);
   const int64_t head = 2 * N * nq + COUNTER_SLOT;
   return dkdv_head_split(n_tiles, nq, nkv) ? head + 2 * N * (int64_t)nq * HD : head;
 }
@@ -825,13 +1112,22 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
                      const float* lse, const bf16_t* o, float* delta, const bf16_t* dout,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* dq,
                      bf16_t* dk, bf16_t* dv, int64_t lddv, int64_t N, int nq, int nkv, int B,
-                     float scale, hipStream_t st) {
-  // the dQ pass writes delta and lse * log2(e), which the dK/dV pass reads
-  // (stream order)
-  // (and zeroes the dK/dV work counter)
+                     float scale, const int64_t* ds_base, int64_t ds_blocks, hipStream_t st) {
   int* counter = reinterpret_cast<int*>(delta + 2 * N * nq);
-  fa128_dq_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
-      q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale, counter);
+  const bool stored = ds_base != nullptr && fa128_ds_path(nq, ds_blocks, B);
+  bf16_t* ds = stored ? reinterpret_cast<bf16_t*>(delta + fa128_ds_offset(N, nq, nkv, n_tiles))
+                      : nullptr;
+  if (stored) {
+    // delta, lse * log2(e) and the zeroed work counter for the dK/dV pass,
+    // which stores dS for the dQ pass (stream order)
+    fa128_bwd_prep_kernel<<<ceil_div_u(N * nq, 16), 256, 0, st>>>(o, dout, lse, delta, N, nq,
+                                                                   counter);
+  } else {
+    // the dQ pass writes delta and lse * log2(e), which the dK/dV pass reads
+    // (stream order), and zeroes the dK/dV work counter
+    fa128_dq_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
+        q, k, v, ldv, lse, o, delta, dout, bounds, tiles, dq, N, nq, nkv, B, scale, counter);
+  }
   const float* lse2 = delta + N * nq;
   const bool split = dkdv_head_split(n_tiles, nq, nkv);
   const int64_t items = (split ? nq : nkv) * n_tiles;
@@ -839,10 +1135,13 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
   float* partial = split ? delta + 2 * N * nq + COUNTER_SLOT : nullptr;
   fa128_dkdv_kernel<<<grid, 256, 0, st>>>(q, k, v, ldv, lse2, delta, dout, bounds, tiles,
                                           (int)n_tiles, dk, dv, lddv, partial, N, nq, nkv, B,
-                                          scale, counter);
+                                          scale, counter, ds, ds_base, (int)ds_blocks);
   if (split)
     fa128_dkdv_reduce_kernel<<<ceil_div_u(2 * N * nkv * HD / 8, 256), 256, 0, st>>>(
         partial, nq / nkv, N, nkv, dk, dv, lddv);
+  if (stored)
+    fa128_dq_ds_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
+        k, ds, ds_base, ds_blocks, bounds, tiles, dq, N, nq, nkv, scale);
   ALODLM_CHECK_LAUNCH("attention_bwd_fa128");
   return ALODLM_OK;
 }

@@ -53,6 +53,24 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t
       : "memory");
 }
 
+// dma16_s for data read once: non-temporal (streamed past the caches' normal
+// retention), so it does not evict operands that other workgroups re-read.
+__device__ __forceinline__ void dma16_s_nt(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t ub = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(ub), "s"(lds)
+      : "memory");
+}
+
 // 4 bytes per lane from the per-lane address g.
 __device__ __forceinline__ void dma4_v(const void* g, uint32_t lds) {
   uint32_t saved;

@@ -65,6 +65,16 @@ def attention_tiles(offsets):
     return [v for _, s, start in tiles for v in (s, start)]
 
 
+def ds_block_base(offsets):
+    """First 32x32 dS block of each segment, and the total, for the stored-dS
+    attention backward: a segment of L tokens holds T (T + 1) blocks per query
+    head, T = ceil(L / 32) (the allowed pairs of 32-row query and key tiles
+    of its clean and noisy streams).  int64 [S + 1]."""
+    lengths = np.diff(np.asarray(offsets, dtype=np.int64))
+    tiles = (lengths + 31) // 32
+    return np.concatenate([[0], np.cumsum(tiles * (tiles + 1))]).astype(np.int64)
+
+
 def _to_device(array, device):
     """Host array -> device tensor through pinned memory, without blocking."""
     return torch.from_numpy(np.ascontiguousarray(array)).pin_memory().to(device, non_blocking=True)
@@ -95,6 +105,10 @@ class DualStreamMask:
         self.row_segment = row_segment
         self.tiles = _to_device(np.asarray(attention_tiles(offsets), dtype=np.int32),
                                 device).view(-1, 2)
+        # the stored-dS attention backward's block table (block size 32 only)
+        base = ds_block_base(offsets)
+        self.ds_blocks = int(base[-1]) if self.block_size == 32 else 0
+        self.ds_base = _to_device(base, device) if self.ds_blocks else None
 
     @classmethod
     def from_plan(cls, plan, device):
@@ -333,12 +347,13 @@ class Kernels:
     def _attention_bwd(self, q, k, v, ldv, o, lse, do, dq, dk, dv, lddv, mask):
         d, N = self.dims, q.shape[0]
         n_tiles = 0 if mask.tiles is None else mask.tiles.shape[0]
+        ds_blocks = getattr(mask, "ds_blocks", 0)
         ws = self._workspace(query("alodlm_attention_bwd_workspace", N, d.heads, d.kv_heads,
-                                   d.head_dim, n_tiles))
+                                   d.head_dim, n_tiles, ds_blocks))
         call("alodlm_attention_bwd", ptr(q), ptr(k), ptr(v), ldv, ptr(o), ptr(lse), ptr(do),
              ptr(mask.boundaries), ptr(mask.row_segment), ptr(mask.tiles), n_tiles, ptr(dq),
-             ptr(dk), ptr(dv), lddv, ptr(ws), N, d.heads, d.kv_heads, d.head_dim,
-             mask.block_size, self.code, self._stream())
+             ptr(dk), ptr(dv), lddv, ptr(ws), ptr(getattr(mask, "ds_base", None)), ds_blocks,
+             N, d.heads, d.kv_heads, d.head_dim, mask.block_size, self.code, self._stream())
 
     def _attention_fwd_flops(self, q, k, v, ldv, o, lse, mask):
         """Algorithmic forward FLOPs: 4*dh per allowed (q, k) pair and head."""

@@ -413,7 +413,8 @@ def run_attention(spec, device, steps, warmup):
     lse = torch.empty(nq, N, dtype=torch.float32, device=device)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     n_tiles = mask.tiles.shape[0]
-    ws = torch.empty(_lib.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, n_tiles),
+    ws = torch.empty(_lib.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, n_tiles,
+                                mask.ds_blocks),
                      dtype=torch.float32, device=device)
     st = _lib.stream_handle(device)
     P = _lib.ptr
@@ -424,13 +425,17 @@ def run_attention(spec, device, steps, warmup):
                   P(mask.row_segment), P(mask.tiles), n_tiles, P(o), P(lse), N, nq, nkv, dh, 32,
                   code, st)
 
-    def bwd():
+    def bwd(stored=True):
         _lib.call("alodlm_attention_bwd", P(q), P(k), P(v), nkv * dh, P(o), P(lse), P(do),
                   P(mask.boundaries), P(mask.row_segment), P(mask.tiles), n_tiles, P(dq), P(dk),
-                  P(dv), nkv * dh, P(ws), N, nq, nkv, dh, 32, code, st)
+                  P(dv), nkv * dh, P(ws), P(mask.ds_base) if stored else None, mask.ds_blocks,
+                  N, nq, nkv, dh, 32, code, st)
 
     out = {}
-    for name, fn, per_pair in (("attention_fwd", fwd, 4), ("attention_bwd", bwd, 8)):
+    # attention_bwd: the step's path (dK/dV stores dS, dQ = dS K);
+    # attention_bwd_recompute: the dQ pass that recomputes S, P and dP
+    for name, fn, per_pair in (("attention_fwd", fwd, 4), ("attention_bwd", bwd, 8),
+                               ("attention_bwd_recompute", lambda: bwd(False), 8)):
         for _ in range(warmup):
             fn()
         stream = torch.cuda.current_stream(device)

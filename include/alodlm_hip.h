@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 4
+#define ALODLM_ABI_VERSION 5
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -217,25 +217,36 @@ int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t
  * bf16 and head_dim 64/128 the MFMA flash kernels run, otherwise (or with
  * tiles == NULL) the reference kernels.
  * bwd: dq [rows, nq*dh], dk [rows, nkv*dh], dv (stride lddv) from do.
- * `workspace` holds alodlm_attention_bwd_workspace(rows, nq, nkv, dh, n_tiles)
- * floats (delta per head and row; for head_dim 128 also lse * log2(e) per
- * head and row, the dK/dV pass's work counter, and with few key tiles per kv
- * head float32 dK/dV partials per query head).  Calls that share a workspace
- * must not overlap.
+ * `workspace` holds alodlm_attention_bwd_workspace(rows, nq, nkv, dh, n_tiles,
+ * ds_blocks) floats (delta per head and row; for head_dim 128 also
+ * lse * log2(e) per head and row, the dK/dV pass's work counter, with few key
+ * tiles per kv head float32 dK/dV partials per query head, and the stored dS
+ * blocks).  Calls that share a workspace must not overlap.
+ * Stored dS (head_dim 128, bf16, block_size 32): with ds_base (device int64
+ * [S+1], each segment's first 32x32 block as alodlm_attention_ds_blocks
+ * fills it) and ds_blocks (its total, > 0), the dK/dV pass stores the bf16 dS
+ * of every allowed pair and dQ is one dS*K product over them, instead of
+ * recomputing S, P and dP; ds_base NULL (or ds_blocks 0, or a buffer of
+ * nq * ds_blocks * 2 KiB at or above 2 GiB) selects the recomputing dQ pass.
+ * alodlm_attention_ds_blocks is host code: token_offsets are the S+1 token
+ * offsets of the pack (host memory).
  * ------------------------------------------------------------------------ */
 int alodlm_attention_fwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const int64_t* bounds, const int32_t* row_segment,
                          const int32_t* tiles, int64_t n_tiles, void* o, float* lse,
                          int64_t rows, int64_t nq, int64_t nkv, int64_t dh, int64_t block_size,
                          int dtype, void* stream);
+int64_t alodlm_attention_ds_blocks(const int64_t* token_offsets, int64_t segments,
+                                   int64_t block_size, int64_t* base_out);
 int64_t alodlm_attention_bwd_workspace(int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
-                                       int64_t n_tiles);
+                                       int64_t n_tiles, int64_t ds_blocks);
 int alodlm_attention_bwd(const void* q, const void* k, const void* v, int64_t ldv,
                          const void* o, const float* lse, const void* dout,
                          const int64_t* bounds, const int32_t* row_segment,
                          const int32_t* tiles, int64_t n_tiles, void* dq, void* dk, void* dv,
-                         int64_t lddv, float* workspace, int64_t rows, int64_t nq, int64_t nkv,
-                         int64_t dh, int64_t block_size, int dtype, void* stream);
+                         int64_t lddv, float* workspace, const int64_t* ds_base,
+                         int64_t ds_blocks, int64_t rows, int64_t nq, int64_t nkv, int64_t dh,
+                         int64_t block_size, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * SwiGLU ([tf] modeling_qwen3.py:81-83): gu = [gate | up] of width 2*inter;

@@ -108,3 +108,48 @@ def test_embed_plan_limits_on_the_host():
                   151936, _lib.BF16_CODE, None)
     # zero rows is a no-op that touches nothing
     _lib.call("alodlm_embed_plan", None, 0, 151936, None, None)
+
+
+def test_ds_block_table_matches_mask():
+    """The stored-dS attention backward's block table (host only): the library's
+    alodlm_attention_ds_blocks and layers.ds_block_base agree, and per segment
+    the 32x32 (query tile, key tile) blocks holding an allowed pair of the
+    dense dual-stream mask (alodlm/batch.py:23-31) are exactly T (T + 1),
+    T = ceil(L / 32), numbered without gaps or repeats by the kernels'
+    clean-first, row-by-row order."""
+    import numpy as np
+    import torch
+    from alodlm_amd import _lib
+    from alodlm_amd.batch import attention_mask
+    from alodlm_amd.layers import ds_block_base
+    if not _lib.LIBRARY.exists():
+        pytest.skip("library not built")
+    offsets = np.asarray([0, 1, 33, 97, 225, 288, 640], dtype=np.int64)
+    base = np.zeros(len(offsets), dtype=np.int64)
+    total = _lib.query("alodlm_attention_ds_blocks", offsets.ctypes.data, len(offsets) - 1, 32,
+                       base.ctypes.data)
+    assert total == base[-1] and np.array_equal(base, ds_block_base(offsets))
+    assert _lib.query("alodlm_attention_ds_blocks", offsets.ctypes.data, len(offsets) - 1, 16,
+                      None) == 0
+    for a, b in zip(offsets, offsets[1:]):
+        L = int(b - a)
+        T = (L + 31) // 32
+        mask = attention_mask(L, 32, "cpu")
+        seen = []
+        for qs in (0, L):          # clean, noisy query stream
+            for qt in range(T):
+                for ks in (0, L):
+                    for kt in range(T):
+                        q = slice(qs + 32 * qt, min(qs + 32 * qt + 32, qs + L))
+                        k = slice(ks + 32 * kt, min(ks + 32 * kt + 32, ks + L))
+                        if bool(mask[q, k].any()):
+                            seen.append((qs > 0, qt, ks > 0, kt))
+        assert len(seen) == T * (T + 1) == base[list(offsets).index(b)] - base[list(offsets).index(a)]
+        half = T * (T + 1) // 2
+        index = sorted((half if qn else 0) + qt * (qt + 1) // 2 + (qt if kn else kt)
+                       for qn, qt, kn, kt in seen)
+        assert index == list(range(T * (T + 1)))
+        # the clean stream never sees a noisy key; a noisy tile's only noisy
+        # key tile is its own
+        assert all(qn or not kn for qn, qt, kn, kt in seen)
+        assert all(kt == qt for qn, qt, kn, kt in seen if kn)

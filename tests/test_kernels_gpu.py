@@ -252,19 +252,36 @@ ATTN_CASES = [
     (torch.bfloat16, 2, 2, 64, [0, 200, 390], 24, "mfma"),
     (torch.bfloat16, 2, 1, 128, [0, 1024], 32, "mfma"),
     (torch.bfloat16, 4, 2, 128, [0, 512, 1000, 1001], 32, "mfma"),
+    # head_dim 128 with the dQ pass that recomputes S, P and dP (no stored dS)
+    (torch.bfloat16, 4, 1, 128, [0, 300, 333], 32, "mfma-recompute"),
+    (torch.bfloat16, 4, 2, 128, [0, 512, 1000, 1001], 32, "mfma-recompute"),
 ]
+
+
+def _ds_table(L, bounds, block):
+    """(device ds_base, ds_blocks) of the stored-dS backward from the
+    library's host helper (ds_blocks is 0 unless block is 32)."""
+    import numpy as np
+    offs = np.asarray(bounds, dtype=np.int64)
+    base = np.zeros(len(bounds), dtype=np.int64)
+    n = L.query("alodlm_attention_ds_blocks", offs.ctypes.data, len(bounds) - 1, block,
+                base.ctypes.data)
+    return (torch.from_numpy(base).to(DEV) if n else None), n
 
 
 @pytest.mark.parametrize("dtype,nq,nkv,dh,bounds,block,path", ATTN_CASES)
 def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block, path):
     """Attention (dual-stream mask) with q/k norm + rotary, forward and backward,
     against autograd through the oracle's restatement in float64.  `path`
-    selects the reference kernels (no tile table) or the MFMA flash kernels."""
+    selects the reference kernels (no tile table) or the MFMA flash kernels
+    (with block size 32 and head_dim 128 the dK/dV pass stores dS and dQ is
+    one dS*K product; "mfma-recompute" runs the dQ pass that recomputes)."""
     from alodlm_amd.batch import attention_tiles
     L = lib()
     log(f"attention nq={nq} nkv={nkv} dh={dh} bounds={bounds} block={block} {dtype} {path}")
     tiles = torch.tensor(attention_tiles(bounds), dtype=torch.int32).view(-1, 2).to(DEV)
-    tiles_ptr = L.ptr(tiles) if path == "mfma" else None
+    tiles_ptr = L.ptr(tiles) if path.startswith("mfma") else None
+    ds_base, ds_blocks = _ds_table(L, bounds, block) if path == "mfma" else (None, 0)
     g = torch.Generator().manual_seed(dh + nq)
     positions, row_seg, packed = _dual_stream(bounds, block, dh)
     N = len(positions)
@@ -290,14 +307,15 @@ def test_qknorm_rope_attention_fwd_bwd(dtype, nq, nkv, dh, bounds, block, path):
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dqkv = torch.zeros(N, W, dtype=dtype, device=DEV)
-    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0]),
+    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0],
+                             ds_blocks),
                      dtype=torch.float32,
                      device=DEV)
     dout_d = dout.to(DEV)
     L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
            L.ptr(dout_d), L.ptr(bnd_d), L.ptr(seg_d), tiles_ptr, tiles.shape[0], L.ptr(dq),
-           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block,
-           code, st())
+           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), L.ptr(ds_base), ds_blocks,
+           N, nq, nkv, dh, block, code, st())
     dwq = torch.zeros(dh, dtype=torch.float32, device=DEV)
     dwk = torch.zeros(dh, dtype=torch.float32, device=DEV)
     ws2 = torch.empty(L.query("alodlm_qknorm_rope_bwd_workspace", N, nq, nkv, dh) * 2 + 16,
@@ -447,17 +465,19 @@ def test_cast_covers_more_than_2_32_elements():
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("stored", [True, False])
 @pytest.mark.parametrize("seg_len,n_seg", [(1024, 8), (2048, 1)])
-def test_attention_fa128_large_packs_against_torch_fp32(seg_len, n_seg):
+def test_attention_fa128_large_packs_against_torch_fp32(seg_len, n_seg, stored):
     """head_dim-128 attention at the 1.7B head layout (16 q / 8 kv heads) on
     long packs: 8 x 1024 tokens keeps one dK/dV workgroup per (kv head, key
     tile); 1 x 2048 splits the dK/dV work by query head and reduces the float32
-    partials.  Reference: torch float32 autograd per segment under the
+    partials; `stored`: dQ from the dS the dK/dV pass stores, else the dQ pass
+    that recomputes.  Reference: torch float32 autograd per segment under the
     dual-stream mask (alodlm/batch.py:23-31), on the GPU."""
     from alodlm_amd.batch import attention_mask, attention_tiles
     L = lib()
     nq, nkv, dh, block = 16, 8, 128, 32
-    log(f"attention fa128 large pack seg_len={seg_len} n_seg={n_seg}")
+    log(f"attention fa128 large pack seg_len={seg_len} n_seg={n_seg} stored={stored}")
     bounds = [i * seg_len for i in range(n_seg + 1)]
     N = 2 * bounds[-1]
     tiles = torch.tensor(attention_tiles(bounds), dtype=torch.int32).view(-1, 2).to(DEV)
@@ -477,12 +497,15 @@ def test_attention_fa128_large_packs_against_torch_fp32(seg_len, n_seg):
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dqkv = torch.zeros(N, W, dtype=torch.bfloat16, device=DEV)
-    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0]),
+    ds_base, ds_blocks = _ds_table(L, bounds, block) if stored else (None, 0)
+    assert not stored or ds_blocks == n_seg * (seg_len // 32) * (seg_len // 32 + 1)
+    ws = torch.empty(L.query("alodlm_attention_bwd_workspace", N, nq, nkv, dh, tiles.shape[0],
+                             ds_blocks),
                      dtype=torch.float32, device=DEV)
     L.call("alodlm_attention_bwd", L.ptr(q), L.ptr(k), L.ptr(v), W, L.ptr(o), L.ptr(lse),
            L.ptr(dout), L.ptr(packed), L.ptr(seg), L.ptr(tiles), tiles.shape[0], L.ptr(dq),
-           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), N, nq, nkv, dh, block, 1,
-           st())
+           L.ptr(dk), L.ptr(dqkv[:, (nq + nkv) * dh:]), W, L.ptr(ws), L.ptr(ds_base), ds_blocks,
+           N, nq, nkv, dh, block, 1, st())
     torch.cuda.synchronize()
     dv = dqkv[:, (nq + nkv) * dh:]
     mask = attention_mask(seg_len, block, DEV)

@@ -344,7 +344,7 @@ def test_8b_layer_shapes_match_oracle():
     # one short segment: few key tiles per key-value head, so the dK/dV pass
     # is split by query head (its workspace holds the float32 partials)
     from alodlm_amd import _lib
-    assert (_lib.query("alodlm_attention_bwd_workspace", 2048, 32, 8, 128, 16)
+    assert (_lib.query("alodlm_attention_bwd_workspace", 2048, 32, 8, 128, 16, 0)
             > 2 * 2048 * 32)
     _compare_with_oracle(model, params, dims, obj, ids, labels, bounds, seed=12)
 
@@ -383,5 +383,5 @@ def test_full_8b_step_properties():
     from alodlm_amd import _lib
     # one 2048-token sequence: 32 key tiles per key-value head, so the dK/dV
     # pass is split by query head
-    assert _lib.query("alodlm_attention_bwd_workspace", 4096, 32, 8, 128, 32) > 2 * 4096 * 32
+    assert _lib.query("alodlm_attention_bwd_workspace", 4096, 32, 8, 128, 32, 0) > 2 * 4096 * 32
     _full_size("8b", seed=22)
