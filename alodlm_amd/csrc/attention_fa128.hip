@@ -919,8 +919,7 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
   const int qt0 = (start - (qn ? L : 0)) >> 5;  // first 32-row query tile of the tile
   const int nqt = (q1 - start + 31) >> 5;       // its query tiles (1..4)
   const int half_blocks = ds_half_blocks(L);
-  // the head's blocks; every block read is checked against ds_blocks
-  const int dsb = (int)ds_blocks;
+  // the head's blocks
   const bf16_t* dsh = ds + (int64_t)h * ds_blocks * (DS_BLOCK_BYTES / 2);
   const int64_t seg_blocks = ds_base[seg];
   const int64_t ldk = (int64_t)nkv * HD, ldq = (int64_t)nq * HD;
@@ -946,18 +945,33 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
     lim[j] = j < nqt ? q - (qn ? 1 : 0) : -1;
     eq[j] = j < nqt && qn ? q : -1;
   }
+  // The largest block this tile reads (last query tile, its last key tile)
+  // is checked once against the buffer; a table that does not fit reads
+  // nothing (dQ 0) rather than past the buffer.
+  {
+    const int q = qt0 + nqt - 1;
+    const bool fits = seg_blocks >= 0 && tri[0] >= 0 && (int64_t)seg_blocks + (qn ? half_blocks : 0) +
+                                                            (int64_t)q * (q + 1) / 2 + q < ds_blocks;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lim[j] = fits ? lim[j] : -1;
+      eq[j] = fits ? eq[j] : -1;
+    }
+  }
+  // key tile kt lies in [lo, hi] (sign bit of the two differences)
+  auto in_range = [](int kt, int lo, int hi) { return ((kt - lo) | (hi - kt)) >= 0; };
   // this wavefront's two query tiles (qb is 0 or 2)
   const int lim0 = qb ? lim[2] : lim[0], lim1 = qb ? lim[3] : lim[1];
   const int eq0 = qb ? eq[2] : eq[0], eq1 = qb ? eq[3] : eq[1];
-  // The key tiles: range 0 (clean keys), then range 1 (noisy keys).
+  // The key tiles: range 0 (clean keys, from key tile 0), then range 1
+  // (noisy keys, from tile kt1 of the noisy stream); key tile t of the walk
+  // is (range t >= n0, stream tile kt(t)).
   const Interval2 R = key_ranges(start, q1, L, 32);
   const int n0 = R.hi0 > R.lo0 ? (R.hi0 - R.lo0 + 31) / 32 : 0;
   const int n1 = R.hi1 > R.lo1 ? (R.hi1 - R.lo1 + 31) / 32 : 0;
   const int n = n0 + n1;
-  auto key_tile = [&](int t, int& r, int& k0) {
-    r = t >= n0;
-    k0 = r ? R.lo1 + 32 * (t - n0) : R.lo0 + 32 * t;
-  };
+  const int kt1 = (R.lo1 - L) >> 5;
+  auto stream_tile = [&](int t) { return t < n0 ? t : kt1 + (t - n0); };
   // Per-lane parts of the direct loads, fixed for the whole walk: load i of
   // this wavefront fills tile rows x = 8 wave + 4 i + lane / 16, 16-byte slot
   // lane % 16, i.e. logical chunk c = slot ^ swz(x) (head_dim 8 c.. of the K
@@ -972,31 +986,57 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
     ds_lane[i] = (uint32_t)((x * 32 + (c & 3) * 8) * 2);
     ds_q[i] = c >> 2;
   }
+  const uint32_t lds_w = lds_addr(lds) + (uint32_t)(wave * 8 * ROWB);  // this wave's rows
   // Key tile t into stage t % DQ_STAGES: the K rows, and for each query tile
   // of the tile its dS^T block with this key tile (byte offset from the
   // head's first block, a scalar per query tile), or the head's first block
-  // when the mask rules the pair out.
+  // when the mask rules the pair out.  The four direct loads share one M0
+  // save: M0 is the LDS destination, the wave-uniform base a scalar pair.
   auto issue = [&](int t) {
-    int r, k0;
-    key_tile(t, r, k0);
-    const int kt = (k0 - (r ? L : 0)) >> 5;
-    const int stg = t % DQ_STAGES;
+    const int r = t >= n0, kt = stream_tile(t);
+    const int64_t krow = base + (r ? L : 0) + 32 * kt;  // first key row
     uint32_t boff[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int blk = tri[j] + kt;
-      const int ok = (r ? (int)(kt == eq[j]) : (int)(kt <= lim[j])) & (int)(blk < dsb);
-      boff[j] = ((uint32_t)blk * DS_BLOCK_BYTES) & (uint32_t)(-ok);
+      // range 0: key tiles [0, lim]; range 1: [eq, eq]
+      const bool ok = in_range(kt, r ? eq[j] : 0, r ? eq[j] : lim[j]);
+      boff[j] = ok ? (uint32_t)(tri[j] + kt) * DS_BLOCK_BYTES : 0u;
     }
-    const bool k_whole = base + k0 + 32 <= N;  // no K row to clamp
+    uint32_t off[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int r0 = wave * 8 + i * 4;
-      if (k_whole) dma16_s(kh + (base + k0) * ldk, k_lane[i], lds_addr(lds[stg][0] + r0 * ROWB));
-      else dload4(lds[stg][0], r0, kh, ldk, base + k0, N - 1, lane);
       const uint32_t b01 = ds_q[i] & 1 ? boff[1] : boff[0];
       const uint32_t b23 = ds_q[i] & 1 ? boff[3] : boff[2];
-      dma16_s_nt(dsh, (ds_q[i] & 2 ? b23 : b01) + ds_lane[i], lds_addr(lds[stg][1] + r0 * ROWB));
+      off[i] = (ds_q[i] & 2 ? b23 : b01) + ds_lane[i];
+    }
+    const uint32_t l0 = lds_w + (uint32_t)((t % DQ_STAGES) * (2 * 32 * ROWB));
+    if (krow + 32 <= N) {
+      const bf16_t* kb = kh + krow * ldk;
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %[sv], m0\n\t"
+          "s_mov_b32 m0, %[l0]\n\t"
+          "global_load_lds_dwordx4 %[k0], %[kb]\n\t"
+          "s_add_u32 m0, %[l0], %[r4]\n\t"
+          "global_load_lds_dwordx4 %[k1], %[kb]\n\t"
+          "s_add_u32 m0, %[l0], %[dt]\n\t"
+          "global_load_lds_dwordx4 %[s0], %[db] nt\n\t"
+          "s_add_u32 m0, %[l0], %[dt4]\n\t"
+          "global_load_lds_dwordx4 %[s1], %[db] nt\n\t"
+          "s_mov_b32 m0, %[sv]"
+          : [sv] "=&s"(saved)
+          : [l0] "s"(l0), [k0] "v"(k_lane[0]), [k1] "v"(k_lane[1]), [s0] "v"(off[0]),
+            [s1] "v"(off[1]), [kb] "s"(kb), [db] "s"(dsh), [r4] "n"(4 * ROWB),
+            [dt] "n"(32 * ROWB), [dt4] "n"(36 * ROWB)
+          : "memory");
+    } else {  // rows past the pack's last row re-read it (their dS is 0)
+      const int stg = t % DQ_STAGES;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r0 = wave * 8 + i * 4;
+        dload4(lds[stg][0], r0, kh, ldk, krow, N - 1, lane);
+        dma16_s_nt(dsh, off[i], lds_addr(lds[stg][1] + r0 * ROWB));
+      }
     }
   };
 #pragma unroll
@@ -1012,12 +1052,11 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
     __syncthreads();
     // the stage of key tile t - 1 is free: key tile t + DQ_STAGES - 1 goes there
     if (t + DQ_STAGES - 1 < n) issue(t + DQ_STAGES - 1);
-    int r, k0;
-    key_tile(t, r, k0);
-    const int kt = (k0 - (r ? L : 0)) >> 5;
+    const int r = t >= n0, kt = stream_tile(t);
     const char* kt_lds = lds[t % DQ_STAGES][0];
     const char* st_lds = lds[t % DQ_STAGES][1];
-    const bool ok0 = r ? kt == eq0 : kt <= lim0, ok1 = r ? kt == eq1 : kt <= lim1;
+    const bool ok0 = in_range(kt, r ? eq0 : 0, r ? eq0 : lim0);
+    const bool ok1 = in_range(kt, r ? eq1 : 0, r ? eq1 : lim1);
     if (!ok0 && !ok1) continue;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
