@@ -958,20 +958,27 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
       eq[j] = fits ? eq[j] : -1;
     }
   }
-  // key tile kt lies in [lo, hi] (sign bit of the two differences)
-  auto in_range = [](int kt, int lo, int hi) { return ((kt - lo) | (hi - kt)) >= 0; };
-  // this wavefront's two query tiles (qb is 0 or 2)
-  const int lim0 = qb ? lim[2] : lim[0], lim1 = qb ? lim[3] : lim[1];
-  const int eq0 = qb ? eq[2] : eq[0], eq1 = qb ? eq[3] : eq[1];
   // The key tiles: range 0 (clean keys, from key tile 0), then range 1
-  // (noisy keys, from tile kt1 of the noisy stream); key tile t of the walk
-  // is (range t >= n0, stream tile kt(t)).
+  // (noisy keys, from tile kt1 = qt0 of the noisy stream, one per query tile
+  // of a noisy tile).  In walk order t, query tile j takes the clean key tiles
+  // t <= lim[j] (block tri[j] + t) and the noisy key tile t == e[j] (block
+  // tri[j] + eq[j]).
   const Interval2 R = key_ranges(start, q1, L, 32);
   const int n0 = R.hi0 > R.lo0 ? (R.hi0 - R.lo0 + 31) / 32 : 0;
   const int n1 = R.hi1 > R.lo1 ? (R.hi1 - R.lo1 + 31) / 32 : 0;
   const int n = n0 + n1;
   const int kt1 = (R.lo1 - L) >> 5;
-  auto stream_tile = [&](int t) { return t < n0 ? t : kt1 + (t - n0); };
+  int e[4];
+  uint32_t b0[4], b1[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    e[j] = eq[j] >= 0 ? n0 + (eq[j] - kt1) : -1;
+    b0[j] = (uint32_t)tri[j] * DS_BLOCK_BYTES;
+    b1[j] = (uint32_t)(tri[j] + eq[j]) * DS_BLOCK_BYTES;
+  }
+  // this wavefront's two query tiles (qb is 0 or 2)
+  const int lim0 = qb ? lim[2] : lim[0], lim1 = qb ? lim[3] : lim[1];
+  const int e0 = qb ? e[2] : e[0], e1 = qb ? e[3] : e[1];
   // Per-lane parts of the direct loads, fixed for the whole walk: load i of
   // this wavefront fills tile rows x = 8 wave + 4 i + lane / 16, 16-byte slot
   // lane % 16, i.e. logical chunk c = slot ^ swz(x) (head_dim 8 c.. of the K
@@ -990,18 +997,18 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
   // Key tile t into stage t % DQ_STAGES: the K rows, and for each query tile
   // of the tile its dS^T block with this key tile (byte offset from the
   // head's first block, a scalar per query tile), or the head's first block
-  // when the mask rules the pair out.  The four direct loads share one M0
-  // save: M0 is the LDS destination, the wave-uniform base a scalar pair.
+  // when the query tile does not take the key tile.  The four direct loads
+  // share one M0 save: M0 is the LDS destination, the wave-uniform base a
+  // scalar pair.  Tiles are issued in walk order, so the first K row and the
+  // clean-tile block offsets advance by one tile per call.
+  int64_t krow = base;       // first K row of the next tile to issue
+  uint32_t tb = 0;           // its clean-tile block offset t * 2 KB
   auto issue = [&](int t) {
-    const int r = t >= n0, kt = stream_tile(t);
-    const int64_t krow = base + (r ? L : 0) + 32 * kt;  // first key row
+    if (t == n0) krow = base + L + 32 * kt1;
     uint32_t boff[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // range 0: key tiles [0, lim]; range 1: [eq, eq]
-      const bool ok = in_range(kt, r ? eq[j] : 0, r ? eq[j] : lim[j]);
-      boff[j] = ok ? (uint32_t)(tri[j] + kt) * DS_BLOCK_BYTES : 0u;
-    }
+    for (int j = 0; j < 4; ++j)
+      boff[j] = t <= lim[j] ? b0[j] + tb : (t == e[j] ? b1[j] : 0u);
     uint32_t off[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -1038,6 +1045,8 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
         dma16_s_nt(dsh, off[i], lds_addr(lds[stg][1] + r0 * ROWB));
       }
     }
+    krow += 32;
+    tb += DS_BLOCK_BYTES;
   };
 #pragma unroll
   for (int t = 0; t < DQ_STAGES - 1; ++t)
@@ -1052,11 +1061,9 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
     __syncthreads();
     // the stage of key tile t - 1 is free: key tile t + DQ_STAGES - 1 goes there
     if (t + DQ_STAGES - 1 < n) issue(t + DQ_STAGES - 1);
-    const int r = t >= n0, kt = stream_tile(t);
     const char* kt_lds = lds[t % DQ_STAGES][0];
     const char* st_lds = lds[t % DQ_STAGES][1];
-    const bool ok0 = in_range(kt, r ? eq0 : 0, r ? eq0 : lim0);
-    const bool ok1 = in_range(kt, r ? eq1 : 0, r ? eq1 : lim1);
+    const bool ok0 = t <= lim0 || t == e0, ok1 = t <= lim1 || t == e1;
     if (!ok0 && !ok1) continue;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
