@@ -85,16 +85,29 @@ class FusedAdamW(torch.optim.Optimizer):
                 total += p.numel() * (8 if p.dtype == torch.float32 else 12)
         return total
 
+    def _arena_engine(self):
+        """The bound model's engine when its float32 arena holds the gradients
+        of a backward since the last zero_grad (else None)."""
+        engine = self._bound_engine()
+        return engine if engine is not None and engine.grads_pending else None
+
+    def _has_grads(self):
+        """Whether a step has gradients to apply: the bound arena's, or any
+        ``.grad`` (a backward that ran before this optimizer was bound fills
+        ``.grad``, as an unbound model always does)."""
+        return (self._arena_engine() is not None
+                or any(p.grad is not None for p in self._params()))
+
     def _grads(self, params):
         """(gradient tensors, dtype code) for ``params``: the bound model's
-        float32 arena views, or ``.grad`` (zeros where unset).  None when the
-        bound model holds no gradients since the last zero_grad."""
-        engine = self._bound_engine()
+        float32 arena views, or ``.grad`` (zeros where unset).  None when there
+        are no gradients since the last zero_grad."""
+        engine = self._arena_engine()
         if engine is not None:
-            if not engine.grads_pending:
-                return None, None
             return ([engine.arena.view(engine.grads, self._names[id(p)]) for p in params],
                     _lib.F32_CODE)
+        if self._bound_engine() is not None and not self._has_grads():
+            return None, None
         grads = [p.grad if p.grad is not None else torch.zeros_like(p) for p in params]
         for g in grads:
             if g.dtype != self._dtype or not g.is_contiguous():
@@ -222,7 +235,7 @@ class FusedAdamW(torch.optim.Optimizer):
     def step(self, closure=None):
         loss = closure() if closure is not None else None
         self._check_tables()
-        if self._bound_engine() is not None and not self._bound_engine().grads_pending:
+        if self._bound_engine() is not None and not self._has_grads():
             # no gradients since zero_grad: nothing to update (torch's AdamW
             # skips parameters whose .grad is None)
             return loss

@@ -201,3 +201,41 @@ def test_unbound_optimizer_rebuilds_tables_when_parameters_move():
     opt.step()
     torch.cuda.synchronize()
     assert not torch.equal(p.detach(), first)
+
+
+def test_optimizer_created_after_backward_applies_grad():
+    """A FusedAdamW created after the backward (which then filled .grad, as
+    for any model without a bound optimizer) steps on those .grad values, as
+    torch.optim.AdamW would; after zero_grad a step changes nothing; the next
+    backward goes to the float32 arena the optimizer now reads."""
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    model, obj, ids, bounds = _tiny_bf16(seed=8)
+    kw = _step_inputs(obj, ids, bounds, 8)
+    loss, _ = model(ids.to(DEV), ids.to(DEV), bounds, **kw)
+    loss.backward()
+    grads = {n: p.grad.float().clone() for n, p in model.named_parameters()}
+    opt = FusedAdamW(param_groups(model, 0.01), lr=1e-3, max_grad_norm=1.0)
+    masters0 = {n: p.detach().float().clone() for n, p in model.named_parameters()}
+    opt.step()
+    torch.cuda.synchronize()
+    norm = float(torch.sqrt(sum((g.double() ** 2).sum() for g in grads.values())))
+    assert float(opt.last_grad_norm) == pytest.approx(norm, rel=1e-5)
+    clip = min(1.0, 1.0 / (norm + 1e-6))
+    groups = {id(p): grp["weight_decay"] for grp in opt.param_groups for p in grp["params"]}
+    for name, p in model.named_parameters():
+        gi = grads[name].double() * clip
+        want = masters0[name].double() * (1 - 1e-3 * groups[id(p)]) - 1e-3 * gi / (gi.abs() + 1e-8)
+        torch.testing.assert_close(opt.state[p]["master"].double(), want, atol=2e-6, rtol=1e-5,
+                                   msg=name)
+    opt.zero_grad(set_to_none=True)
+    before = {n: p.detach().clone() for n, p in model.named_parameters()}
+    opt.step()
+    torch.cuda.synchronize()
+    assert all(torch.equal(p.detach(), before[n]) for n, p in model.named_parameters())
+    loss, _ = model(ids.to(DEV), ids.to(DEV), bounds, **kw)
+    loss.backward()
+    assert all(p.grad is None for p in model.parameters())
+    assert model.float32_grads() is not None
+    opt.step()
+    torch.cuda.synchronize()
+    assert not torch.equal(model.exit_gate.net.weight.detach(), before["exit_gate.net.weight"])
