@@ -87,6 +87,59 @@ __device__ __forceinline__ void dload4(char* tile, int r0, const bf16_t* g, int6
   dma16_v(g + gr * ld + c * 8, lds_addr(tile + r0 * ROWB));
 }
 
+// A 64-key K/V tile pair (forward / dQ) by direct loads.  Load i of wavefront
+// w fills tile rows x = 16 w + 4 i + lane / 16, 16-byte slot lane % 16, i.e.
+// logical chunk (lane % 16) ^ swz(x) of the key's K / V row; the per-lane
+// byte offsets of those chunks from the tile's first row are fixed for the
+// whole walk (kv_lane_offsets), so a tile costs no vector arithmetic: the
+// first rows' addresses are scalar pairs and the eight loads share one M0
+// save.  l0 is the wavefront's first K row in the stage (its V rows follow
+// KT rows later).  Every row of the tile must exist (first row + KT <= N).
+struct KVLanes {
+  uint32_t k[4], v[4];
+};
+__device__ __forceinline__ KVLanes kv_lane_offsets(int wave, int lane, int64_t ldk, int64_t ldv) {
+  KVLanes o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int x = wave * 16 + 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ swz(x);
+    o.k[i] = (uint32_t)((x * ldk + c * 8) * 2);
+    o.v[i] = (uint32_t)((x * ldv + c * 8) * 2);
+  }
+  return o;
+}
+__device__ __forceinline__ void issue_kv64(uint32_t l0, const bf16_t* kb, const bf16_t* vb,
+                                           const KVLanes& o) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %[sv], m0\n\t"
+      "s_mov_b32 m0, %[l0]\n\t"
+      "global_load_lds_dwordx4 %[k0], %[kb]\n\t"
+      "s_add_u32 m0, %[l0], %[r4]\n\t"
+      "global_load_lds_dwordx4 %[k1], %[kb]\n\t"
+      "s_add_u32 m0, %[l0], %[r8]\n\t"
+      "global_load_lds_dwordx4 %[k2], %[kb]\n\t"
+      "s_add_u32 m0, %[l0], %[r12]\n\t"
+      "global_load_lds_dwordx4 %[k3], %[kb]\n\t"
+      "s_add_u32 m0, %[l0], %[vr0]\n\t"
+      "global_load_lds_dwordx4 %[v0], %[vb]\n\t"
+      "s_add_u32 m0, %[l0], %[vr4]\n\t"
+      "global_load_lds_dwordx4 %[v1], %[vb]\n\t"
+      "s_add_u32 m0, %[l0], %[vr8]\n\t"
+      "global_load_lds_dwordx4 %[v2], %[vb]\n\t"
+      "s_add_u32 m0, %[l0], %[vr12]\n\t"
+      "global_load_lds_dwordx4 %[v3], %[vb]\n\t"
+      "s_mov_b32 m0, %[sv]"
+      : [sv] "=&s"(saved)
+      : [l0] "s"(l0), [kb] "s"(kb), [vb] "s"(vb), [k0] "v"(o.k[0]), [k1] "v"(o.k[1]),
+        [k2] "v"(o.k[2]), [k3] "v"(o.k[3]), [v0] "v"(o.v[0]), [v1] "v"(o.v[1]),
+        [v2] "v"(o.v[2]), [v3] "v"(o.v[3]), [r4] "n"(4 * ROWB), [r8] "n"(8 * ROWB),
+        [r12] "n"(12 * ROWB), [vr0] "n"(KT * ROWB), [vr4] "n"((KT + 4) * ROWB),
+        [vr8] "n"((KT + 8) * ROWB), [vr12] "n"((KT + 12) * ROWB)
+      : "memory");
+}
+
 // A/B operand fragment from a row: 8 bf16 of chunk `chunk` of tile row `row`.
 __device__ __forceinline__ bf16x8_t row_frag(const char* tile, int row, int chunk) {
   return *reinterpret_cast<const bf16x8_t*>(tile + row * ROWB + ((chunk ^ swz(row)) << 4));
@@ -197,12 +250,19 @@ fa128_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const Interval2 first = keys_of_query(T.start, true, L, B), last = keys_of_query(T.q1 - 1, true, L, B);
   const bf16_t* kh = k + hk * HD;
   const bf16_t* vh = v + hk * HD;
+  const KVLanes kvo = kv_lane_offsets(wave, lane, ldk, ldv);
+  const uint32_t lds_w = lds_addr(lds) + (uint32_t)(wave * 16 * ROWB);  // this wave's rows
   auto issue = [&](int stg, int k0) {
+    const int64_t row0 = base + k0;
+    if (row0 + KT <= N) {
+      issue_kv64(lds_w + (uint32_t)(stg * (2 * KT * ROWB)), kh + row0 * ldk, vh + row0 * ldv, kvo);
+    } else {  // keys past the pack's last row re-read it (they are masked)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r0 = wave * 16 + i * 4;
-      dload4(lds[stg][0], r0, kh, ldk, base + k0, N - 1, lane);
-      dload4(lds[stg][1], r0, vh, ldv, base + k0, N - 1, lane);
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = wave * 16 + i * 4;
+        dload4(lds[stg][0], r0, kh, ldk, row0, N - 1, lane);
+        dload4(lds[stg][1], r0, vh, ldv, row0, N - 1, lane);
+      }
     }
   };
   int r, k0;
@@ -350,12 +410,19 @@ fa128_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const Interval2 first = keys_of_query(T.start, true, L, B), last = keys_of_query(T.q1 - 1, true, L, B);
   const bf16_t* kh = k + hk * HD;
   const bf16_t* vh = v + hk * HD;
+  const KVLanes kvo = kv_lane_offsets(wave, lane, ldk, ldv);
+  const uint32_t lds_w = lds_addr(lds) + (uint32_t)(wave * 16 * ROWB);  // this wave's rows
   auto issue = [&](int stg, int k0) {
+    const int64_t row0 = base + k0;
+    if (row0 + KT <= N) {
+      issue_kv64(lds_w + (uint32_t)(stg * (2 * KT * ROWB)), kh + row0 * ldk, vh + row0 * ldv, kvo);
+    } else {  // keys past the pack's last row re-read it (they are masked)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r0 = wave * 16 + i * 4;
-      dload4(lds[stg][0], r0, kh, ldk, base + k0, N - 1, lane);
-      dload4(lds[stg][1], r0, vh, ldv, base + k0, N - 1, lane);
+      for (int i = 0; i < 4; ++i) {
+        const int r0 = wave * 16 + i * 4;
+        dload4(lds[stg][0], r0, kh, ldk, row0, N - 1, lane);
+        dload4(lds[stg][1], r0, vh, ldv, row0, N - 1, lane);
+      }
     }
   };
   int r, k0;
