@@ -504,13 +504,21 @@ bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int6
   return true;
 }
 
-// Splits of K for ALODLM_EPI_ACCUM products with few output tiles.
+// Splits of K for ALODLM_EPI_ACCUM products with few output tiles: the
+// fewest (powers of two up to 8, each split keeping >= 32 k stages) whose
+// rounds of 256 workgroups (one per CU) cost the least per unit of work.
+// Splits that only add rounds cost float partials and their reduction: the
+// 1.7B step's dW of the QKV and O projections take 2 and 4 splits (one
+// round), 22 us faster each than at 4 and 8.
 int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
   const int64_t ksteps = K / KMIN;
-  int64_t s = 1;
-  while (tiles * s < 512 && ksteps / (s * 2) >= 32) s *= 2;
-  return s;
+  const int64_t cus = 256;
+  auto cost = [&](int64_t s) { return (double)((tiles * s + cus - 1) / cus) / (double)s; };
+  int64_t best = 1;
+  for (int64_t s = 2; s <= 8 && ksteps / s >= 32; s *= 2)
+    if (cost(s) < 0.98 * cost(best)) best = s;
+  return best;
 }
 
 // Splits of a bf16-output (STORE) product: the fewest that bring the rounds

@@ -471,6 +471,7 @@ def run_gemm(spec, device, steps, warmup):
     shapes = [("qkv_fwd", N, QW, H, 1, 0, E[0]), ("o_fwd", N, H, QD, 1, 0, E[1]),
               ("gate_up_fwd", N, 2 * I, H, 1, 0, E[0]), ("down_fwd", N, H, I, 1, 0, E[1]),
               ("dx_gate_up", N, H, 2 * I, 1, 0, E[0]), ("dx_down", N, I, H, 1, 0, E[0]),
+              ("dw_qkv", QW, H, N, 0, 0, E[2]), ("dw_o", H, QD, N, 0, 0, E[2]),
               ("dw_gate_up", 2 * I, H, N, 0, 0, E[2]), ("dw_down", H, I, N, 0, 0, E[2])]
     g = torch.Generator(device=device).manual_seed(7)
     st = _lib.stream_handle(device)

@@ -252,6 +252,9 @@ ATTN_CASES = [
     (torch.bfloat16, 2, 2, 64, [0, 200, 390], 24, "mfma"),
     (torch.bfloat16, 2, 1, 128, [0, 1024], 32, "mfma"),
     (torch.bfloat16, 4, 2, 128, [0, 512, 1000, 1001], 32, "mfma"),
+    # 21 heads: the q/k-norm kernels load several groups of four heads per
+    # pass (a partial last group, and more than one pass per row)
+    (torch.bfloat16, 18, 3, 128, [0, 100, 133], 32, "mfma"),
     # head_dim 128 with the dQ pass that recomputes S, P and dP (no stored dS)
     (torch.bfloat16, 4, 1, 128, [0, 300, 333], 32, "mfma-recompute"),
     (torch.bfloat16, 4, 2, 128, [0, 512, 1000, 1001], 32, "mfma-recompute"),
