@@ -930,7 +930,7 @@ fa128_dkdv_reduce_kernel(const float* __restrict__ partial, int group, int64_t N
 // delta[h, r] = sum_e dO[r, h, e] O[r, h, e] and lse2[h, r] = lse[h, r] log2(e)
 // (what the dK/dV pass reads when it runs first), and the dK/dV work counter
 // zeroed.  16 lanes per (head, row), 8 head_dim values each; items are
-// head-major so that a workgroup writes 16 consecutive rows of one head.
+// row-major so that a workgroup reads whole rows of dO and O.
 __global__ void __launch_bounds__(256)
 fa128_bwd_prep_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ dout,
                       const float* __restrict__ lse, float* __restrict__ delta, int64_t N, int nq,
@@ -939,8 +939,9 @@ fa128_bwd_prep_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ d
   const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   if (item >= N * nq) return;
   const int sub = threadIdx.x & 15;
-  const int h = (int)(item / N);
-  const int64_t r = item - (int64_t)h * N;
+  // row-major items: a workgroup reads whole rows (all heads), contiguous
+  const int64_t r = item / nq;
+  const int h = (int)(item - r * nq);
   const int64_t off = r * nq * HD + (int64_t)h * HD + sub * 8;
   float a[8], b[8];
   Vec8<bf16_t>::load(o + off, a);
@@ -951,8 +952,9 @@ fa128_bwd_prep_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ d
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1) s += __shfl_xor(s, w, 16);
   if (sub == 0) {
-    delta[item] = s;
-    delta[N * nq + item] = lse[item] * FA_LOG2E;
+    const int64_t hr = (int64_t)h * N + r;  // [head][row] layout
+    delta[hr] = s;
+    delta[N * nq + hr] = lse[hr] * FA_LOG2E;
   }
 }
 
