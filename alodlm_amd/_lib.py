@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -71,7 +71,7 @@ SIGNATURES = {
     "alodlm_decode_begin": [P, P, I64, I64, P],
     "alodlm_decode_commit": [P, P, I64, I64, I32, P],
     "alodlm_objective_workspace": [I64, I64, I64],
-    "alodlm_objective": [P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P],
+    "alodlm_objective": [P, P, P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P, P],
     "alodlm_outcome_loss": [P, P, P, P, P, P, I64, I64, I64, F32, F32, F32, P, P, P, P, P],
     "alodlm_masked_sequence_ids": [P, P, I64, I64, P, P, P],
     "alodlm_sequence_score": [P, P, P, I64, I64, P, P, P, P],
@@ -83,7 +83,10 @@ SIGNATURES = {
                      P],
     "alodlm_cast_f32": [P, P, P, I64, I32, P],
     "alodlm_scale_f32": [P, P, I64, P],
+    "alodlm_scale": [P, P, I64, I32, P],
+    "alodlm_scale_add_f32": [P, P, I64, P, I32, P],
     "alodlm_transpose": [P, P, I64, I64, I32, P],
+    "alodlm_transpose_checked": [P, P, I64, I64, I32, P, P],
 }
 _RESTYPE = {
     "alodlm_last_error": ctypes.c_char_p,

@@ -81,16 +81,22 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restric
 // distinct banks).  One workgroup of 256 threads per tile.
 template <typename T>
 __global__ void __launch_bounds__(256)
-transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols) {
+transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols,
+                 int32_t* __restrict__ nonfinite) {
   __shared__ T tile[64][65];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  bool bad = false;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int rr = ty + 4 * i;
     const int64_t r = r0 + rr, c = c0 + tx;
-    if (r < rows && c < cols) tile[rr][tx] = src[r * cols + c];
+    if (r < rows && c < cols) {
+      tile[rr][tx] = src[r * cols + c];
+      bad |= !isfinite(Elem<T>::load(src, r * cols + c));
+    }
   }
+  if (nonfinite != nullptr && bad) *nonfinite = 1;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -105,17 +111,27 @@ transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, i
 // per tile row on the way in, 8 per transposed row on the way out).
 __global__ void __launch_bounds__(256)
 transpose16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t rows,
-                   int64_t cols) {
+                   int64_t cols, int32_t* __restrict__ nonfinite) {
   __shared__ uint16_t tile[64][64 + 8];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int t = threadIdx.x, part = (t & 7) * 8;
+  uint32_t bad = 0;
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     const int rr = (t >> 3) + 32 * pass;
     const int64_t r = r0 + rr, c = c0 + part;
-    if (r < rows && c < cols)
-      *reinterpret_cast<uint4*>(&tile[rr][part]) = *reinterpret_cast<const uint4*>(src + r * cols + c);
+    if (r < rows && c < cols) {
+      const uint4 v = *reinterpret_cast<const uint4*>(src + r * cols + c);
+      *reinterpret_cast<uint4*>(&tile[rr][part]) = v;
+      // a bf16 element is inf or NaN when its exponent bits are all ones:
+      // 0x7f80 in either half of a 32-bit word
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        bad |= ((w[e] & 0x7f80u) == 0x7f80u) | ((w[e] & 0x7f800000u) == 0x7f800000u);
+    }
   }
+  if (nonfinite != nullptr && bad) *nonfinite = 1;
   __syncthreads();
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
@@ -162,6 +178,39 @@ __global__ void scale_kernel(float* __restrict__ x, const float* __restrict__ s,
   const float k = s[0];
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] *= k;
+}
+
+// x *= s[0] in the storage dtype (rounded once per element).
+template <typename T>
+__global__ void scale_any_kernel(T* __restrict__ x, const float* __restrict__ s, int64_t n) {
+  const float k = s[0];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    Elem<T>::store(x, i, Elem<T>::load(x, i) * k);
+}
+
+// y = s[0] * x + (accumulate ? y : 0) in float32, four elements per thread
+// and step where both are 16-byte aligned (the tail takes the rest).
+__global__ void scale_add_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                 const float* __restrict__ s, int64_t n, int accumulate) {
+  const float k = s ? s[0] : 1.0f;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t head = 0;
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0) {
+    head = n / 4 * 4;
+    for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < head;
+         i += stride * 4) {
+      const float4 a = *reinterpret_cast<const float4*>(x + i);
+      float4 b = accumulate ? *reinterpret_cast<const float4*>(y + i) : make_float4(0, 0, 0, 0);
+      b.x += k * a.x;
+      b.y += k * a.y;
+      b.z += k * a.z;
+      b.w += k * a.w;
+      *reinterpret_cast<float4*>(y + i) = b;
+    }
+  }
+  for (int64_t i = head + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (accumulate ? y[i] : 0.0f) + k * x[i];
 }
 
 // Blocks of 256 for a grid-stride sweep over n elements (at most 8 per CU slot
@@ -217,6 +266,11 @@ extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, vo
 
 extern "C" int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
                                 void* stream) {
+  return alodlm_transpose_checked(src, dst, rows, cols, dtype, nullptr, stream);
+}
+
+extern "C" int alodlm_transpose_checked(const void* src, void* dst, int64_t rows, int64_t cols,
+                                        int dtype, int32_t* nonfinite, void* stream) {
   ALODLM_CHECK_ARG(rows >= 0 && cols >= 0, "transpose: negative shape");
   ALODLM_CHECK_ARG(rows <= 64 * 65535LL, "transpose: too many rows");
   if (rows == 0 || cols == 0) return ALODLM_OK;
@@ -225,12 +279,13 @@ extern "C" int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_
   if (dtype == ALODLM_BF16 && rows % 8 == 0 && cols % 8 == 0 &&
       ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
     transpose16_kernel<<<grid, 256, 0, as_stream(stream)>>>((const uint16_t*)src, (uint16_t*)dst,
-                                                            rows, cols);
+                                                            rows, cols, nonfinite);
     ALODLM_CHECK_LAUNCH("transpose");
     return ALODLM_OK;
   }
   ALODLM_DISPATCH(dtype, T, {
-    transpose_kernel<T><<<grid, 256, 0, as_stream(stream)>>>((const T*)src, (T*)dst, rows, cols);
+    transpose_kernel<T><<<grid, 256, 0, as_stream(stream)>>>((const T*)src, (T*)dst, rows, cols,
+                                                             nonfinite);
   });
   ALODLM_CHECK_LAUNCH("transpose");
   return ALODLM_OK;
@@ -250,5 +305,25 @@ extern "C" int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* s
   if (n == 0) return ALODLM_OK;
   scale_kernel<<<sweep_blocks(n), 256, 0, as_stream(stream)>>>(x, scale, n);
   ALODLM_CHECK_LAUNCH("scale_f32");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_scale(void* x, const float* scale, int64_t n, int dtype, void* stream) {
+  ALODLM_CHECK_ARG(n >= 0 && scale != nullptr, "scale: bad arguments");
+  if (n == 0) return ALODLM_OK;
+  ALODLM_DISPATCH(dtype, T, {
+    scale_any_kernel<T><<<sweep_blocks(n), 256, 0, as_stream(stream)>>>((T*)x, scale, n);
+  });
+  ALODLM_CHECK_LAUNCH("scale");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_scale_add_f32(const float* x, float* y, int64_t n, const float* scale,
+                                    int accumulate, void* stream) {
+  ALODLM_CHECK_ARG(n >= 0, "scale_add_f32: negative size");
+  if (n == 0) return ALODLM_OK;
+  scale_add_kernel<<<sweep_blocks((n + 3) / 4), 256, 0, as_stream(stream)>>>(x, y, scale, n,
+                                                                              accumulate);
+  ALODLM_CHECK_LAUNCH("scale_add_f32");
   return ALODLM_OK;
 }

@@ -32,7 +32,7 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
                  const int32_t* __restrict__ ar_target, const int64_t* __restrict__ bounds,
                  int64_t S, int64_t rows, int K, float prior_c, float beta_mi, float beta_marg,
                  float* __restrict__ out, float* __restrict__ dgate, float* __restrict__ dce,
-                 float dgate_scale, float* __restrict__ ws) {
+                 float dgate_scale, float* __restrict__ ws, const int32_t* __restrict__ nonfinite) {
   __shared__ float scratch[16];
   __shared__ float qbar_log[OBJ_MAX_DEPTH], prior_log[OBJ_MAX_DEPTH];
   __shared__ float sh_M, sh_wsum;
@@ -180,7 +180,11 @@ objective_kernel(const float* __restrict__ gates, const int32_t* __restrict__ ex
       h0m = H0 / M;
     }
     float total = ((den_v + act_v) + ar) / 2.f;
-    if (BAD > 0.f) total = NAN;  // 0 * sum(gates) propagates non-finite gates (model.py:186)
+    // 0 * sum(logits + gates) (model.py:186): a non-finite gate, or a
+    // non-finite LM-head weight (whose logits column is then non-finite in
+    // every row), makes the loss NaN; a non-finite readout row makes its gate
+    // logit non-finite
+    if (BAD > 0.f || (nonfinite != nullptr && *nonfinite != 0)) total = NAN;
     out[0] = total;
     out[1] = den_v;
     out[2] = act_v;
@@ -204,14 +208,15 @@ extern "C" int alodlm_objective(const float* gates, const int32_t* exits, const 
                                 const int32_t* ar_target, const int64_t* bounds,
                                 int64_t n_segments, int64_t rows, int64_t max_depth,
                                 float depth_prior_c, float kl_beta_mi, float kl_beta_marg,
-                                float* out, float* dgate, float* workspace, void* stream) {
+                                const int32_t* nonfinite, float* out, float* dgate,
+                                float* workspace, void* stream) {
   ALODLM_CHECK_ARG(max_depth >= 2 && max_depth <= OBJ_MAX_DEPTH,
                    "objective: max_depth must be in [2, %d]", OBJ_MAX_DEPTH);
   ALODLM_CHECK_ARG(rows > 0 && n_segments > 0, "objective: empty input");
   objective_kernel<<<1, OBJ_THREADS, 0, as_stream(stream)>>>(
       gates, exits, masked, mask_prob, ce_full, ar_ce, ar_target, bounds, n_segments, rows,
       (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, nullptr, 0.5f,
-      workspace);
+      workspace, nonfinite);
   ALODLM_CHECK_LAUNCH("objective");
   return ALODLM_OK;
 }
@@ -227,7 +232,8 @@ extern "C" int alodlm_outcome_loss(const float* gates, const int32_t* exits, con
   ALODLM_CHECK_ARG(rows > 0 && n_segments > 0, "outcome_loss: empty input");
   objective_kernel<<<1, OBJ_THREADS, 0, as_stream(stream)>>>(
       gates, exits, masked, mask_prob, ce_full, nullptr, nullptr, bounds, n_segments, rows,
-      (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, dce, 1.0f, workspace);
+      (int)max_depth, depth_prior_c, kl_beta_mi, kl_beta_marg, out, dgate, dce, 1.0f, workspace,
+      nullptr);
   ALODLM_CHECK_LAUNCH("outcome_loss");
   return ALODLM_OK;
 }

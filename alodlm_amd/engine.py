@@ -7,9 +7,11 @@ launches on the current stream:
 forward   weight transposes -> embed -> prelude -> for each depth: (re-embed/carry) -> core -> coda
           -> final norm + gate -> exit sampling -> loss-bearing row selection
           -> LM head GEMM -> vocabulary CE (writes dL/dlogits in place)
+          -> LM head dX/dW (dL/dlogits is final at its depth)
           -> objective kernel (loss, metrics, dL/dgate)
-backward  per depth in reverse: LM head dX/dW -> gate head -> final norm ->
-          coda -> carry/re-embed -> core; then prelude and the embedding.
+backward  upstream gradient -> LM head gradient into the arena; per depth in
+          reverse: gate head -> final norm -> coda -> carry/re-embed -> core;
+          then prelude and the embedding.
 
 Activation policy: every layer application keeps its input, the q|k|v
 projections, the attention output and log-sum-exp, the post-attention
@@ -23,6 +25,12 @@ Parameters live in one contiguous arena per step engine (q|k|v and gate|up of
 every layer adjacent, so each pair is one GEMM); gradients accumulate in a
 float32 arena with the same offsets and are returned to autograd in the
 parameter dtype.
+
+Memory that varies from step to step (the loss-bearing row count of each
+depth) never sizes an allocation: one depth's logits live in a persistent
+buffer for the pack's row count, and the LM head's backward consumes them at
+that depth, so every allocation of a step has the same size at every step of
+the same pack shape and the caching allocator reuses its blocks.
 """
 
 from dataclasses import dataclass
@@ -175,10 +183,20 @@ class _TransposedWeights:
             dst = self.buf[off:off + src.numel()].view(cols, rows)
             setattr(owner, name, dst)
             self.jobs.append((src, dst, rows, cols))
+        # set by the refresh when an LM-head weight is inf or NaN: every row's
+        # logits then hold a non-finite column, which makes the reference's
+        # loss NaN through its 0 * sum(logits) term (alodlm/model.py:186)
+        self.nonfinite = torch.zeros(1, dtype=torch.int32, device=engine.device)
 
     def refresh(self, code, stream):
-        for src, dst, rows, cols in self.jobs:
-            call("alodlm_transpose", ptr(src), ptr(dst), rows, cols, code, stream)
+        self.nonfinite.zero_()
+        last = len(self.jobs) - 1
+        for i, (src, dst, rows, cols) in enumerate(self.jobs):
+            if i == last:   # the LM head
+                call("alodlm_transpose_checked", ptr(src), ptr(dst), rows, cols, code,
+                     ptr(self.nonfinite), stream)
+            else:
+                call("alodlm_transpose", ptr(src), ptr(dst), rows, cols, code, stream)
 
 
 class StepEngine(Kernels):
@@ -224,19 +242,22 @@ class StepEngine(Kernels):
         self.fused_optimizer = None
         self.grads_pending = False
         self._written = None
+        # the readout's persistent buffers (_readout_buffers)
+        self._readout = None
 
     # ------------------------------------------------------------------ memory policy
-    KEEP_FRACTION = 0.95  # of the device memory a step may plan to use
+    KEEP_MARGIN = 0.06  # of the device memory left unplanned (allocator fragmentation)
 
     def _decide_keep(self, N):
         """(keep rotary q/k, keep norm outputs) for this step.  The first step
         keeps neither and measures how far its forward and backward raise the
         allocated memory (the device's peak statistics are reset at its start);
-        the second step decides once, keeping each set only if the allocations
-        live at its start, plus that growth, plus optimizer state still to be
-        allocated (the decision can precede the first optimizer step under
-        gradient accumulation), plus the set's bytes stay under KEEP_FRACTION
-        of the device."""
+        the second step decides once, keeping each set only if that growth,
+        plus optimizer state still to be allocated (the decision can precede
+        the first optimizer step under gradient accumulation), plus the set's
+        bytes fit in what this process can still allocate - the device's free
+        memory (memory other processes hold is not free) plus the blocks the
+        caching allocator holds unused - less KEEP_MARGIN of the device."""
         dev = self.device
         if self._keep is not None:
             # a pack with more rows than the one the decision was made for
@@ -250,19 +271,22 @@ class StepEngine(Kernels):
         if self._step_peak is None:  # the first step ran no backward
             return (False, False)
         growth = self._step_peak - self._step_alloc
-        budget = self.KEEP_FRACTION * torch.cuda.get_device_properties(dev).total_memory
+        allocated = torch.cuda.memory_allocated(dev)
+        cached = torch.cuda.memory_reserved(dev) - allocated
+        free, total = torch.cuda.mem_get_info(dev)
+        headroom = free + cached - self.KEEP_MARGIN * total
         d, cfg = self.dims, self.cfg
         apps = cfg.loop_start + cfg.max_depth * (d.layers - cfg.loop_start)
         elem = 2 if self.dtype == torch.bfloat16 else 4
         rotary = apps * N * (d.heads + d.kv_heads) * d.head_dim * elem
         norms = apps * N * 2 * d.hidden * elem
-        used = torch.cuda.memory_allocated(dev) + growth + self._optimizer_state_to_come()
+        need = growth + self._optimizer_state_to_come()
         if not self._grads_existed and self.grads is not None:
             # the float32 gradient arena was allocated during the first step:
-            # it is in both the growth and the memory now allocated
-            used -= self.grads.numel() * 4
-        keep_rot = used + rotary <= budget
-        keep_norm = keep_rot and used + rotary + norms <= budget
+            # it is in the growth and already allocated now
+            need -= self.grads.numel() * 4
+        keep_rot = need + rotary <= headroom
+        keep_norm = keep_rot and need + rotary + norms <= headroom
         self._keep = (keep_rot, keep_norm)
         self._keep_rows = N
         return self._keep
@@ -340,11 +364,33 @@ class StepEngine(Kernels):
                  depth, K, N, st)
         return readout
 
-    def _lm_readout(self, readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad, rec):
+    def _readout_buffers(self, N):
+        """Persistent buffers of the readout for packs of N rows: the logits
+        of one depth's loss-bearing rows ([R, V], R <= N, rounded up to 32),
+        the gathered rows and their input gradient.  Allocated once per pack
+        size, so the step's largest allocation has the same size at every
+        step whatever the loss-bearing row counts."""
+        cap = -(-N // 32) * 32
+        if self._readout is None or self._readout[0] != cap:
+            self._readout = None
+            H, V = self.dims.hidden, self.dims.vocab
+            self._readout = (cap, self._empty(cap, V), self._empty(cap, H), self._empty(cap, H))
+        return self._readout[1:]
+
+    def _lm_readout(self, readout, depth, gates, exits, b, wsum, ar_coef, ce_all, ent_all,
+                    need_grad, rec, g_lm=None, lm_first=True):
         """Loss-bearing rows of pass ``depth`` through the LM head and the
         vocabulary cross-entropy (alodlm/model.py:161,180-181; loss.py:12-32):
         rows are selected and weighted by alodlm_select_rows, their logits
-        become dL/dlogits in place."""
+        become dL/dlogits in place (with a unit upstream gradient), and each
+        row's cross-entropy and token entropy -sum p log p (the decoder's
+        commit score, alodlm/inference.py:114-117) land in row order in
+        ``ce_all[depth]`` / ``ent_all[depth]``.  That
+        gradient is final here, so with ``need_grad`` the LM head's backward
+        runs right away: the readout gradient [N, H] is kept in ``rec`` and
+        the LM head's weight gradient goes into the float32 ``g_lm`` (written
+        when ``lm_first``, else accumulated).  Returns whether it wrote
+        ``g_lm``."""
         d, K = self.dims, self.cfg.max_depth
         N, H = readout.shape
         V = d.vocab
@@ -358,24 +404,39 @@ class StepEngine(Kernels):
              ptr(sel_target), ptr(sel_coef), ptr(sel_count), st)
         R = int(sel_count.item())
         rec["R"], rec["sel_rows"] = R, sel_rows
-        if R:
-            # Rows padded to a multiple of 32 with zeros: their logits and
-            # dL/dlogits are exactly zero, and the LM-head dW product (whose
-            # depth is the row count) runs on whole 32-deep k stages.
-            Rp = -(-R // 32) * 32
-            xsel = self._empty(Rp, H)
-            if Rp > R:
-                xsel[R:].zero_()
-            call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
-            logits = self._empty(Rp, V)
-            self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
-            ce = torch.empty(R, dtype=torch.float32, device=self.device)
-            call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
-                 ptr(sel_count), R, V, ptr(ce), None, c, st)
-            call("alodlm_scatter_ce", ptr(ce), ptr(sel_rows), ptr(sel_count), R,
-                 ptr(ce_all[depth]), N, st)
+        if need_grad:
+            rec["dread"] = self._empty(N, H)
+        if not R:
             if need_grad:
-                rec["xsel"], rec["dlogits"] = xsel, logits
+                rec["dread"].zero_()
+            return False
+        # Rows padded to a multiple of 32 with zeros: their logits and
+        # dL/dlogits are exactly zero, and the LM-head dW product (whose
+        # depth is the row count) runs on whole 32-deep k stages.
+        Rp = -(-R // 32) * 32
+        logits_buf, xsel_buf, dsel_buf = self._readout_buffers(N)
+        xsel = xsel_buf[:Rp]
+        if Rp > R:
+            xsel[R:].zero_()
+        call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
+        logits = logits_buf[:Rp]
+        self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
+        ce = torch.empty(2, R, dtype=torch.float32, device=self.device)
+        call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
+             ptr(sel_count), R, V, ptr(ce[0]), ptr(ce[1]), c, st)
+        call("alodlm_scatter_ce", ptr(ce[0]), ptr(sel_rows), ptr(sel_count), R,
+             ptr(ce_all[depth]), N, st)
+        call("alodlm_scatter_ce", ptr(ce[1]), ptr(sel_rows), ptr(sel_count), R,
+             ptr(ent_all[depth]), N, st)
+        if not need_grad:
+            return False
+        # d readout = dlogits . W_lm ; dW_lm (+)= dlogits^T . readout
+        dsel = dsel_buf[:R]
+        self._gemm(logits, V, 1, self.lm_head, H, 0, dsel, H, R, H, V)
+        self._gemm(logits, V, 0, xsel, H, 0, g_lm, H, V, H, Rp,
+                   epi=EPI_STORE_F32 if lm_first else EPI_ACCUM)
+        call("alodlm_scatter_rows", ptr(dsel), ptr(sel_rows), R, ptr(rec["dread"]), N, H, c, st)
+        return True
 
     def _objective(self, gates, exits, b, ce_all, N, S, K):
         out = torch.empty(10, dtype=torch.float32, device=self.device)
@@ -384,42 +445,54 @@ class StepEngine(Kernels):
         ws = self._workspace(query("alodlm_objective_workspace", N, S, K))
         call("alodlm_objective", ptr(gates), ptr(exits), ptr(b.masked), ptr(b.mask_probability),
              ptr(ce_all), ptr(ce_all), ptr(b.ar_target), ptr(b.boundaries), S, N, K,
-             cfg.depth_prior_c, cfg.kl_beta_mi, cfg.kl_beta_marg, ptr(out), ptr(dgate), ptr(ws),
-             self._stream())
+             cfg.depth_prior_c, cfg.kl_beta_mi, cfg.kl_beta_marg, ptr(self.transposed.nonfinite),
+             ptr(out), ptr(dgate), ptr(ws), self._stream())
         return out, dgate
 
-    def _readout_bwd(self, rec, depth, dgate, grad_scale, g_lm, g_norm, g_gw, g_gb, g_db,
-                     first_lm=False):
-        """Backward of pass ``depth``'s readout: LM head dX/dW (``first_lm``:
-        the LM head's gradient is written, not accumulated), gate head, final
-        norm; returns d final_in."""
-        d = self.dims
+    def _readout_bwd(self, rec, depth, dgate, scale, g_norm, g_gw, g_gb, g_db):
+        """Backward of pass ``depth``'s readout after the LM head (whose
+        backward ran in the forward): the upstream gradient ``scale`` (a
+        float32 device scalar, or None for 1) applied to the readout
+        gradient, the gate head, the final norm; returns d final_in."""
         N, H = rec["readout"].shape
-        V = d.vocab
         st, c = self._stream(), self.code
-        R = rec["R"]
-        dread = self._empty(N, H)
-        if R:
-            dsel = self._empty(R, H)
-            # d readout = dlogits . W_lm ; dW_lm += dlogits^T . readout
-            self._gemm(rec["dlogits"], V, 1, self.lm_head, H, 0, dsel, H, R, H, V,
-                       alpha=grad_scale)
-            self._gemm(rec["dlogits"], V, 0, rec["xsel"], H, 0, g_lm, H, V, H,
-                       rec["xsel"].shape[0], alpha=grad_scale,
-                       epi=EPI_STORE_F32 if first_lm else EPI_ACCUM)
-            call("alodlm_scatter_rows", ptr(dsel), ptr(rec["sel_rows"]), R, ptr(dread), N, H,
-                 c, st)
-            del dsel
-        else:
-            dread.zero_()
+        dread = rec.pop("dread")
+        if scale is not None:
+            call("alodlm_scale", ptr(dread), ptr(scale), dread.numel(), c, st)
         ws = self._workspace(query("alodlm_gate_bwd_workspace", N, H))
-        call("alodlm_gate_bwd", ptr(dgate), ptr(rec["readout"]), grad_scale, ptr(g_gw), ptr(g_gb),
+        call("alodlm_gate_bwd", ptr(dgate), ptr(rec["readout"]), 1.0, ptr(g_gw), ptr(g_gb),
              ptr(g_db), depth, N, H, ptr(ws), c, st)
         dr = self._empty(N, H)
         ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
         call("alodlm_rmsnorm_bwd", ptr(dread), ptr(rec["final_in"]), ptr(rec["rstd_f"]),
              ptr(self.final_norm), None, ptr(dr), ptr(g_norm), ptr(ws), N, H, c, st)
         return dr
+
+    def _lm_grad_store(self, state, scale, grads, accumulate):
+        """The LM head's weight gradient of the forward (unit upstream
+        gradient, float32) into the arena: scaled by ``scale`` and written,
+        or added under ``accumulate``; zero when no depth had loss-bearing
+        rows."""
+        lo, hi = self.arena.lm_span
+        dst = grads[lo:hi]
+        if state["lm_written"]:
+            call("alodlm_scale_add_f32", ptr(state["g_lm"]), ptr(dst), hi - lo, ptr(scale),
+                 int(accumulate), self._stream())
+        elif not accumulate:
+            dst.zero_()
+        state["g_lm"] = None
+
+    def _upstream(self, grad_scale, dgate):
+        """The upstream gradient of the loss as a float32 device scalar (None
+        for a host 1.0), applied to the gate-logit gradients ``dgate``."""
+        if isinstance(grad_scale, (int, float)):
+            if grad_scale == 1.0:
+                return None
+            scale = torch.tensor([float(grad_scale)], dtype=torch.float32, device=self.device)
+        else:
+            scale = grad_scale.detach().to(device=self.device, dtype=torch.float32).reshape(1)
+        call("alodlm_scale_f32", ptr(dgate), ptr(scale), dgate.numel(), self._stream())
+        return scale
 
     def _grad_views(self, grads):
         a = self.arena
@@ -434,7 +507,6 @@ class StepEngine(Kernels):
         """Run the forward of the step; returns (out[10] float tensor, state)."""
         if not self.arena.valid():
             raise RuntimeError("model parameters were moved after the step engine was built")
-        self._ws = None
         cfg, d = self.cfg, self.dims
         K = cfg.max_depth
         st, c = self._stream(), self.code
@@ -451,6 +523,10 @@ class StepEngine(Kernels):
         N, H, V = b.ids.numel(), d.hidden, d.vocab
         S = b.boundaries.numel() - 1
         saves = [] if need_grad else None
+        # the readout's persistent buffers and this step's LM-head gradient
+        # exist before the keep decision measures the memory
+        self._readout_buffers(N)
+        g_lm = self._empty(V, H, dtype=torch.float32) if need_grad else None
         self._keep_now = self._decide_keep(N) if need_grad else (False, False)
         x = self._empty(N, H)
         call("alodlm_embed_gather", ptr(self.embed), ptr(b.ids), ptr(x), N, H, V, c, st)
@@ -459,11 +535,13 @@ class StepEngine(Kernels):
         gates = torch.empty(K, N, dtype=torch.float32, device=self.device)
         exits = torch.full((N,), K, dtype=torch.int32, device=self.device)
         ce_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
+        ent_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
         wsum = torch.empty(1, dtype=torch.float32, device=self.device)
         call("alodlm_inverse_weight_sum", ptr(b.masked), ptr(b.mask_probability), N, ptr(wsum), st)
         ar_coef = 0.5 / (K * b.ar_count) if b.ar_count else 0.0
         depths = []
         core_in = x
+        lm_written = False
         for depth in range(K):
             rec = {}
             if depth:
@@ -479,21 +557,24 @@ class StepEngine(Kernels):
             for li in range(cfg.loop_end, d.layers):
                 r = self._layer_fwd(li, r, b, rec["coda_saves"])
             readout = self._gate_pass(r, depth, gates, exits, b, exit_uniforms, generator, rec)
-            self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad,
-                             rec)
+            lm_written |= self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all,
+                                           ent_all, need_grad, rec, g_lm, not lm_written)
             depths.append(rec)
         out, dgate = self._objective(gates, exits, b, ce_all, N, S, K)
         self.last_rows = [rec["R"] for rec in depths]
-        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "dgate": dgate,
-                 "prelude": saves, "depths": depths}
+        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "entropy": ent_all,
+                 "dgate": dgate, "prelude": saves, "depths": depths, "g_lm": g_lm,
+                 "lm_written": lm_written}
         return out, state
 
     def backward(self, state, grad_scale, accumulate=False):
         """Backward of the step into the float32 gradient arena ``self.grads``
-        (returned).  Without ``accumulate`` the arena's previous contents are
-        replaced: each matrix's first contribution is written, the embedding
-        and the small tensors are zeroed first; with it every contribution is
-        added (gradient accumulation)."""
+        (returned), for the loss's upstream gradient ``grad_scale`` (a float,
+        or a device scalar that is never read on the host).  Without
+        ``accumulate`` the arena's previous contents are replaced: each
+        matrix's first contribution is written, the embedding and the small
+        tensors are zeroed first; with it every contribution is added
+        (gradient accumulation)."""
         cfg, d = self.cfg, self.dims
         K, st, c = cfg.max_depth, self._stream(), self.code
         b = state["batch"]
@@ -508,14 +589,14 @@ class StepEngine(Kernels):
         self.grad_layers = [_layer_views(self.arena, grads, i, grads=True) for i in range(d.layers)]
         g_embed, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
+        scale = self._upstream(grad_scale, state["dgate"])
+        self._lm_grad_store(state, scale, grads, accumulate)
         plan_original = self.embed_plan(b.original) if K > 1 else None
         dnext = None  # gradient at the core input of depth+1
-        lm_written = accumulate
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
-            dr = self._readout_bwd(rec, depth, state["dgate"][depth], grad_scale, g_lm, g_norm,
-                                   g_gw, g_gb, g_db, first_lm=not lm_written)
-            lm_written = lm_written or rec["R"] > 0
+            dr = self._readout_bwd(rec, depth, state["dgate"][depth], scale, g_norm, g_gw, g_gb,
+                                   g_db)
             for saved in reversed(rec["coda_saves"]):
                 dr = self._layer_bwd(dr, saved, b, grads)
             if dnext is not None:
@@ -529,10 +610,6 @@ class StepEngine(Kernels):
         for saved in reversed(state["prelude"]):
             dx = self._layer_bwd(dx, saved, b, grads)
         self.embed_scatter(dx, self.embed_plan(b.ids), g_embed)
-        if not lm_written:
-            # no pass had a loss-bearing row: the LM head's gradient is zero
-            lo, hi = self.arena.lm_span
-            grads[lo:hi].zero_()
         self._written = None
         return grads
 
@@ -559,7 +636,6 @@ class StepEngine(Kernels):
         K, N = cfg.max_depth, x0.shape[0]
         if x0.shape != (batch.ids.numel(), d.hidden) or x0.dtype != self.dtype:
             raise ValueError("x0 must be [rows, hidden] in the parameter dtype")
-        self._ws = None
         self.transposed.refresh(self.code, self._stream())
         b = batch
         self._rope = Rope(positions=b.positions, inv_freq=self.inv_freq)
@@ -621,7 +697,9 @@ class StepEngine(Kernels):
         autoregressive target), the vocabulary cross-entropy; then the
         objective.  ``batch`` holds masked, original (targets),
         mask_probability, boundaries (segment offsets over the N rows),
-        ar_target and ar_count.
+        ar_target and ar_count.  The state holds the per-pass cross-entropy
+        and token entropy of the loss-bearing rows (``ce``, ``entropy``
+        [K, N] float32, zero elsewhere).
 
         Returns (out[10] as the step's, state for readout_backward)."""
         cfg, d = self.cfg, self.dims
@@ -630,29 +708,31 @@ class StepEngine(Kernels):
         if len(finals) != K or any(f.shape != (N, d.hidden) or f.dtype != self.dtype
                                    for f in finals):
             raise ValueError("finals must be max_depth tensors [rows, hidden] in the parameter dtype")
-        self._ws = None
         st = self._stream()
         self.transposed.refresh(self.code, st)
         b = batch
+        g_lm = self._empty(d.vocab, d.hidden, dtype=torch.float32) if need_grad else None
         S = b.boundaries.numel() - 1
         gates = torch.empty(K, N, dtype=torch.float32, device=self.device)
         exits = torch.full((N,), K, dtype=torch.int32, device=self.device)
         ce_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
+        ent_all = torch.zeros(K, N, dtype=torch.float32, device=self.device)
         wsum = torch.empty(1, dtype=torch.float32, device=self.device)
         call("alodlm_inverse_weight_sum", ptr(b.masked), ptr(b.mask_probability), N, ptr(wsum), st)
         ar_coef = 0.5 / (K * b.ar_count) if b.ar_count else 0.0
         depths = []
+        lm_written = False
         for depth in range(K):
             rec = {}
             readout = self._gate_pass(finals[depth].contiguous(), depth, gates, exits, b,
                                       exit_uniforms, generator, rec)
-            self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all, need_grad,
-                             rec)
+            lm_written |= self._lm_readout(readout, depth, gates, exits, b, wsum, ar_coef, ce_all,
+                                           ent_all, need_grad, rec, g_lm, not lm_written)
             depths.append(rec)
         out, dgate = self._objective(gates, exits, b, ce_all, N, S, K)
         self.last_rows = [rec["R"] for rec in depths]
-        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "dgate": dgate,
-                 "depths": depths}
+        state = {"batch": b, "gates": gates, "exits": exits, "ce": ce_all, "entropy": ent_all,
+                 "dgate": dgate, "depths": depths, "g_lm": g_lm, "lm_written": lm_written}
         return out, state
 
     def readout_backward(self, state, grad_scale=1.0):
@@ -661,10 +741,12 @@ class StepEngine(Kernels):
         norm, gate)."""
         K = self.cfg.max_depth
         grads = torch.zeros(self.arena.total, dtype=torch.float32, device=self.device)
-        _, g_norm, g_lm, g_gw, g_gb, g_db = self._grad_views(grads)
+        _, g_norm, _, g_gw, g_gb, g_db = self._grad_views(grads)
+        scale = self._upstream(grad_scale, state["dgate"])
+        self._lm_grad_store(state, scale, grads, False)
         dfinals = [None] * K
         for depth in reversed(range(K)):
             dfinals[depth] = self._readout_bwd(state["depths"][depth], depth,
-                                               state["dgate"][depth], grad_scale, g_lm, g_norm,
-                                               g_gw, g_gb, g_db)
+                                               state["dgate"][depth], scale, g_norm, g_gw, g_gb,
+                                               g_db)
         return dfinals, grads

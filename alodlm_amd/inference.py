@@ -26,9 +26,11 @@ How this implementation is organised:
   rows after the cached prefix.  Committed rows come first in a window and the
   run being retired is the first of them, so keeping it is a length increment,
   not a copy.
-* **Layers on the step's kernels.**  Every layer application is
-  ``Kernels.layer_window``: RMSNorm, the GEMMs, q/k-norm + RoPE, attention,
-  SwiGLU.  The window's mask (every cached key, causal inside the window;
+* **Layers on the step's kernels.**  Every layer application is a call of
+  the module-level ``layer_forward`` (``alodlm_amd.model``, bound here as the
+  reference binds it), which runs ``Kernels.layer_window``: RMSNorm, the
+  GEMMs, q/k-norm + RoPE, attention, SwiGLU, with the window's keys and
+  values written in place (``layers.WindowSlot``).  The window's mask (every cached key, causal inside the window;
   alodlm/inference.py:77-79) is the clean stream of one dual-stream segment
   (``WindowMask``).  The carry norm plus re-embedding is one ``carry_select``
   launch, the final norm and gate one ``final_norm_gate`` launch, and the
@@ -42,7 +44,8 @@ import time
 import torch
 
 from ._lib import call, ptr
-from .layers import Rope, WindowMask
+from .layers import WindowMask, WindowSlot
+from .model import layer_forward
 
 # header fields (include/alodlm_hip.h, ALODLM_DECODE_*)
 HEADER = 16
@@ -280,6 +283,15 @@ class _DeviceState:
         call("alodlm_decode_plan", self.ref, stream)
 
 
+def rope_tables(positions, inv_freq, dtype):
+    """cos/sin [rows, head_dim] of the rotary embedding at ``positions``, the
+    computation of [tf] modeling_qwen3.py:126-137 (float32 angles
+    position x inverse frequency, duplicated halves, rounded to ``dtype``)."""
+    freqs = positions.to(torch.float32)[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), -1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
 class Decoder:
     """Adaptive recurrent decoding (alodlm/inference.py:66-246) with the step's
     HIP kernels and device-side window state."""
@@ -323,15 +335,21 @@ class Decoder:
         cache.reserve(P + rows)
         tiled = e.dtype == torch.bfloat16 and d.head_dim in (64, 128)
         lay = WindowMask(P, rows, tiled, e.device, block_size=c.block_size)
-        rope = Rope(positions=positions, inv_freq=e.inv_freq)
+        cos, sin = rope_tables(positions, e.inv_freq, e.dtype)
         H, V = d.hidden, d.vocab
+        modules = self.model.backbone.model.layers
 
         def layer(index, h, depth):
+            # every layer application goes through the module-level
+            # layer_forward, as alodlm/inference.py:83-88 does; the slot lets
+            # it write the window's keys/values after the cached rows
             key = cache.key(index, depth)
             kbuf, vbuf = cache.buffers(key)
+            slot = WindowSlot(e, e.layers[index], kbuf, vbuf, lay)
+            h, kv = layer_forward(modules[index], h, cos, sin, lay, slot)
             if window is not None:
-                window[key] = cache.rows(key, P, rows)
-            return e.layer_window(e.layers[index], h, rope, lay, kbuf, vbuf)
+                window[key] = kv
+            return h
 
         hidden = e._empty(rows, H)
         call("alodlm_embed_gather", ptr(e.embed), ptr(ids), ptr(hidden), rows, H, V, code, st)

@@ -1,13 +1,11 @@
-"""One Qwen3 decoder layer on the HIP kernels (drop-in for alodlm/model.py:41-80).
+"""One Qwen3 decoder layer on the HIP kernels.
 
-The forward and backward schedules of a layer application live here and are
-shared by the fused training step (``engine.StepEngine``), the decoder and
-the reference's public layer functions:
-
-* ``rotary(q, k, cos, sin)`` (alodlm/model.py:41-46);
-* ``layer_forward(layer, hidden, cos, sin, mask, prefix=None)`` returning
-  ``(hidden, (k, v))`` (alodlm/model.py:49-76);
-* ``training_layer(layer, hidden, cos, sin, mask)`` (alodlm/model.py:79-80).
+The forward and backward schedules of a layer application live here
+(``Kernels.layer_fwd``, ``layer_bwd``, ``layer_window``) and are shared by the
+fused training step (``engine.StepEngine``), the decoder and the reference's
+public layer functions, which ``alodlm_amd.model`` defines where the
+reference does (alodlm/model.py:41-80): ``rotary``, ``layer_forward`` and
+``training_layer`` run on the autograd nodes and mask forms of this module.
 
 The attention mask is one of
 
@@ -625,15 +623,6 @@ class _LayerFunction(torch.autograd.Function):
         return (None, None, None, dx, *grads)
 
 
-def rotary(q, k, cos, sin):
-    """q * cos + rotate_half(q) * sin and the same for k (alodlm/model.py:41-46).
-
-    q [N, nq, dh], k [N, nkv, dh]; cos, sin [N, dh] (used in q's dtype).
-    Differentiable in q and k."""
-    _check_device(q, "rotary")
-    return _Rotary.apply(q, k, cos.to(q.dtype).contiguous(), sin.to(q.dtype).contiguous())
-
-
 class _Rotary(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, cos, sin):
@@ -664,54 +653,43 @@ class _Rotary(torch.autograd.Function):
         return grads[0], grads[1], None, None
 
 
-def layer_forward(layer, hidden, cos, sin, mask, prefix=None):
-    """Apply one decoder layer and return ``(hidden, (k, v))`` with the current
-    rows' rotated keys and values [L, kv_heads, head_dim] (alodlm/model.py:49-76).
+class WindowSlot:
+    """A decoding window's place in a prefix cache, passed to
+    ``layer_forward`` as its ``prefix``: the layer's key/value buffers
+    ``k``/``v`` [capacity, kv_heads, head_dim] whose rows [0, P) hold the
+    cached prefix, the window's mask (a ``WindowMask`` over P prefix rows),
+    and the kernels and arena weights of the model the layer belongs to
+    (``weights`` may carry the out-contiguous copies of its matrices, which the
+    caller keeps current).  The layer writes the window's rotated keys and
+    values straight into rows [P, P + L) and returns views of them."""
 
-    ``layer`` is a transformers Qwen3 decoder layer, ``hidden`` [L, H], cos/sin
-    [L, head_dim] in the model dtype, ``mask`` as in the module docstring.
-    ``prefix`` = (k, v) of cached rows [P, kv_heads, head_dim] runs the decoding
-    window, whose mask must then be the prefix + causal window mask; that
-    form (also without a prefix: the causal mask) runs without autograd.
-    Under the dual-stream mask the output is differentiable in ``hidden`` and
-    the layer's parameters; the returned k, v carry no autograd history."""
-    _check_device(hidden, "layer_forward")
-    kernels = _kernels_for(layer, hidden)
-    d = kernels.dims
-    L = hidden.shape[0]
-    kind = _kernel_mask(mask, L, hidden.device)
-    rope = Rope(cos=cos.to(hidden.dtype).contiguous(), sin=sin.to(hidden.dtype).contiguous())
-    if prefix is None and not (isinstance(kind, tuple) and kind[0] == "window"):
-        y, k, v = _LayerFunction.apply(kernels, kind, rope, hidden,
-                                       *LayerWeights.module_tensors(layer))
-        return y, (k, v)
-    P = kind[1] if isinstance(kind, tuple) else None
-    if P is None:
-        raise ValueError("a prefix cache needs the prefix + causal window mask")
-    if prefix is None:
-        prefix_k = prefix_v = hidden.new_empty(0, d.kv_heads, d.head_dim)
-    else:
-        prefix_k, prefix_v = prefix
-    if prefix_k.shape[0] != P:
-        raise ValueError(f"the mask allows {P} prefix keys but the cache holds {prefix_k.shape[0]}")
-    params = LayerWeights.module_tensors(layer)
-    if torch.is_grad_enabled() and (hidden.requires_grad or any(p.requires_grad for p in params)):
-        raise RuntimeError("layer_forward under the decoding window mask runs without autograd; "
-                           "wrap the call in torch.no_grad() (training takes the dual-stream "
-                           "mask)")
-    KD = d.kv_heads * d.head_dim
-    kbuf = hidden.new_empty(P + L, KD)
-    vbuf = hidden.new_empty(P + L, KD)
-    kbuf[:P].copy_(prefix_k.reshape(P, KD))
-    vbuf[:P].copy_(prefix_v.reshape(P, KD))
-    tiled = hidden.dtype == torch.bfloat16 and d.head_dim in (64, 128)
-    window = WindowMask(P, L, tiled, hidden.device)
-    with torch.no_grad():
-        w = LayerWeights.from_tensors(*params)
-        y = kernels.layer_window(w, hidden.detach().contiguous(), rope, window, kbuf, vbuf)
-    return y, (kbuf[P:].view(L, d.kv_heads, d.head_dim), vbuf[P:].view(L, d.kv_heads, d.head_dim))
+    def __init__(self, kernels, weights, k, v, mask):
+        self.kernels, self.weights = kernels, weights
+        self.k, self.v, self.mask = k, v, mask
+
+    def run(self, layer, hidden, cos, sin):
+        d = self.kernels.dims
+        L, P = hidden.shape[0], self.mask.prefix
+        if self.weights.wqkv.data_ptr() != layer.self_attn.q_proj.weight.data_ptr():
+            raise ValueError("the window slot belongs to another layer")
+        if self.k.shape[0] < P + L or self.v.shape[0] < P + L or L != self.mask.window:
+            raise ValueError("the window does not fit the slot's cache rows")
+        rope = Rope(cos=table(cos, L, d.head_dim, hidden), sin=table(sin, L, d.head_dim, hidden))
+        y = self.kernels.layer_window(self.weights, hidden.contiguous(), rope, self.mask,
+                                      self.k, self.v)
+        return y, (self.k[P:P + L], self.v[P:P + L])
 
 
-def training_layer(layer, hidden, cos, sin, mask):
-    """The layer output alone (alodlm/model.py:79-80)."""
-    return layer_forward(layer, hidden, cos, sin, mask)[0]
+def table(t, rows, head_dim, like):
+    """A rotary cos/sin table as the kernels read it: [rows, head_dim]
+    contiguous in ``like``'s dtype, on its device.  A leading dimension of 1
+    is dropped (the shape rotary embedding modules return); any other shape
+    raises ValueError (the kernels read rows x head_dim values)."""
+    if t.ndim == 3 and t.shape[0] == 1:
+        t = t[0]
+    if t.ndim != 2 or tuple(t.shape) != (rows, head_dim):
+        raise ValueError(f"cos/sin must be [{rows}, {head_dim}] (rows x head_dim), "
+                         f"got {tuple(t.shape)}")
+    if t.device != like.device:
+        raise ValueError("cos/sin must be on the device of the rows they rotate")
+    return t.to(like.dtype).contiguous()

@@ -7,6 +7,10 @@ the whole training step - batch building, rollout over the recurrent depths,
 cross-entropies and the objective - on the gfx950 HIP kernels through
 ``StepEngine`` and returns ``(loss, metrics)``; ``loss.backward()`` runs the
 hand-scheduled backward and fills every parameter's ``.grad``.
+
+The reference's layer functions are defined here as in alodlm/model.py:41-80:
+``rotary``, ``layer_forward`` (also the decoder's layer call) and
+``training_layer``, each on the layer kernels of ``alodlm_amd.layers``.
 """
 
 import json
@@ -21,6 +25,8 @@ import torch.nn as nn
 from . import _lib
 from .config import ModelConfig, local_dir
 from .engine import METRIC_NAMES, StepEngine
+from .layers import (LayerWeights, Rope, WindowMask, WindowSlot, _LayerFunction, _Rotary,
+                     _check_device, _kernel_mask, _kernels_for, table)
 
 
 class GateHead(nn.Module):
@@ -43,6 +49,91 @@ class GateHead(nn.Module):
 
     def forward(self, features, depth):
         return self.net(features).squeeze(-1) + self.depth_bias[depth]
+
+
+def rotary(q, k, cos, sin):
+    """q * cos + rotate_half(q) * sin and the same for k (alodlm/model.py:41-46),
+    one kernel launch per tensor.
+
+    q [L, nq, dh] and k [L, nkv, dh] share rows, head_dim, dtype and device;
+    cos, sin are [L, dh] (or [1, L, dh]) and are used in q's dtype.
+    Differentiable in q and k.  Other shapes raise ValueError (the
+    reference's broadcasting error)."""
+    if q.ndim != 3 or k.ndim != 3:
+        raise ValueError("rotary takes q [rows, heads, head_dim] and k [rows, kv_heads, head_dim]")
+    L, _, dh = q.shape
+    if k.shape[0] != L or k.shape[2] != dh:
+        raise ValueError(f"k {tuple(k.shape)} must have q's rows and head_dim ({L}, {dh})")
+    if k.dtype != q.dtype or k.device != q.device:
+        raise ValueError("q and k must share dtype and device")
+    if dh % 2:
+        raise ValueError("head_dim must be even for the rotary embedding")
+    cos, sin = table(cos, L, dh, q), table(sin, L, dh, q)
+    _check_device(q, "rotary")
+    return _Rotary.apply(q, k, cos, sin)
+
+
+def layer_forward(layer, hidden, cos, sin, mask, prefix=None):
+    """Apply one decoder layer and return ``(hidden, (k, v))`` with the current
+    rows' rotated keys and values [L, kv_heads, head_dim] (alodlm/model.py:49-76).
+
+    ``layer`` is a transformers Qwen3 decoder layer, ``hidden`` [L, H], cos/sin
+    [L, head_dim], ``mask`` one of the forms ``alodlm_amd.layers`` lists.
+    ``prefix`` = (k, v) of cached rows [P, kv_heads, head_dim] runs the decoding
+    window, whose mask must then be the prefix + causal window mask; that
+    form (also without a prefix: the causal mask) runs without autograd.
+    ``prefix`` may also be a ``layers.WindowSlot`` (what the decoder passes):
+    the window's keys and values are then written in place after the cached
+    rows.  Under the dual-stream mask the output is differentiable in
+    ``hidden`` and the layer's parameters; the returned k, v carry no autograd
+    history."""
+    if isinstance(prefix, WindowSlot):
+        _check_device(hidden, "layer_forward")
+        return prefix.run(layer, hidden, cos, sin)
+    kernels = _kernels_for(layer, hidden)
+    d = kernels.dims
+    if hidden.ndim != 2 or hidden.shape[1] != layer.input_layernorm.weight.shape[0]:
+        raise ValueError(f"hidden must be [rows, {layer.input_layernorm.weight.shape[0]}]")
+    L = hidden.shape[0]
+    rope = Rope(cos=table(cos, L, d.head_dim, hidden), sin=table(sin, L, d.head_dim, hidden))
+    _check_device(hidden, "layer_forward")
+    kind = _kernel_mask(mask, L, hidden.device)
+    if prefix is None and not (isinstance(kind, tuple) and kind[0] == "window"):
+        y, k, v = _LayerFunction.apply(kernels, kind, rope, hidden,
+                                       *LayerWeights.module_tensors(layer))
+        return y, (k, v)
+    P = kind[1] if isinstance(kind, tuple) else None
+    if P is None:
+        raise ValueError("a prefix cache needs the prefix + causal window mask")
+    if prefix is None:
+        prefix_k = prefix_v = hidden.new_empty(0, d.kv_heads, d.head_dim)
+    else:
+        prefix_k, prefix_v = prefix
+    if prefix_k.shape[0] != P or prefix_v.shape[0] != P:
+        raise ValueError(f"the mask allows {P} prefix keys but the cache holds {prefix_k.shape[0]}")
+    KD = d.kv_heads * d.head_dim
+    if prefix_k.numel() != P * KD or prefix_v.numel() != P * KD:
+        raise ValueError(f"cached keys and values must be [{P}, {d.kv_heads}, {d.head_dim}]")
+    params = LayerWeights.module_tensors(layer)
+    if torch.is_grad_enabled() and (hidden.requires_grad or any(p.requires_grad for p in params)):
+        raise RuntimeError("layer_forward under the decoding window mask runs without autograd; "
+                           "wrap the call in torch.no_grad() (training takes the dual-stream "
+                           "mask)")
+    kbuf = hidden.new_empty(P + L, KD)
+    vbuf = hidden.new_empty(P + L, KD)
+    kbuf[:P].copy_(prefix_k.reshape(P, KD))
+    vbuf[:P].copy_(prefix_v.reshape(P, KD))
+    tiled = hidden.dtype == torch.bfloat16 and d.head_dim in (64, 128)
+    window = WindowMask(P, L, tiled, hidden.device)
+    with torch.no_grad():
+        w = LayerWeights.from_tensors(*params)
+        y = kernels.layer_window(w, hidden.detach().contiguous(), rope, window, kbuf, vbuf)
+    return y, (kbuf[P:].view(L, d.kv_heads, d.head_dim), vbuf[P:].view(L, d.kv_heads, d.head_dim))
+
+
+def training_layer(layer, hidden, cos, sin, mask):
+    """The layer output alone (alodlm/model.py:79-80)."""
+    return layer_forward(layer, hidden, cos, sin, mask)[0]
 
 
 class _Step(torch.autograd.Function):
@@ -73,9 +164,10 @@ class _Step(torch.autograd.Function):
             raise RuntimeError("the step was run without gradient tracking")
         ctx.state = None
         if engine.fused_optimizer is not None:
-            # the upstream gradient scales the LM head and gate products
-            # (everything else is linear in them); one read of the scalar
-            engine.backward(state, float(grad_loss), accumulate=engine.grads_pending)
+            # the upstream gradient (a device scalar, never read on the host)
+            # scales the LM head's and the gate's gradients and the readout
+            # gradient that every other gradient is linear in
+            engine.backward(state, grad_loss, accumulate=engine.grads_pending)
             del state
             engine.grads_pending = True
             engine.note_step_peak()
@@ -184,6 +276,14 @@ class ALoDLM(nn.Module):
         self._fused_optimizer = optimizer
         if self._engine is not None:
             self._engine.fused_optimizer = optimizer
+
+    def zero_grad(self, set_to_none=True):
+        """Clear the gradients: every parameter's ``.grad`` and, with a bound
+        FusedAdamW, the float32 gradients of the step's arena (the next
+        backward writes them afresh instead of accumulating)."""
+        super().zero_grad(set_to_none)
+        if self._engine is not None:
+            self._engine.grads_pending = False
 
     def float32_grads(self):
         """name -> float32 gradient of the last backward(s) since zero_grad when

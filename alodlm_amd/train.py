@@ -162,7 +162,8 @@ def save_training_state(directory, model, optimizer, scheduler, loader_position=
     * ``optimizer.bin``: a ``torch.optim.AdamW`` state dict - per parameter
       index (groups in order) ``step`` (float tensor), ``exp_avg`` and
       ``exp_avg_sq``, plus ``master``, the float32 master weight, which a torch
-      AdamW carries along unused; group fields as torch.optim.AdamW records;
+      AdamW carries along unused; group fields as torch.optim.AdamW records,
+      and ``initial_lr`` as the LR scheduler adds it;
     * ``custom_checkpoint_0.pkl``: the LR scheduler's state dict (the
       reference registers its scheduler for checkpointing,
       alodlm/train.py:58);
@@ -179,7 +180,11 @@ def save_training_state(directory, model, optimizer, scheduler, loader_position=
     state, groups = {}, []
     for group in optimizer.param_groups:
         defaults = _adamw_group_defaults(group["lr"])
-        fields = {**defaults, **{k: v for k, v in group.items() if k in defaults}}
+        # torch AdamW's own fields, plus the schedule's base rate that a
+        # LambdaLR records in each group (the reference's saved groups carry
+        # it, and a scheduler rebuilt with last_epoch >= 0 reads it)
+        kept = set(defaults) | {"initial_lr"}
+        fields = {**defaults, **{k: v for k, v in group.items() if k in kept}}
         ids = []
         for p in group["params"]:
             i = index.setdefault(id(p), len(index))

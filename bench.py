@@ -206,6 +206,17 @@ def _roofline(timer, steps, spec=None):
     return roof, classes
 
 
+def _allocator_counters(device):
+    """Cumulative caching-allocator counters: free-and-retry events (each one
+    synchronizes the device and returns cached blocks), device allocations
+    and frees, and the peak of reserved bytes."""
+    s = torch.cuda.memory_stats(device)
+    return {"num_alloc_retries": s.get("num_alloc_retries", 0),
+            "num_device_alloc": s.get("num_device_alloc", 0),
+            "num_device_free": s.get("num_device_free", 0),
+            "reserved_peak": s.get("reserved_bytes.all.peak", 0)}
+
+
 def _release():
     import gc
     gc.collect()
@@ -244,13 +255,24 @@ def run_step(spec, device, steps, warmup, kernel_timing):
         timer = KernelTimer()
         timer.wrap(engine)
     torch.cuda.synchronize()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    alloc = [_allocator_counters(device)]
     t0 = time.perf_counter()
+    marks[0].record()
     rows = []
     for i in range(steps):
         loss = one_step()
+        marks[i + 1].record()
+        alloc.append(_allocator_counters(device))
         rows.append(list(engine.last_rows))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    step_ms = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
+    for i, t in enumerate(step_ms):
+        d = {k: alloc[i + 1][k] - alloc[i][k] for k in alloc[0]}
+        print(f"[bench] {spec['name']} step {i}: {t:.1f} ms, allocator retries "
+              f"{d['num_alloc_retries']}, device mallocs {d['num_device_alloc']}, frees "
+              f"{d['num_device_free']}", file=sys.stderr, flush=True)
     print(f"[bench] {spec['name']}: timed {steps} steps in {elapsed:.3f}s loss {float(loss):.4f}",
           file=sys.stderr, flush=True)
     ms = 1000.0 * elapsed / steps
@@ -270,6 +292,13 @@ def run_step(spec, device, steps, warmup, kernel_timing):
                                             "norm_outputs": bool(engine._keep and engine._keep[1])}},
         "mfu": round(step_f / (ms / 1000.0) / PEAK_BF16, 4),
         "step_tflop": round(step_f / 1e12, 1),
+        "step_ms": {"min": round(min(step_ms), 2),
+                    "median": round(sorted(step_ms)[len(step_ms) // 2], 2),
+                    "max": round(max(step_ms), 2)},
+        "allocator": {"alloc_retries": alloc[-1]["num_alloc_retries"] - alloc[0]["num_alloc_retries"],
+                      "device_mallocs": alloc[-1]["num_device_alloc"] - alloc[0]["num_device_alloc"],
+                      "device_frees": alloc[-1]["num_device_free"] - alloc[0]["num_device_free"],
+                      "reserved_peak_gib": round(alloc[-1]["reserved_peak"] / 2**30, 1)},
     }
     if timer is not None:
         record["roofline"], record["kernel_classes"] = _roofline(timer, steps, spec)
@@ -607,6 +636,7 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "device": device_info(),
         "memory": head["memory"], "mfu": head["mfu"], "step_tflop": head["step_tflop"],
+        "step_ms": head["step_ms"], "allocator": head["allocator"],
     }
     if "roofline" in head:
         line["roofline"], line["kernel_classes"] = head["roofline"], head["kernel_classes"]

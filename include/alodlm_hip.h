@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 5
+#define ALODLM_ABI_VERSION 6
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -421,6 +421,11 @@ int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n
  *   regularization_cost, profile_mean_depth, first_pass_halt_probability,
  *   ar_loss, masked_count.
  * dgate [K, rows] = d total / d gate (unit upstream gradient).
+ * total is NaN when a gate is non-finite or when `nonfinite` (nullable) holds
+ * a nonzero value: the reference adds 0 * sum(logits + gates) to the loss
+ * (model.py:186), and the step sets that flag when an LM-head weight is
+ * non-finite (alodlm_transpose_checked), which makes a logits column
+ * non-finite in every row, computed or not.
  * One workgroup; `workspace` holds alodlm_objective_workspace(rows, S, K) floats.
  * ------------------------------------------------------------------------ */
 int64_t alodlm_objective_workspace(int64_t rows, int64_t n_segments, int64_t max_depth);
@@ -428,8 +433,8 @@ int alodlm_objective(const float* gates, const int32_t* exits, const uint8_t* ma
                      const float* mask_prob, const float* ce_full, const float* ar_ce,
                      const int32_t* ar_target, const int64_t* bounds, int64_t n_segments,
                      int64_t rows, int64_t max_depth, float depth_prior_c, float kl_beta_mi,
-                     float kl_beta_marg, float* out, float* dgate, float* workspace,
-                     void* stream);
+                     float kl_beta_marg, const int32_t* nonfinite, float* out, float* dgate,
+                     float* workspace, void* stream);
 /* outcome_loss alone (alodlm/loss.py:35-90): the objective above without the
  * autoregressive part; out[0..9] as above with out[0] = (denoising + actor)
  * / 2 and out[8] = 0, so the outcome loss is out[1] + out[2].  dgate [K, rows]
@@ -506,6 +511,16 @@ int alodlm_adamw(void* const* params, float* const* master, float* const* exp_av
 int alodlm_cast_f32(const float* src, const float* scale, void* dst, int64_t n, int dtype,
                     void* stream);
 int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream);
+/* x *= scale[0] in the storage dtype (scale is a device scalar), and the
+ * float32 y = scale[0] * x + (accumulate ? y : 0) (scale may be NULL for 1).
+ * The step computes the LM head's input and weight gradients in the forward,
+ * where dL/dlogits is final at each depth, for a unit upstream gradient; the
+ * backward applies torch's loss.backward() seed (alodlm/train.py:136,
+ * alodlm/model.py:161 through torch.nn.Linear's backward) with these, without
+ * reading it on the host. */
+int alodlm_scale(void* x, const float* scale, int64_t n, int dtype, void* stream);
+int alodlm_scale_add_f32(const float* x, float* y, int64_t n, const float* scale, int accumulate,
+                         void* stream);
 /* dst[c][r] = src[r][c] for a row-major rows x cols matrix (dst and src must
  * not overlap).  The step keeps transposed copies of the projection and
  * LM-head weights ([in, out], refreshed at the start of every forward) so
@@ -514,6 +529,13 @@ int alodlm_scale_f32(float* x, const float* scale, int64_t n, void* stream);
  * alodlm/model.py:52-58,161 read through torch.nn.Linear. */
 int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
                      void* stream);
+/* The same transpose, storing 1 into *nonfinite (not cleared here) when any
+ * element of src is inf or NaN: the step copies the LM-head weight with it,
+ * so that the loss can follow the reference's 0 * sum(logits) term
+ * (alodlm/model.py:186) without computing the logits of rows that carry no
+ * loss. */
+int alodlm_transpose_checked(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
+                             int32_t* nonfinite, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,5 +21,6 @@ def projection_vector(index, numel):
 
 
 def sample_indices(numel, count=256):
+    """``count`` strided indices into a tensor of ``numel`` elements."""
     stride = max(1, numel // count)
     return np.arange(0, numel, stride)[:count]

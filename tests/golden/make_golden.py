@@ -21,6 +21,16 @@ numpy, loadable with ``allow_pickle=False``).  Cases:
   reference runs with ``precision: bf16`` (its eager bf16 rounding sequence
   on the CPU): the same outputs, gates and gradient summaries as float64 of
   the bf16 values.
+* ``step_1p7b_layers_bf16``: Qwen3-1.7B layer shapes (hidden 2048, 16 / 8
+  heads of 128, SwiGLU 6144), vocabulary 151936, two layers run as the
+  recurrent core (loop 0-2), K = 4, one 2048-token segment, the bf16 weights
+  of tests/test_shapes_gpu.py (seed 31): the reference's bf16 step (loss,
+  metrics, masks, gates, exits, every depth's masked cross-entropies,
+  per-gradient norm, projection and a 4096-element strided sample) and, under
+  ``f32_``, the reference's float32 step on the same (bf16-valued) weights
+  with the bf16 run's exits - the reference's own bf16-vs-float32 gap at
+  that shape.  ``--cases step_1p7b_layers_bf16`` writes this case alone
+  (about ten minutes and 40 GB on 8 cores).
 """
 
 import argparse
@@ -118,9 +128,127 @@ def step_case(model, ids, labels, boundaries, seed, lr, full_grads, capture):
     return out
 
 
+def real_shape_run(model, ids, labels, boundaries, seed, forced_exits=None, samples=4096):
+    """The reference forward + backward at a real shape: loss, metrics, batch,
+    gates, exits, the masked cross-entropies [K, M] and gradient summaries.
+    ``forced_exits`` (a previous run's exits) replaces the rollout's exit
+    uniforms by 0 at each row's exit depth and 1 elsewhere, so the run takes
+    exactly those exits (alodlm/model.py:163-167 selects u < hazard)."""
+    import alodlm.model as reference_model
+    captured = {}
+    original_rollout = type(model).rollout
+    original_outcome = reference_model.outcome_loss
+    original_rand_like = torch.rand_like
+    K = model.config.max_depth
+    depth = {"d": 0}
+
+    def rollout(self, batch):
+        logits, gates, exits = original_rollout(self, batch)
+        captured["batch"] = batch
+        captured["gates"] = torch.stack([g.detach() for g in gates]).float()
+        captured["exits"] = exits.clone()
+        return logits, gates, exits
+
+    def outcome(ce, *args, **kwargs):
+        captured["ce"] = ce.detach().float().clone()
+        return original_outcome(ce, *args, **kwargs)
+
+    def rand_like(t, *args, **kwargs):
+        d = depth["d"]
+        depth["d"] += 1
+        return torch.where(forced_exits == d + 1, 0.0, 1.0).to(t.dtype)
+
+    type(model).rollout = rollout
+    reference_model.outcome_loss = outcome
+    if forced_exits is not None:
+        torch.rand_like = rand_like
+    try:
+        torch.manual_seed(seed)
+        loss, metrics = model(ids, labels, boundaries)
+    finally:
+        type(model).rollout = original_rollout
+        reference_model.outcome_loss = original_outcome
+        torch.rand_like = original_rand_like
+    if forced_exits is not None:
+        assert depth["d"] == K - 1
+    loss.backward()
+    b = captured["batch"]
+    out = {"loss": np.float64(loss.item()), "gates": captured["gates"].numpy(),
+           "exits": captured["exits"].numpy(), "ce": captured["ce"].numpy(),
+           "ids": b.ids.numpy(), "original": b.original.numpy(), "positions": b.positions.numpy(),
+           "masked": b.masked.numpy(), "mask_probability": b.mask_probability.numpy(),
+           "boundaries": b.boundaries.numpy()}
+    for key, value in metrics.items():
+        out["metric_" + key] = np.float64(value.item())
+    names = [n for n, _ in model.named_parameters()]
+    for index, (name, p) in enumerate(model.named_parameters()):
+        g = p.grad.detach().double().flatten()
+        out["gnorm_" + name] = np.float64(g.norm().item())
+        out["gproj_" + name] = np.float64((g * projection_vector(index, g.numel())).sum().item())
+        out["gsample_" + name] = g[torch.as_tensor(sample_indices(g.numel(), samples))].numpy()
+    out["param_names"] = np.array(names)
+    model.zero_grad(set_to_none=True)
+    return out
+
+
+def reference_bf16(ALoDLM, backbone, cfg, state):
+    """The reference model in bfloat16 as its training loads one
+    (alodlm/train.py:38-39 -> ALoDLM.from_pretrained(dir, config, bfloat16),
+    model.py:95-114): the backbone saved and read back by transformers with
+    that dtype, which keeps the rotary inverse frequencies in float32 (a
+    ``.to(bfloat16)`` of the module would round them), then ``state`` (the
+    parameters, gate included) loaded."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as directory:
+        backbone.save_pretrained(directory)
+        model = ALoDLM.from_pretrained(directory, cfg, torch.bfloat16, require_gate=False)
+    assert model.backbone.model.rotary_emb.inv_freq.dtype == torch.float32
+    model.load_state_dict(state, strict=True)
+    return model
+
+
+def real_shape_case(ALoDLM, ModelConfig, Qwen3Config, Qwen3ForCausalLM, seed=31):
+    from oracle.step import Objective
+    from tests.test_shapes_gpu import MASK_ID, VOCAB, _bf16_params, _dims, _tokens
+    dims = _dims(2048, 16, 8, 6144, layers=2)
+    obj = Objective(loop_start=0, loop_end=2, mask_token_id=MASK_ID, block_size=32)
+    params = _bf16_params(dims, obj, seed=seed)
+    cfg = ModelConfig(loop_start=0, loop_end=2, mask_token_id=MASK_ID, block_size=32,
+                      attention_backend="sdpa", compile_layers=False,
+                      gradient_checkpointing=False)
+    with torch.device("meta"):
+        backbone = Qwen3ForCausalLM(Qwen3Config(
+            hidden_size=2048, intermediate_size=6144, num_hidden_layers=2,
+            num_attention_heads=16, num_key_value_heads=8, head_dim=128, vocab_size=VOCAB,
+            max_position_embeddings=4096, rms_norm_eps=1e-6,
+            rope_parameters={"rope_type": "default", "rope_theta": 1e6},
+            bos_token_id=1, eos_token_id=2, pad_token_id=0, tie_word_embeddings=False))
+    backbone = backbone.to_empty(device="cpu")
+    model = reference_bf16(ALoDLM, backbone, cfg,
+                           {(k if k.startswith("exit_gate.") else "backbone." + k): v
+                            for k, v in params.items()})
+    del backbone
+    ids, labels, bounds = _tokens([2048], seed=seed)
+    out = real_shape_run(model, ids, labels, bounds, seed)
+    out.update({"in_ids": ids.numpy(), "in_labels": labels.numpy(),
+                "in_boundaries": bounds.numpy(), "seed": np.int64(seed)})
+    model = model.float()
+    f32 = real_shape_run(model, ids, labels, bounds, seed,
+                         forced_exits=torch.as_tensor(out["exits"]))
+    assert np.array_equal(f32["masked"], out["masked"]) and np.array_equal(f32["exits"],
+                                                                          out["exits"])
+    for key in ("loss", "gates", "ce"):
+        out["f32_" + key] = f32[key]
+    for key, value in f32.items():
+        if key.startswith(("metric_", "gnorm_", "gproj_", "gsample_")):
+            out["f32_" + key] = value
+    return out
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--reference", default="/root/reference")
+    parser.add_argument("--cases", nargs="*", help="write only these cases")
     args = parser.parse_args()
     sys.path.insert(0, args.reference)
     sys.path.insert(0, str(Path(args.reference) / "tests"))
@@ -131,6 +259,14 @@ def main():
     from helpers import tiny_model
     from transformers import Qwen3Config, Qwen3ForCausalLM
 
+    if args.cases == ["step_1p7b_layers_bf16"]:
+        torch.set_num_threads(8)
+        arrays = real_shape_case(ALoDLM, ModelConfig, Qwen3Config, Qwen3ForCausalLM)
+        np.savez_compressed(HERE / "step_1p7b_layers_bf16.npz", **arrays)
+        print(json.dumps({"written": ["step_1p7b_layers_bf16"], "loss": float(arrays["loss"]),
+                          "f32_loss": float(arrays["f32_loss"])}))
+        return
+    wanted = set(args.cases or [])
     cases = {}
     # --- dual-stream batches --------------------------------------------------
     g = torch.Generator().manual_seed(7)
@@ -182,16 +318,17 @@ def main():
     ids = torch.randint(0, 1024, (512,), generator=g)
     cases["step_tiny"] = step_case(model, ids, ids.clone(), torch.tensor([0, 128, 256, 384, 512]),
                                    0, 1e-4, False, None)
-    model = ALoDLM(Qwen3ForCausalLM(backbone.config), cfg)
-    model.load_state_dict({(k if k.startswith("exit_gate.") else "backbone." + k): v
-                           for k, v in params.items()}, strict=True)
-    model = model.to(torch.bfloat16)
+    model = reference_bf16(ALoDLM, Qwen3ForCausalLM(backbone.config), cfg,
+                           {(k if k.startswith("exit_gate.") else "backbone." + k):
+                            v.to(torch.bfloat16) for k, v in params.items()})
     cases["step_tiny_bf16"] = step_case(model, ids, ids.clone(),
                                         torch.tensor([0, 128, 256, 384, 512]), 0, 1e-4, False, None)
 
     meta = {"torch": torch.__version__}
     import transformers
     meta["transformers"] = transformers.__version__
+    if wanted:
+        cases = {k: v for k, v in cases.items() if k in wanted}
     for name, arrays in cases.items():
         np.savez_compressed(HERE / f"{name}.npz", **arrays)
     (HERE / "versions.json").write_text(json.dumps(meta, indent=2) + "\n")

@@ -53,7 +53,7 @@ def test_library_loads_and_reports_abi():
     # argument validation runs on the host and returns ALODLM_EINVAL without a GPU
     with pytest.raises(ValueError):
         _lib.call("alodlm_objective", None, None, None, None, None, None, None, None, 1, 4, 99,
-                  0.4, 0.1, 1.0, None, None, None, None)
+                  0.4, 0.1, 1.0, None, None, None, None, None)
 
 
 def test_gemm_workspace_policy():

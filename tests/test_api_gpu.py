@@ -27,7 +27,7 @@ from alodlm_amd.attention import plan_to_device, sparse_attention, sparse_plan
 from alodlm_amd.batch import build_batch
 from alodlm_amd.config import ModelConfig
 from alodlm_amd.credit import masked_sequence_ids, sequence_score_function
-from alodlm_amd.layers import layer_forward, rotary, training_layer
+from alodlm_amd.model import layer_forward, rotary, training_layer
 from alodlm_amd.loss import autoregressive_loss, outcome_loss
 from oracle import step as O
 from tests import golden

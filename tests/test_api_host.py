@@ -100,3 +100,65 @@ def test_layer_forward_mask_forms():
         _kernel_mask(bad, L, "cpu")
     with pytest.raises(ValueError, match="dual-stream"):
         _kernel_mask(torch.ones(L, L, dtype=torch.bool), L, "cpu")
+
+
+def test_rotary_rejects_mismatched_operands():
+    """rotary (alodlm/model.py:41-46) checks its operands on the host before
+    any launch: k shares q's rows, head_dim, dtype and device, and the
+    cos/sin tables are [rows, head_dim] (the reference raises a broadcasting
+    error for each of these)."""
+    from alodlm_amd.model import rotary
+    q, k = torch.zeros(6, 4, 8), torch.zeros(6, 2, 8)
+    cos = sin = torch.zeros(6, 8)
+    cases = [
+        ((q, torch.zeros(5, 2, 8), cos, sin), "rows and head_dim"),
+        ((q, torch.zeros(6, 2, 4), cos, sin), "rows and head_dim"),
+        ((q, k.double(), cos, sin), "dtype"),
+        ((q, k, torch.zeros(5, 8), sin), r"cos/sin must be \[6, 8\]"),
+        ((q, k, cos, torch.zeros(6, 4)), r"cos/sin must be \[6, 8\]"),
+        ((q, k, torch.zeros(2, 6, 8), sin), r"cos/sin must be \[6, 8\]"),
+        ((torch.zeros(6, 4, 7), torch.zeros(6, 2, 7), torch.zeros(6, 7), torch.zeros(6, 7)),
+         "even"),
+        ((q.view(6, 32), k, cos, sin), "rows, heads, head_dim"),
+    ]
+    for args, message in cases:
+        with pytest.raises(ValueError, match=message):
+            rotary(*args)
+    # well-formed operands pass the checks and stop at the device check
+    with pytest.raises(ValueError, match="CUDA"):
+        rotary(q, k, cos.unsqueeze(0), sin)
+
+
+def test_layer_forward_rejects_short_tables_and_rows():
+    """layer_forward (alodlm/model.py:49-76) checks the hidden width and the
+    cos/sin tables against the layer before any launch."""
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer
+    from alodlm_amd.model import layer_forward, training_layer
+    cfg = Qwen3Config(hidden_size=32, intermediate_size=64, num_attention_heads=4,
+                      num_key_value_heads=2, head_dim=8, num_hidden_layers=1, vocab_size=64)
+    layer = Qwen3DecoderLayer(cfg, 0)
+    L = 6
+    x = torch.zeros(L, 32)
+    causal = torch.ones(L, L, dtype=torch.bool).tril()
+    with pytest.raises(ValueError, match=r"cos/sin must be \[6, 8\]"):
+        layer_forward(layer, x, torch.zeros(L - 1, 8), torch.zeros(L, 8), causal)
+    with pytest.raises(ValueError, match=r"cos/sin must be \[6, 8\]"):
+        training_layer(layer, x, torch.zeros(L, 8), torch.zeros(L, 4), causal)
+    with pytest.raises(ValueError, match=r"hidden must be \[rows, 32\]"):
+        layer_forward(layer, torch.zeros(L, 16), torch.zeros(L, 8), torch.zeros(L, 8), causal)
+    with pytest.raises(ValueError, match="CUDA"):
+        layer_forward(layer, x, torch.zeros(1, L, 8), torch.zeros(L, 8), causal)
+
+
+def test_layer_functions_live_in_model_and_inference_binds_layer_forward():
+    """The reference defines rotary, layer_forward and training_layer in
+    alodlm/model.py:41-80 and its decoder imports layer_forward from there
+    (alodlm/inference.py:11): the same names resolve here, and the decoder's
+    module-level name is the one its layer calls look up."""
+    import alodlm_amd as alodlm
+    import alodlm_amd.inference as inference
+    import alodlm_amd.model as model
+    for name in ("rotary", "layer_forward", "training_layer", "GateHead", "ALoDLM"):
+        assert hasattr(alodlm.model, name)
+    assert inference.layer_forward is model.layer_forward

@@ -212,6 +212,48 @@ def test_bf16_head_dim_128_cache_matches_fresh_prefill():
     assert out["generated_tokens"] == 20
 
 
+def test_committed_token_continues_as_latent_after_injection():
+    """tests/test_inference.py:86-113 restated: the decoder's layer calls go
+    through the module-level ``alodlm_amd.inference.layer_forward``
+    (alodlm/inference.py:11,84), so a patched layer sees every core input.
+    Row 0 commits on pass one (left-to-right, q = 1), restarts pass two from
+    its token's embedding, and pass three carries the normalised output of
+    pass two's core forward."""
+    from unittest.mock import patch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    from alodlm_amd.config import ModelConfig
+    from alodlm_amd.inference import DecodeConfig, Decoder, PrefixCache
+    from alodlm_amd.model import ALoDLM
+    log("latent carry through the patched layer_forward")
+    torch.manual_seed(42)
+    backbone = Qwen3ForCausalLM(Qwen3Config(
+        hidden_size=32, intermediate_size=64, num_hidden_layers=3, num_attention_heads=4,
+        num_key_value_heads=2, head_dim=8, vocab_size=64, max_position_embeddings=128,
+        bos_token_id=1, eos_token_id=2, pad_token_id=0))
+    model = ALoDLM(backbone, ModelConfig(loop_start=1, loop_end=2, mask_token_id=3,
+                                         block_size=4)).to(DEV)
+    cfg = DecodeConfig(q=1, tau=0, mode="left1", max_new_tokens=4)
+    core_inputs = []
+
+    def record_layer(layer, hidden, cos, sin, mask, prefix=None):
+        if layer is model.backbone.model.layers[1]:
+            core_inputs.append(hidden.clone())
+        result = hidden + torch.arange(hidden.shape[-1], dtype=hidden.dtype,
+                                       device=hidden.device) / 32
+        return result, (hidden.unsqueeze(1), hidden.unsqueeze(1))
+
+    ids = torch.full((4,), model.config.mask_token_id, device=DEV)
+    rows = torch.arange(4, device=DEV)
+    with torch.inference_mode(), patch("alodlm_amd.inference.layer_forward", record_layer):
+        Decoder(model, tokenizer())._window(ids, rows, PrefixCache(model.config), rows, cfg, rows)
+    assert len(core_inputs) == 4
+    assert not torch.equal(core_inputs[1][0], core_inputs[2][0])
+    with torch.inference_mode():
+        expected = model.backbone.model.norm(
+            core_inputs[1] + torch.arange(32, dtype=core_inputs[1].dtype, device=DEV) / 32)
+    torch.testing.assert_close(core_inputs[2][0], expected[0])
+
+
 def test_invalid_decode_config_and_context_fail():
     """tests/test_inference.py:115-122."""
     from alodlm_amd.inference import DecodeConfig, Decoder

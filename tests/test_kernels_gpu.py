@@ -435,7 +435,7 @@ def test_objective_kernel_matches_oracle(K, depths):
     ad, bd = ar_target.to(DEV), bounds.to(DEV)
     L.call("alodlm_objective", L.ptr(gd), L.ptr(ed), L.ptr(md), L.ptr(pd), L.ptr(cfd), L.ptr(cfd),
            L.ptr(ad), L.ptr(bd), 3, rows, K, cfg.depth_prior_c,
-           cfg.kl_beta_mi, cfg.kl_beta_marg, L.ptr(out), L.ptr(dgate), L.ptr(ws), st())
+           cfg.kl_beta_mi, cfg.kl_beta_marg, None, L.ptr(out), L.ptr(dgate), L.ptr(ws), st())
     torch.cuda.synchronize()
     out = out.cpu().double()
     assert abs(out[0] - total.item()) < 1e-5 * max(1, abs(total.item()))

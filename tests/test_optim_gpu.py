@@ -170,6 +170,32 @@ def test_fused_optimizer_reads_float32_gradients():
                                    msg=name)
 
 
+def test_model_zero_grad_clears_bound_float32_gradients():
+    """With a bound FusedAdamW, ``model.zero_grad()`` (nn.Module's, the loop
+    model.zero_grad(); loss.backward(); opt.step()) clears the float32
+    gradients too: each backward after it gives the gradients of that step
+    alone, bit for bit the gradients of a fresh model on the same step."""
+    from alodlm_amd.optim import FusedAdamW, param_groups
+    model, obj, ids, bounds = _tiny_bf16(seed=8)
+    fresh, _, _, _ = _tiny_bf16(seed=8)
+    FusedAdamW(param_groups(model, 0.01), lr=1e-3, max_grad_norm=1.0)
+    FusedAdamW(param_groups(fresh, 0.01), lr=1e-3, max_grad_norm=1.0)
+    for seed in (8, 9, 10):
+        kw = _step_inputs(obj, ids, bounds, seed)
+        model.zero_grad()
+        loss, _ = model(ids.to(DEV), ids.to(DEV), bounds, **kw)
+        loss.backward()
+        if fresh._engine is not None:
+            fresh._engine.grads_pending = False   # a fresh step: the arena is overwritten
+        loss_f, _ = fresh(ids.to(DEV), ids.to(DEV), bounds, **kw)
+        loss_f.backward()
+        got, want = model.float32_grads(), fresh.float32_grads()
+        for name in want:
+            assert torch.equal(got[name], want[name]), (seed, name)
+    model.zero_grad()
+    assert model.float32_grads() is None
+
+
 def test_moving_bound_parameters_is_refused():
     """After a FusedAdamW bound the model's parameters, re-homing a parameter
     (which would leave the optimizer's tables pointing at freed memory) makes

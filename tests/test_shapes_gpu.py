@@ -209,7 +209,8 @@ def _check_sampled_ce(state, lm_head, count=64, seed=0):
     """Cross-entropies of sampled loss-bearing rows against a float32 CPU
     recompute from the step's readout rows: logits rounded to bf16 as the
     LM-head product stores them, CE = logsumexp - logit[target] rounded to
-    bf16 (alodlm/model.py:180-181 in bf16)."""
+    bf16 (alodlm/model.py:180-181 in bf16); and their token entropies
+    -sum p log p of the same logits (alodlm/inference.py:114-117) to 2e-3."""
     b = state["batch"]
     W = lm_head.detach().float().cpu()
     g = torch.Generator().manual_seed(seed)
@@ -229,6 +230,10 @@ def _check_sampled_ce(state, lm_head, count=64, seed=0):
         got = state["ce"][d].cpu()[rows]
         for r, v in zip(ref.tolist(), got.tolist()):
             assert abs(v - r) <= _bf16_ulp(r) + 2e-3, (d, v, r)
+        logp = logits.log_softmax(-1)
+        ent = -(logp.exp() * logp).sum(-1)
+        got_ent = state["entropy"][d].cpu()[rows]
+        assert bool(((got_ent - ent).abs() <= 2e-3).all()), (d, (got_ent - ent).abs().max())
         checked += len(rows)
     assert checked >= count // 2
 
@@ -385,3 +390,102 @@ def test_full_8b_step_properties():
     # pass is split by query head
     assert _lib.query("alodlm_attention_bwd_workspace", 4096, 32, 8, 128, 32, 0) > 2 * 4096 * 32
     _full_size("8b", seed=22)
+
+
+def _sample_cosines(named, g, prefix=""):
+    """Cosine of each gradient's strided sample (tests/golden.sample_indices,
+    4096 elements) against the golden's ``prefix + gsample_`` vectors, by
+    golden parameter name."""
+    from tests.golden import sample_indices
+    out = {}
+    for name in g["param_names"]:
+        grad = named[name].double().flatten()
+        mine = grad[torch.as_tensor(sample_indices(grad.numel(), 4096))]
+        out[str(name)] = cosine(mine, torch.as_tensor(g[prefix + "gsample_" + name]))
+    return out
+
+
+def test_1p7b_layer_shapes_match_reference_bf16_run():
+    """The reference's own bf16 step at Qwen3-1.7B layer shapes
+    (tests/golden/step_1p7b_layers_bf16.npz: hidden 2048, 16 / 8 heads of 128,
+    SwiGLU 6144, vocabulary 151936, two layers as the recurrent core, one
+    2048-token segment; the reference loaded in bf16 as its training does),
+    and its float32 step on the same weights with the same exits.
+
+    Masks are bit-exact (the reference's CPU draws replayed); the step takes
+    the reference run's exits (uniforms replayed to them) so that both runs
+    score the same rows.  Against the reference's bf16 run: per-row masked
+    cross-entropies within two bf16 steps, halting probabilities within 5e-2
+    (mean 5e-3), the loss within 1e-2, gradient norms within 3 % and gradient
+    samples at cosine >= 0.999 (the 4-element depth bias and the 1-element
+    gate bias, score-function sums, at 0.99).  The reference's own bf16 run
+    is held to the same bounds against its float32 run, which is what makes
+    them the right size: the HIP step is no further from either reference run
+    than they are from each other."""
+    from tests import golden
+    from tests.helpers import cpu_draws
+    g = golden.load("step_1p7b_layers_bf16")
+    seed = int(g["seed"])
+    dims = _dims(2048, 16, 8, 6144, layers=2)
+    obj = O.Objective(loop_start=0, loop_end=2, mask_token_id=MASK_ID, block_size=32)
+    K = obj.max_depth
+    params = _bf16_params(dims, obj, seed=seed)
+    model = make_model(dims, obj, {k: v.float() for k, v in params.items()}, dtype=torch.bfloat16)
+    ids, labels = torch.as_tensor(g["in_ids"]), torch.as_tensor(g["in_labels"])
+    bounds = torch.as_tensor(g["in_boundaries"])
+    draws, _ = cpu_draws(labels, bounds, obj.block_size, seed, K)
+    ref_exits = torch.as_tensor(g["exits"])
+    log("1.7B layer shapes against the reference's bf16 and float32 runs")
+    engine = model.engine()
+    out, state = engine.forward(ids.cuda(), labels.cuda(), bounds, True, draws=draws,
+                                exit_uniforms=[u.cuda() for u in _replay_uniforms(ref_exits, K)])
+    grads = engine.backward(state, 1.0)
+    torch.cuda.synchronize()
+    out = out.cpu().double()
+    b = state["batch"]
+    for key in ("ids", "original", "positions", "masked", "mask_probability", "boundaries"):
+        np.testing.assert_array_equal(getattr(b, key).cpu().numpy(), g[key], err_msg=key)
+    assert torch.equal(state["exits"].cpu().long(), ref_exits.long())
+    masked = b.masked.cpu()
+    live = torch.arange(K)[:, None] < ref_exits[masked][None, :]
+    hip_ce = state["ce"].cpu()[:, masked].double()[live]
+    ref_ce = torch.as_tensor(g["ce"]).double()[live]
+    f32_ce = torch.as_tensor(g["f32_ce"]).double()[live]
+    ulp = torch.tensor([_bf16_ulp(v) for v in ref_ce.tolist()], dtype=torch.float64)
+    assert bool(((hip_ce - ref_ce).abs() <= 2 * ulp + 1e-3).all())
+    hazards = lambda x: torch.sigmoid(torch.as_tensor(x).double())
+    hip_h, ref_h, f32_h = (hazards(state["gates"].cpu()), hazards(g["gates"]),
+                           hazards(g["f32_gates"]))
+    named = {n: engine.arena.view(grads, n).cpu() for n in engine.arena.names}
+    named = {(n[len("backbone."):] if n.startswith("backbone.") else n): v
+             for n, v in named.items()}
+    report = {}
+    for label, loss, h, cos, norms in (
+            ("hip vs reference bf16", out[0], hip_h, _sample_cosines(named, g), None),
+            ("hip vs reference fp32", out[0], hip_h, None, None),
+            ("reference bf16 vs fp32", float(g["loss"]), ref_h, None, None)):
+        base = float(g["f32_loss"]) if "fp32" in label else float(g["loss"])
+        hb = f32_h if "fp32" in label else ref_h
+        gap = (h - hb).abs()
+        report[label] = (abs(loss - base) / abs(base), gap.mean().item(), gap.max().item())
+    ref_cos = {str(n): cosine(torch.as_tensor(g["gsample_" + n]),
+                              torch.as_tensor(g["f32_gsample_" + n])) for n in g["param_names"]}
+    hip_f32_cos = _sample_cosines(named, g, prefix="f32_")
+    hip_cos = _sample_cosines(named, g)
+    log(f"loss hip {out[0]:.5f}, reference bf16 {float(g['loss']):.5f}, reference fp32 "
+        f"{float(g['f32_loss']):.5f}; (loss rel-err, halting |diff| mean, max): {report}")
+    log(f"worst gradient-sample cosine: hip vs ref bf16 {min(hip_cos.values()):.5f}, hip vs "
+        f"ref fp32 {min(hip_f32_cos.values()):.5f}, ref bf16 vs ref fp32 "
+        f"{min(ref_cos.values()):.5f}")
+    score_function = ("exit_gate.depth_bias", "exit_gate.net.bias")
+    for label, (rel, mean, top) in report.items():
+        assert rel <= 1e-2 and mean <= 5e-3 and top <= 5e-2, (label, rel, mean, top)
+    for name in g["param_names"]:
+        name = str(name)
+        floor = 0.99 if name in score_function else 0.999
+        for which, c in (("ref bf16", hip_cos[name]), ("ref fp32", hip_f32_cos[name]),
+                         ("ref bf16 vs fp32", ref_cos[name])):
+            assert c >= floor, (name, which, c)
+        norm = named[name].double().norm().item()
+        ref_norm = float(g["gnorm_" + name])
+        assert abs(norm - ref_norm) <= 3e-2 * ref_norm + 1e-12, (name, norm, ref_norm)

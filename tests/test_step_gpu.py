@@ -283,6 +283,52 @@ def test_tiny_step_without_masked_rows_or_targets():
     assert torch.equal(grads.cpu(), torch.zeros_like(grads.cpu()))
 
 
+def test_nonfinite_logits_or_readout_make_the_loss_nan():
+    """The reference adds 0 * sum(logits + gates) to the loss
+    (alodlm/model.py:186), over the logits of every row, so one non-finite
+    logit anywhere makes the loss NaN while the metrics keep their values.
+    On a pack whose labels are all ignored (no row carries loss, so no logit
+    is computed here and every metric is 0): a finite model gives loss 0; a
+    -inf or NaN LM-head weight (a non-finite logits column in every row)
+    gives NaN; so does an infinite embedding row (non-finite readout rows,
+    hence non-finite gate logits).  With loss-bearing rows a -inf LM-head
+    weight gives NaN as well."""
+    log("tiny step, non-finite LM head / readout")
+    dims, obj = TINY
+    params = O.init_params(dims, obj.gate_init_pi, seed=4)
+    model = make_model(dims, obj, params)
+    ids, _, bounds = _tiny_inputs(seed=4)
+    labels = torch.full_like(ids, -100)
+    engine = model.engine()
+    gen = torch.Generator(device="cuda").manual_seed(4)
+
+    def run(lab):
+        out, _ = engine.forward(ids.cuda(), lab.cuda(), bounds, False, generator=gen)
+        return out.cpu()
+
+    assert torch.equal(run(labels)[:9], torch.zeros(9))
+    W = model.backbone.lm_head.weight
+    E = model.backbone.model.embed_tokens.weight
+    for bad in (float("-inf"), float("nan")):
+        with torch.no_grad():
+            keep = W[5, 7].item()
+            W[5, 7] = bad
+        out = run(labels)
+        assert torch.isnan(out[0]), bad
+        assert torch.equal(out[1:9], torch.zeros(8)), bad
+        with torch.no_grad():
+            W[5, 7] = keep
+    assert torch.equal(run(labels)[:9], torch.zeros(9))
+    with torch.no_grad():
+        row = E[int(ids[0])].clone()
+        E[int(ids[0])] = float("inf")
+    assert torch.isnan(run(labels)[0])
+    with torch.no_grad():
+        E[int(ids[0])] = row
+        W[5, 7] = float("-inf")
+    assert torch.isnan(run(ids)[0])
+
+
 def test_tiny_step_without_masked_rows_matches_oracle():
     """Masking draws that mask nothing (every block's count round(n * p) = 0):
     M = 0, so the objective is the autoregressive loss alone; loss and every

@@ -257,6 +257,14 @@ def test_training_state_restores_into_the_reference(tmp_path):
     assert ref_sched.get_last_lr() == sched.get_last_lr()
     assert [g["lr"] for g in ref_opt.param_groups] == [g["lr"] for g in opt.param_groups]
     assert torch.equal(torch.rand(3), expect)
+    # the saved groups carry the keys of the reference's own accelerate-saved
+    # optimizer state (initial_lr included), so a scheduler built later with
+    # last_epoch >= 0 finds its base rates
+    ours = torch.load(tmp_path / "state" / "optimizer.bin", weights_only=True)["param_groups"]
+    theirs = torch.load(REFERENCE_CHECKPOINT / "training_state" / "optimizer.bin",
+                        weights_only=True)["param_groups"]
+    assert [set(g) for g in ours] == [set(g) for g in theirs]
+    assert [g["initial_lr"] for g in ref_opt.param_groups] == [1e-5, 1e-5]
 
 
 def test_train_needs_gpu(tmp_path):
@@ -303,7 +311,17 @@ def _engine_for_keep(monkeypatch, alloc, peak, fused_state):
                          types.SimpleNamespace(state_bytes_to_come=lambda: fused_state * 2**30))
     e._keep, e._keep_rows, e._step_alloc, e._step_peak = None, 0, None, None
     values = iter(alloc)
-    monkeypatch.setattr("torch.cuda.memory_allocated", lambda dev=None: next(values) * 2**30)
+    last = {"bytes": 0}
+
+    def allocated(dev=None):
+        last["bytes"] = next(values) * 2**30
+        return last["bytes"]
+
+    # a 100 GiB device that this process alone uses, with no cached blocks
+    monkeypatch.setattr("torch.cuda.memory_allocated", allocated)
+    monkeypatch.setattr("torch.cuda.memory_reserved", lambda dev=None: last["bytes"])
+    monkeypatch.setattr("torch.cuda.mem_get_info",
+                        lambda dev=None: (100 * 2**30 - last["bytes"], 100 * 2**30))
     monkeypatch.setattr("torch.cuda.max_memory_allocated", lambda dev=None: peak * 2**30)
     monkeypatch.setattr("torch.cuda.reset_peak_memory_stats", lambda dev=None: None)
     monkeypatch.setattr("torch.cuda.get_device_properties", lambda dev=None: _FakeProps())
@@ -315,7 +333,8 @@ def test_keep_decision_counts_optimizer_state_not_yet_allocated(monkeypatch):
     any optimizer step) adds the bound FusedAdamW's state still to come; a
     decision after the first optimizer step has none to add.  With N = 262144
     rows and 16 layer applications the rotary q/k take 12 GiB and the norm
-    outputs 16 GiB; the budget is 95 GiB."""
+    outputs 16 GiB; the budget is 94 GiB (a 6 % margin of the 100 GiB
+    device)."""
     N = 262144
     # first forward: 20 GiB allocated; the step peaks at 50 GiB (growth 30)
     e = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=30)
@@ -329,7 +348,7 @@ def test_keep_decision_counts_optimizer_state_not_yet_allocated(monkeypatch):
     e2._decide_keep(N)
     e2._step_peak = 50 * 2**30
     assert e2._decide_keep(N) == (True, False)
-    # a smaller pack keeps both: 80 + 6 + 8 <= 95
+    # a smaller pack keeps both: 80 + 6 + 8 <= 94
     e3 = _engine_for_keep(monkeypatch, [20, 20], 50, fused_state=30)
     e3._decide_keep(N // 2)
     e3._step_peak = 50 * 2**30
