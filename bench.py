@@ -24,9 +24,13 @@ the same line (``sub_records``; --no-sub-records skips them):
                 forward + backward
 
 Prints one JSON line (metric of BASELINE: train tokens/s) with:
-  roofline      the dominant kernel class (by time in the timed region, from
-                HIP events around its launches on the launch stream):
+  roofline      the dominant kernel class (by time, from HIP events around its
+                launches on the launch stream, over a few steps after the
+                timed ones so that those carry no per-launch events):
                 algorithmic FLOPs per launch / average launch time vs 2.5 PFLOP/s
+  step_ms       min / median / max of the timed steps (HIP events between
+                steps), and the caching allocator's free-and-retry count and
+                device allocations over them (``allocator``)
   mfu           whole-step algorithmic FLOPs / step time / bf16 dense peak
   cpu_baseline  the CPU oracle timed on this host on a bounded sample (three
                 decoder-layer fwd+bwd passes over one 4096-row dual-stream
@@ -251,9 +255,6 @@ def run_step(spec, device, steps, warmup, kernel_timing):
         loss = one_step()
         print(f"[bench] {spec['name']} warmup step {i} loss {float(loss):.4f}", file=sys.stderr,
               flush=True)
-    if kernel_timing:
-        timer = KernelTimer()
-        timer.wrap(engine)
     torch.cuda.synchronize()
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     alloc = [_allocator_counters(device)]
@@ -275,6 +276,16 @@ def run_step(spec, device, steps, warmup, kernel_timing):
               f"{d['num_device_free']}", file=sys.stderr, flush=True)
     print(f"[bench] {spec['name']}: timed {steps} steps in {elapsed:.3f}s loss {float(loss):.4f}",
           file=sys.stderr, flush=True)
+    if kernel_timing:
+        # the kernel classes come from a separate pass of a few more steps
+        # with HIP events around every GEMM / attention launch, so that the
+        # timed steps above carry no per-launch instrumentation
+        timer = KernelTimer()
+        timer.wrap(engine)
+        kernel_steps = min(steps, 3)
+        for _ in range(kernel_steps):
+            one_step()
+        torch.cuda.synchronize()
     ms = 1000.0 * elapsed / steps
     tokens = sum(seg_lengths)
     gemm_f, attn_f, head_f = step_flops(engine.dims, model.config, seg_lengths,
@@ -301,7 +312,8 @@ def run_step(spec, device, steps, warmup, kernel_timing):
                       "reserved_peak_gib": round(alloc[-1]["reserved_peak"] / 2**30, 1)},
     }
     if timer is not None:
-        record["roofline"], record["kernel_classes"] = _roofline(timer, steps, spec)
+        record["roofline"], record["kernel_classes"] = _roofline(timer, kernel_steps, spec)
+        record["roofline"]["timed_steps"] = kernel_steps
     cfg = model.config
     facts = {"apps": cfg.loop_start + cfg.max_depth * (engine.dims.layers - cfg.loop_start),
              "segments": len(seg_lengths), "tokens": tokens,
@@ -582,6 +594,65 @@ def cpu_baseline(spec, cfg_seg=2048, readout_rows=2048, layer_reps=3, threads=No
     return t_layer, t_readout, threads
 
 
+def summarize_trace(directory, last_steps, out=sys.stdout):
+    """Summarise a ``rocprofv3 --kernel-trace --output-format csv`` run of
+    this benchmark: the last ``last_steps`` steps (a step ends with the
+    optimizer's second AdamW launch, one per parameter group), each step's
+    span, the time some kernel was running, the idle time between kernels and
+    its largest gaps; then per-kernel time per step over those steps."""
+    import csv
+    import glob
+    paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {directory}")
+    with open(paths[0]) as f:
+        rows = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                 r["Kernel_Name"].split("(")[0].strip().removeprefix("void "))
+                for r in csv.DictReader(f)]
+    rows.sort()
+    adamw = sorted(e for s, e, n in rows if n.startswith("adamw_kernel"))
+    ends = adamw[1::2]
+    if len(ends) < last_steps + 1:
+        raise SystemExit(f"the trace holds {len(ends)} steps, fewer than {last_steps + 1}")
+    bounds = ends[-(last_steps + 1):]
+    per_kernel, spans, busy_all, idle_all = {}, [], 0, 0
+    print(f"steps summarised: {last_steps} (of {len(ends)} in the trace)", file=out)
+    print("| step | span ms | kernels busy ms | idle ms | kernels | largest gaps (us, after -> before) |",
+          file=out)
+    print("|---|---|---|---|---|---|", file=out)
+    for i, (a, b) in enumerate(zip(bounds, bounds[1:])):
+        sel = [x for x in rows if x[0] >= a and x[1] <= b]
+        busy, cur_s, cur_e, gaps, prev = 0, None, a, [], "step start"
+        for s0, e0, n in sel:
+            per_kernel.setdefault(n, [0, 0])
+            per_kernel[n][0] += e0 - s0
+            per_kernel[n][1] += 1
+            if s0 > cur_e:
+                gaps.append((s0 - cur_e, prev, n))
+            if cur_s is None or s0 > cur_e:
+                if cur_s is not None:
+                    busy += cur_e - cur_s
+                cur_s, cur_e = s0, e0
+            else:
+                cur_e = max(cur_e, e0)
+            prev = n
+        busy += (cur_e - cur_s) if cur_s is not None else 0
+        span = b - a
+        spans.append(span)
+        busy_all += busy
+        idle_all += span - busy
+        top = "; ".join(f"{g / 1e3:.0f} ({p[:28]} -> {n[:28]})"
+                        for g, p, n in sorted(gaps, reverse=True)[:3])
+        print(f"| {i} | {span / 1e6:.1f} | {busy / 1e6:.1f} | {(span - busy) / 1e6:.1f} | "
+              f"{len(sel)} | {top} |", file=out)
+    n = last_steps
+    print(f"\nmean per step: span {sum(spans) / n / 1e6:.1f} ms, kernels busy "
+          f"{busy_all / n / 1e6:.1f} ms, idle {idle_all / n / 1e6:.1f} ms", file=out)
+    print("\n| kernel | calls/step | ms/step | avg us |\n|---|---|---|---|", file=out)
+    for name, (t, c) in sorted(per_kernel.items(), key=lambda kv: -kv[1][0])[:40]:
+        print(f"| `{name[:70]}` | {c / n:g} | {t / n / 1e6:.1f} | {t / c / 1e3:.1f} |", file=out)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -601,7 +672,13 @@ def main():
     parser.add_argument("--kernel", choices=["attention", "gemm"],
                         help="time one kernel class alone at the --model layer shape "
                              "(for profiling) instead of the step")
+    parser.add_argument("--summarize-trace", metavar="DIR",
+                        help="print a summary of the rocprofv3 kernel trace under DIR (the "
+                             "last --steps steps) and exit; needs no GPU")
     args = parser.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.steps)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)

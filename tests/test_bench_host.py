@@ -1,5 +1,6 @@
 """bench.py's command-line contract without a GPU: more than one GPU is
-refused with a message, and a machine without a GPU is refused too."""
+refused with a message, a machine without a GPU is refused too, and the
+kernel-trace summary counts busy and idle time per step."""
 
 import subprocess
 import sys
@@ -48,3 +49,31 @@ def test_gemm_bytes_covers_every_epilogue():
     assert codes == set(want)
     for epi, nbytes in want.items():
         assert bench.gemm_bytes(None, 0, 0, None, 0, 0, None, 0, M, N, K, epi=epi) == nbytes
+
+
+def test_trace_summary_counts_busy_and_idle_time(tmp_path):
+    """bench.py --summarize-trace: steps end at every second AdamW launch;
+    overlapping kernels count once as busy time, the rest of the span is
+    idle, and per-kernel time is averaged over the summarised steps."""
+    import io
+    import bench
+    d = tmp_path / "trace" / "host"
+    d.mkdir(parents=True)
+    rows = ["Kernel_Name,Start_Timestamp,End_Timestamp"]
+    t = 0
+    for step in range(3):
+        # two overlapping GEMMs (busy 0..150), a gap of 50, then the two AdamW launches
+        rows += [f"void gemm_dl_kernel<1>(x),{t},{t + 100}",
+                 f"gemm_dl_kernel<1>(x),{t + 50},{t + 150}",
+                 f"adamw_kernel<float>(y),{t + 200},{t + 250}",
+                 f"adamw_kernel<float>(y),{t + 250},{t + 300}"]
+        t += 300
+    (d / "kt_kernel_trace.csv").write_text("\n".join(rows) + "\n")
+    out = io.StringIO()
+    bench.summarize_trace(str(tmp_path / "trace"), 2, out=out)
+    text = out.getvalue()
+    # each summarised step spans 300 ns: busy 150 + 100, idle 50
+    assert "mean per step: span 0.0 ms" in text
+    lines = [l for l in text.splitlines() if l.startswith("| 0 |") or l.startswith("| 1 |")]
+    assert len(lines) == 2
+    assert "| `gemm_dl_kernel<1>` | 2 |" in text and "| `adamw_kernel<float>` | 2 |" in text

@@ -409,19 +409,21 @@ def test_1p7b_layer_shapes_match_reference_bf16_run():
     """The reference's own bf16 step at Qwen3-1.7B layer shapes
     (tests/golden/step_1p7b_layers_bf16.npz: hidden 2048, 16 / 8 heads of 128,
     SwiGLU 6144, vocabulary 151936, two layers as the recurrent core, one
-    2048-token segment; the reference loaded in bf16 as its training does),
-    and its float32 step on the same weights with the same exits.
+    2048-token segment; the reference loaded in bf16 as its training loads
+    it), and its float32 step on the same weights with the same exits.
 
     Masks are bit-exact (the reference's CPU draws replayed); the step takes
     the reference run's exits (uniforms replayed to them) so that both runs
-    score the same rows.  Against the reference's bf16 run: per-row masked
-    cross-entropies within two bf16 steps, halting probabilities within 5e-2
-    (mean 5e-3), the loss within 1e-2, gradient norms within 3 % and gradient
-    samples at cosine >= 0.999 (the 4-element depth bias and the 1-element
-    gate bias, score-function sums, at 0.99).  The reference's own bf16 run
-    is held to the same bounds against its float32 run, which is what makes
-    them the right size: the HIP step is no further from either reference run
-    than they are from each other."""
+    score the same rows.  Against the reference's bf16 run: every live
+    masked cross-entropy within two bf16 steps; the denoising and
+    autoregressive terms within 1e-3; halting probabilities within 5e-2
+    (mean 5e-3).  The loss and the gradients are held to north_star's bounds
+    (loss 1e-2, gradient-sample cosine 0.999, norms 3 %) or, where the
+    reference's own bf16 run misses them against its float32 run (the actor
+    term: bf16 cross-entropies times sums of log q), to twice that gap:
+    measured on the fixture, the reference's loss moves 1.3e-2 and its gate
+    weight, gate bias and depth-bias gradients reach cosine 0.9987, 1 and
+    0.9957 with the gate bias's norm at 0.48 of the float32 one."""
     from tests import golden
     from tests.helpers import cpu_draws
     g = golden.load("step_1p7b_layers_bf16")
@@ -450,42 +452,39 @@ def test_1p7b_layer_shapes_match_reference_bf16_run():
     live = torch.arange(K)[:, None] < ref_exits[masked][None, :]
     hip_ce = state["ce"].cpu()[:, masked].double()[live]
     ref_ce = torch.as_tensor(g["ce"]).double()[live]
-    f32_ce = torch.as_tensor(g["f32_ce"]).double()[live]
     ulp = torch.tensor([_bf16_ulp(v) for v in ref_ce.tolist()], dtype=torch.float64)
-    assert bool(((hip_ce - ref_ce).abs() <= 2 * ulp + 1e-3).all())
-    hazards = lambda x: torch.sigmoid(torch.as_tensor(x).double())
-    hip_h, ref_h, f32_h = (hazards(state["gates"].cpu()), hazards(g["gates"]),
-                           hazards(g["f32_gates"]))
+    ce_diff = (hip_ce - ref_ce).abs()
+    assert bool((ce_diff <= 2 * ulp + 1e-3).all()), ce_diff.max()
+    hz = lambda x: torch.sigmoid(torch.as_tensor(x).double())
+    gap = (hz(state["gates"].cpu()) - hz(g["gates"])).abs()
+    assert gap.mean().item() <= 5e-3 and gap.max().item() <= 5e-2, (gap.mean(), gap.max())
+    for i, key in ((1, "denoising"), (8, "ar_loss")):
+        ref = float(g["metric_" + key])
+        assert abs(out[i] - ref) <= 1e-3 * abs(ref), (key, out[i], ref)
+    rel = lambda a, r: abs(a - r) / abs(r)
+    loss_b, loss_f = float(g["loss"]), float(g["f32_loss"])
+    ref_gap = rel(loss_b, loss_f)
+    log(f"loss: hip {out[0]:.4f}, reference bf16 {loss_b:.4f}, reference fp32 {loss_f:.4f}; "
+        f"rel-err hip vs bf16 {rel(out[0], loss_b):.2e}, hip vs fp32 {rel(out[0], loss_f):.2e}, "
+        f"reference bf16 vs fp32 {ref_gap:.2e}; CE |diff| mean {ce_diff.mean().item():.4f}; "
+        f"halting |diff| mean {gap.mean().item():.2e} max {gap.max().item():.2e}")
+    assert rel(out[0], loss_b) <= max(1e-2, 2 * ref_gap)
+    assert rel(out[0], loss_f) <= max(1e-2, 2 * ref_gap)
     named = {n: engine.arena.view(grads, n).cpu() for n in engine.arena.names}
-    named = {(n[len("backbone."):] if n.startswith("backbone.") else n): v
-             for n, v in named.items()}
-    report = {}
-    for label, loss, h, cos, norms in (
-            ("hip vs reference bf16", out[0], hip_h, _sample_cosines(named, g), None),
-            ("hip vs reference fp32", out[0], hip_h, None, None),
-            ("reference bf16 vs fp32", float(g["loss"]), ref_h, None, None)):
-        base = float(g["f32_loss"]) if "fp32" in label else float(g["loss"])
-        hb = f32_h if "fp32" in label else ref_h
-        gap = (h - hb).abs()
-        report[label] = (abs(loss - base) / abs(base), gap.mean().item(), gap.max().item())
-    ref_cos = {str(n): cosine(torch.as_tensor(g["gsample_" + n]),
-                              torch.as_tensor(g["f32_gsample_" + n])) for n in g["param_names"]}
-    hip_f32_cos = _sample_cosines(named, g, prefix="f32_")
-    hip_cos = _sample_cosines(named, g)
-    log(f"loss hip {out[0]:.5f}, reference bf16 {float(g['loss']):.5f}, reference fp32 "
-        f"{float(g['f32_loss']):.5f}; (loss rel-err, halting |diff| mean, max): {report}")
-    log(f"worst gradient-sample cosine: hip vs ref bf16 {min(hip_cos.values()):.5f}, hip vs "
-        f"ref fp32 {min(hip_f32_cos.values()):.5f}, ref bf16 vs ref fp32 "
-        f"{min(ref_cos.values()):.5f}")
-    score_function = ("exit_gate.depth_bias", "exit_gate.net.bias")
-    for label, (rel, mean, top) in report.items():
-        assert rel <= 1e-2 and mean <= 5e-3 and top <= 5e-2, (label, rel, mean, top)
+    hip_cos, hip_f32_cos = _sample_cosines(named, g), _sample_cosines(named, g, prefix="f32_")
+    worst = []
     for name in g["param_names"]:
         name = str(name)
-        floor = 0.99 if name in score_function else 0.999
-        for which, c in (("ref bf16", hip_cos[name]), ("ref fp32", hip_f32_cos[name]),
-                         ("ref bf16 vs fp32", ref_cos[name])):
-            assert c >= floor, (name, which, c)
+        ref_cos = cosine(torch.as_tensor(g["gsample_" + name]),
+                         torch.as_tensor(g["f32_gsample_" + name]))
+        floor = min(0.999, 1 - 2 * (1 - ref_cos))
         norm = named[name].double().norm().item()
-        ref_norm = float(g["gnorm_" + name])
-        assert abs(norm - ref_norm) <= 3e-2 * ref_norm + 1e-12, (name, norm, ref_norm)
+        norm_b, norm_f = float(g["gnorm_" + name]), float(g["f32_gnorm_" + name])
+        norm_tol = max(3e-2, 2 * rel(norm_b, norm_f))
+        worst.append((hip_cos[name], name, ref_cos))
+        assert hip_cos[name] >= floor, (name, hip_cos[name], ref_cos)
+        assert hip_f32_cos[name] >= floor, (name, hip_f32_cos[name], ref_cos)
+        assert rel(norm, norm_b) <= norm_tol, (name, norm, norm_b, norm_f)
+    worst.sort()
+    log("lowest gradient-sample cosines (hip vs reference bf16, reference bf16 vs fp32): " +
+        ", ".join(f"{n} {c:.5f} ({r:.5f})" for c, n, r in worst[:4]))
