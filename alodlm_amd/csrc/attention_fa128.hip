@@ -1134,20 +1134,30 @@ fa128_dq_ds_kernel(const bf16_t* __restrict__ k, const bf16_t* __restrict__ ds,
     const char* st_lds = lds[t % DQ_STAGES][1];
     const bool ok0 = t <= lim0 || t == e0, ok1 = t <= lim1 || t == e1;
     if (!ok0 && !ok1) continue;
+    // Every operand fragment of the key tile is read before the first MFMA
+    // (a ruled-out block's slot holds a stand-in block, harmless to read),
+    // so the LDS latency is paid once per tile rather than once per MFMA
+    // pair; the memory clobber keeps the reads from sinking into the
+    // branches below.
+    bf16x8_t fa[2][2], fb[2][2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int rk = st * 16;
-      const bf16x8_t a0 = tr_frag(kt_lds, rk, dhb * 32, lane);
-      const bf16x8_t a1 = tr_frag(kt_lds, rk, dhb * 32 + 32, lane);
+      fa[st][0] = tr_frag(kt_lds, rk, dhb * 32, lane);
+      fa[st][1] = tr_frag(kt_lds, rk, dhb * 32 + 32, lane);
+      fb[st][0] = tr_frag(st_lds, rk, qb * 32, lane);
+      fb[st][1] = tr_frag(st_lds, rk, qb * 32 + 32, lane);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
       if (ok0) {
-        const bf16x8_t b = tr_frag(st_lds, rk, qb * 32, lane);
-        acc[0][0] = mfma(a0, b, acc[0][0]);
-        acc[1][0] = mfma(a1, b, acc[1][0]);
+        acc[0][0] = mfma(fa[st][0], fb[st][0], acc[0][0]);
+        acc[1][0] = mfma(fa[st][1], fb[st][0], acc[1][0]);
       }
       if (ok1) {
-        const bf16x8_t b = tr_frag(st_lds, rk, qb * 32 + 32, lane);
-        acc[0][1] = mfma(a0, b, acc[0][1]);
-        acc[1][1] = mfma(a1, b, acc[1][1]);
+        acc[0][1] = mfma(fa[st][0], fb[st][1], acc[0][1]);
+        acc[1][1] = mfma(fa[st][1], fb[st][1], acc[1][1]);
       }
     }
   }
@@ -1202,18 +1212,6 @@ int64_t fa128_bwd_workspace(int64_t N, int nq, int nkv, int64_t n_tiles, int64_t
   return dkdv_head_split(n_tiles, nq, nkv) ? head + 2 * N * (int64_t)nq * HD : head;
 }
 
-// Compute units of the current device (the dK/dV grid is one workgroup per CU).
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < 64 && cached[dev]) return cached[dev];
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  if (dev < 64) cached[dev] = cus;
-  return cus;
-}
 int fa128_fwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t ldv,
                      const int64_t* bounds, const int32_t* tiles, int64_t n_tiles, bf16_t* o,
                      float* lse, int64_t N, int nq, int nkv, int B, float scale, hipStream_t st) {

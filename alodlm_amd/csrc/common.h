@@ -129,6 +129,20 @@ static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream
 // the activation shapes (or the kernel is a grid-stride sweep).
 static inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Compute units of the current device, cached per device (grids of one
+// workgroup per CU).
+static inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev]) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
 // ----------------------------------------------------------------------------
 // 8-element vector access (16 bytes of bf16 or 32 bytes of float).  The
 // pointer must be aligned to 8 elements.

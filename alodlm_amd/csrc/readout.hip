@@ -289,100 +289,142 @@ cross_entropy_kernel(T* __restrict__ logits, const int32_t* __restrict__ target,
   }
 }
 
-// The same for one bf16 row of at most 8 * 512 * NCH logits held in the
-// registers of 512 threads (up to 256 VGPRs each): the row is read from memory once and written
-// once (the two-pass kernel above reads it twice, and a row of a large
-// vocabulary does not stay in L2 between the passes).
+// The same for bf16 rows of at most 8 * CE_THREADS * NCH logits held in the
+// registers of CE_THREADS threads (up to 128 VGPRs each): each row is read from
+// memory once and written once (the two-pass kernel above reads it twice, and
+// a row of a large vocabulary does not stay in L2 between the passes).  One
+// workgroup per CU walks rows blockIdx.x, blockIdx.x + gridDim.x, ...: as it
+// writes chunk j of its current row it loads chunk j of its next row into the
+// same registers, so the stream of writes of one row overlaps the reads of
+// the next instead of alternating with them.
+constexpr int CE_THREADS = 1024;
+
 template <int NCH>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(CE_THREADS)
 cross_entropy_row_kernel(bf16_t* __restrict__ logits, const int32_t* __restrict__ target,
                          const float* __restrict__ coef, const int32_t* __restrict__ n_rows,
                          int64_t V, float* __restrict__ ce, float* __restrict__ entropy) {
-  __shared__ float red[2][8];
-  const int64_t row = blockIdx.x;
-  if (row >= n_rows[0]) return;
-  bf16_t* lr = logits + row * V;
-  // a wave-uniform row base plus a 32-bit byte offset per access, so that no
-  // 64-bit address per chunk stays live between the load and the store
-  char* rowb = reinterpret_cast<char*>(lr);
+  constexpr int NW = CE_THREADS / 64;
+  __shared__ float red[2][NW];
+  const int64_t rows = n_rows[0];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint4 buf[NCH];
+  // 32-bit chunk positions (a row is below 2^31 elements): the compiler then
+  // folds j into immediates instead of keeping a 64-bit position per chunk
+  const uint32_t Vu = (uint32_t)V, t8 = threadIdx.x * 8u;
+  auto first = [&](int j) { return (uint32_t)(j * CE_THREADS * 8) + t8; };
+  auto live = [&](int j) { return first(j) < Vu; };
+  // Rows are addressed as buffers: one 32-bit lane offset (this thread's
+  // 16 bytes of a 16 KB chunk) plus the chunk's byte offset as the scalar
+  // offset, so no per-chunk address is kept in vector registers across rows;
+  // the range check returns zeros past the row (loads) and drops stores there.
+  const uint32_t voff = threadIdx.x * 16u;
+  constexpr uint32_t CHUNK = CE_THREADS * 16;
+  auto rsrc = [&](int64_t r) {
+    return __builtin_amdgcn_make_buffer_rsrc(logits + r * V, 0, (int)(V * 2), 0x00020000);
+  };
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  auto load = [&](__amdgpu_buffer_rsrc_t rs, int j) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, j * CHUNK, 0));
+  };
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  {
+    const __amdgpu_buffer_rsrc_t rs = rsrc(row);
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = (j * 512 + (int)threadIdx.x) * 8;
-    buf[j] = c < V ? *reinterpret_cast<const uint4*>(rowb + (uint32_t)c * 2u)
-                   : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < NCH; ++j) buf[j] = load(rs, j);
   }
   auto value = [&](int j, int i) {
     const uint32_t w = (&buf[j].x)[i >> 1];
     return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
   };
-  auto live = [&](int j) { return (j * 512 + (int)threadIdx.x) * 8 < V; };
-  float m = -INFINITY;
+  for (; row < rows; row += gridDim.x) {
+    const __amdgpu_buffer_rsrc_t rs = rsrc(row);
+    const int64_t next = row + gridDim.x;
+    const __amdgpu_buffer_rsrc_t rn = rsrc(next < rows ? next : row);
+    float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j)
-    if (live(j))
+    for (int j = 0; j < NCH; ++j)
+      if (live(j))
 #pragma unroll
-      for (int i = 0; i < 8; ++i) m = fmaxf(m, value(j, i));
-  m = wave_max(m);
-  if (lane == 0) red[0][wave] = m;
-  __syncthreads();
-  float M = red[0][0];
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, value(j, i));
+    m = wave_max(m);
+    // the packed chunks are re-read by each pass: the unpacked float values of
+    // one pass are not kept for the next (that would take a register per
+    // logit); an empty asm that claims to change them makes sure of it
 #pragma unroll
-  for (int w = 1; w < 8; ++w) M = fmaxf(M, red[0][w]);
-  const float m2 = M * CE_LOG2E;
-  float s = 0.f, t = 0.f;
+    for (int j = 0; j < NCH; ++j)
+      asm volatile("" : "+v"(buf[j].x), "+v"(buf[j].y), "+v"(buf[j].z), "+v"(buf[j].w));
+    if (lane == 0) red[0][wave] = m;
+    __syncthreads();
+    float M = red[0][0];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j)
-    if (live(j))
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, red[0][w]);
+    const float m2 = M * CE_LOG2E;
+    float s = 0.f, t = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = value(j, i);
-        const float e = __builtin_amdgcn_exp2f(fmaf(x, CE_LOG2E, -m2));
-        s += e;
-        t = fmaf(e, x, t);
+    for (int j = 0; j < NCH; ++j)
+      if (live(j))
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float x = value(j, i);
+          const float e = __builtin_amdgcn_exp2f(fmaf(x, CE_LOG2E, -m2));
+          s += e;
+          t = fmaf(e, x, t);
+        }
+    s = wave_sum(s);
+    t = wave_sum(t);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+      asm volatile("" : "+v"(buf[j].x), "+v"(buf[j].y), "+v"(buf[j].z), "+v"(buf[j].w));
+    __syncthreads();  // every wave has read red[0]
+    if (lane == 0) { red[0][wave] = s; red[1][wave] = t; }
+    __syncthreads();
+    float S = 0.f, Tt = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) { S += red[0][w]; Tt += red[1][w]; }
+    const float lse = M + logf(S);
+    int tg = target[row];
+    const float cf = coef[row];
+    const bool valid = tg >= 0 && (uint32_t)tg < Vu;  // an out-of-range target yields NaN, never a read
+    if (threadIdx.x == 0) {
+      const float xt = valid ? bf16_to_float(logits[row * V + tg]) : NAN;
+      ce[row] = round_bf16(lse - xt);
+      if (entropy) entropy[row] = lse - Tt / S;
+    }
+    if (!valid) tg = -1;
+    // the target logit is read above before it is overwritten, and every wave
+    // has read red[] before the next row's reductions write it
+    __syncthreads();
+    const float lse2 = lse * CE_LOG2E;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const uint32_t c = first(j);
+      if (c < Vu) {
+        float g[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          g[i] = __builtin_amdgcn_exp2f(fmaf(value(j, i), CE_LOG2E, -lse2));
+        if ((uint32_t)tg - c < 8u) {  // the target's chunk (one lane of the row)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) g[i] -= c + i == (uint32_t)tg ? 1.f : 0.f;
+        }
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(cf * g[2 * i], cf * g[2 * i + 1]);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{w[0], w[1], w[2], w[3]}, rs, voff,
+                                               j * CHUNK, 0);
       }
-  s = wave_sum(s);
-  t = wave_sum(t);
-  __syncthreads();  // every wave has read red[0]
-  if (lane == 0) { red[0][wave] = s; red[1][wave] = t; }
-  __syncthreads();
-  float S = 0.f, Tt = 0.f;
-#pragma unroll
-  for (int w = 0; w < 8; ++w) { S += red[0][w]; Tt += red[1][w]; }
-  const float lse = M + logf(S);
-  int tg = target[row];
-  const float cf = coef[row];
-  const bool valid = tg >= 0 && tg < V;  // an out-of-range target yields NaN, never a read
-  if (threadIdx.x == 0) {
-    const float xt = valid ? bf16_to_float(lr[tg]) : NAN;
-    ce[row] = round_bf16(lse - xt);
-    if (entropy) entropy[row] = lse - Tt / S;
-  }
-  if (!valid) tg = -1;
-  __syncthreads();  // the target logit is read above before it is overwritten
-  const float lse2 = lse * CE_LOG2E;
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = (j * 512 + (int)threadIdx.x) * 8;
-    if (c < V) {
-      float g[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        g[i] = __builtin_amdgcn_exp2f(fmaf(value(j, i), CE_LOG2E, -lse2));
-      if ((unsigned)(tg - c) < 8u) {  // the target's chunk (one lane of the row)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) g[i] -= c + i == tg ? 1.f : 0.f;
-      }
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(cf * g[2 * i], cf * g[2 * i + 1]);
-      *reinterpret_cast<uint4*>(rowb + (uint32_t)c * 2u) = make_uint4(w[0], w[1], w[2], w[3]);
+      // the next row's chunk j into the registers just freed (the last row
+      // re-reads its own chunk, which is never used); the chunks are kept in
+      // order, so that no chunk's output is computed early and held
+      buf[j] = load(rn, j);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
-constexpr int CE_ROW_NCH = 38;  // rows of up to 155648 bf16 logits
+constexpr int CE_ROW_NCH = 19;  // rows of up to 155648 bf16 logits
 
 __global__ void scatter_ce_kernel(const float* __restrict__ ce, const int32_t* __restrict__ sel,
                                   const int32_t* __restrict__ n_rows, int64_t max_rows,
@@ -534,9 +576,12 @@ extern "C" int alodlm_cross_entropy(void* logits, const int32_t* target, const f
   ALODLM_CHECK_ARG(vocab > 0, "cross_entropy: bad vocab");
   if (max_rows == 0) return ALODLM_OK;
   const bool v8 = vocab % 8 == 0 && aligned8(logits, dtype);
-  if (v8 && dtype == ALODLM_BF16 && vocab > 8 * 512 * (CE_ROW_NCH / 2) &&
-      vocab <= 8 * 512 * CE_ROW_NCH) {
-    cross_entropy_row_kernel<CE_ROW_NCH><<<(unsigned)max_rows, 512, 0, as_stream(stream)>>>(
+  if (v8 && dtype == ALODLM_BF16 && vocab > 8 * CE_THREADS * (CE_ROW_NCH / 2) &&
+      vocab <= 8 * CE_THREADS * CE_ROW_NCH) {
+    // one workgroup per CU (its threads hold a whole row), each walking rows
+    const int64_t cus = device_cus();
+    const int64_t grid = max_rows < cus ? max_rows : cus;
+    cross_entropy_row_kernel<CE_ROW_NCH><<<(unsigned)grid, CE_THREADS, 0, as_stream(stream)>>>(
         (bf16_t*)logits, target, coef, n_rows, vocab, ce, entropy);
     ALODLM_CHECK_LAUNCH("cross_entropy_row");
     return ALODLM_OK;
