@@ -147,16 +147,29 @@ static inline int device_cus() {
 // 8-element vector access (16 bytes of bf16 or 32 bytes of float).  The
 // pointer must be aligned to 8 elements.
 // ----------------------------------------------------------------------------
+// 8 consecutive elements as floats.  load_nt / store_nt are the same accesses
+// marked non-temporal, for streams read or written once that are much larger
+// than the caches.
+typedef unsigned nt_u32x4_t __attribute__((ext_vector_type(4)));
+typedef float nt_f32x4_t __attribute__((ext_vector_type(4)));
 template <typename T> struct Vec8;
 template <> struct Vec8<bf16_t> {
-  static __device__ __forceinline__ void load(const bf16_t* p, float* v) {
-    uint4 u = *reinterpret_cast<const uint4*>(p);
-    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  static __device__ __forceinline__ void unpack(const uint32_t* w, float* v) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = bf16_to_float((bf16_t)(w[i] & 0xffffu));
       v[2 * i + 1] = bf16_to_float((bf16_t)(w[i] >> 16));
     }
+  }
+  static __device__ __forceinline__ void load(const bf16_t* p, float* v) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    unpack(w, v);
+  }
+  static __device__ __forceinline__ void load_nt(const bf16_t* p, float* v) {
+    const nt_u32x4_t u = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    unpack(w, v);
   }
   static __device__ __forceinline__ void store(bf16_t* p, const float* v) {
     uint32_t w[4];
@@ -164,6 +177,14 @@ template <> struct Vec8<bf16_t> {
     for (int i = 0; i < 4; ++i)
       w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  static __device__ __forceinline__ void store_nt(bf16_t* p, const float* v) {
+    nt_u32x4_t w;
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+    w.z = pack_bf16x2(v[4], v[5]);
+    w.w = pack_bf16x2(v[6], v[7]);
+    __builtin_nontemporal_store(w, reinterpret_cast<nt_u32x4_t*>(p));
   }
 };
 template <> struct Vec8<float> {
@@ -173,9 +194,21 @@ template <> struct Vec8<float> {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   }
+  static __device__ __forceinline__ void load_nt(const float* p, float* v) {
+    const nt_f32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4_t*>(p));
+    const nt_f32x4_t b = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4_t*>(p) + 1);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
   static __device__ __forceinline__ void store(float* p, const float* v) {
     reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
     reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  static __device__ __forceinline__ void store_nt(float* p, const float* v) {
+    __builtin_nontemporal_store(nt_f32x4_t{v[0], v[1], v[2], v[3]},
+                                reinterpret_cast<nt_f32x4_t*>(p));
+    __builtin_nontemporal_store(nt_f32x4_t{v[4], v[5], v[6], v[7]},
+                                reinterpret_cast<nt_f32x4_t*>(p) + 1);
   }
 };
 

@@ -24,16 +24,17 @@ __global__ void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ act,
   if (i >= rows * I) return;
   const int64_t r = i / I, c = i % I;
   float g[8], u[8], a[8];
+  // the streams are far larger than the caches and used once here: non-temporal
   if (W == 8) {
-    Vec8<T>::load(gu + r * 2 * I + c, g);
-    Vec8<T>::load(gu + r * 2 * I + I + c, u);
+    Vec8<T>::load_nt(gu + r * 2 * I + c, g);
+    Vec8<T>::load_nt(gu + r * 2 * I + I + c, u);
   } else {
     g[0] = Elem<T>::load(gu, r * 2 * I + c);
     u[0] = Elem<T>::load(gu, r * 2 * I + I + c);
   }
 #pragma unroll
   for (int e = 0; e < W; ++e) a[e] = Elem<T>::round(g[e] / (1.0f + expf(-g[e]))) * u[e];
-  if (W == 8) Vec8<T>::store(act + i, a);
+  if (W == 8) Vec8<T>::store_nt(act + i, a);
   else Elem<T>::store(act, i, a[0]);
 }
 
@@ -50,9 +51,9 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restric
   const int64_t r = i / I, c = i % I;
   float g[8], u[8], da[8], dg[8], du[8], a[8];
   if (W == 8) {
-    Vec8<T>::load(gu + r * 2 * I + c, g);
-    Vec8<T>::load(gu + r * 2 * I + I + c, u);
-    Vec8<T>::load(dact + i, da);
+    Vec8<T>::load_nt(gu + r * 2 * I + c, g);
+    Vec8<T>::load_nt(gu + r * 2 * I + I + c, u);
+    Vec8<T>::load_nt(dact + i, da);
   } else {
     g[0] = Elem<T>::load(gu, r * 2 * I + c);
     u[0] = Elem<T>::load(gu, r * 2 * I + I + c);
@@ -66,9 +67,9 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restric
     a[e] = Elem<T>::round(g[e] / (1.0f + expf(-g[e]))) * u[e];
   }
   if (W == 8) {
-    Vec8<T>::store(dgu + r * 2 * I + c, dg);
-    Vec8<T>::store(dgu + r * 2 * I + I + c, du);
-    if (act) Vec8<T>::store(act + i, a);
+    Vec8<T>::store_nt(dgu + r * 2 * I + c, dg);
+    Vec8<T>::store_nt(dgu + r * 2 * I + I + c, du);
+    if (act) Vec8<T>::store_nt(act + i, a);
   } else {
     Elem<T>::store(dgu, r * 2 * I + c, dg[0]);
     Elem<T>::store(dgu, r * 2 * I + I + c, du[0]);

@@ -380,7 +380,7 @@ int64_t gemm_dl_store_splits(int64_t M, int64_t N, int64_t K);
 void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
-                    int64_t* nsplit_out, hipStream_t st);
+                    int64_t* nsplit_out, int first_into_c, hipStream_t st);
 
 // The 256x256 kernel takes the products whose output fills at least one tile.
 // The 256x256 kernel needs whole 64-deep k tiles for k-contiguous operands.
@@ -453,12 +453,16 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
     // partial buffer), then one reduction rounds their sum to bf16
     const int launch_epi = (epilogue == ALODLM_EPI_STORE && splits > 1) ? ALODLM_EPI_ACCUM : epilogue;
     int64_t nsplit = 1;
+    // an accumulated product's split 0 adds into C in its own epilogue, so the
+    // reduction reads one partial plane fewer: C = (C + p0) + (p1 + ... )
+    const int first_into_c = epilogue == ALODLM_EPI_ACCUM;
     gemm_dl_launch((const bf16_t*)A, lda, a_kmajor, (const bf16_t*)B, ldb, b_kmajor, C, ldc,
                    (const bf16_t*)R, ldr, M, N, K, alpha, launch_epi, workspace, splits, &nsplit,
-                   st);
+                   first_into_c, st);
     ALODLM_CHECK_LAUNCH("gemm_bf16_dl");
     if ((launch_epi == ALODLM_EPI_ACCUM || launch_epi == ALODLM_EPI_STORE_F32) && nsplit > 1) {
       if (epilogue == ALODLM_EPI_STORE) splitk_store(workspace, nsplit, M, N, (bf16_t*)C, ldc, st);
+      else if (first_into_c) splitk_reduce(workspace + M * N, nsplit - 1, M, N, (float*)C, ldc, st);
       else splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st,
                          epilogue == ALODLM_EPI_STORE_F32);
       ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");

@@ -45,7 +45,7 @@
 //
 // Workgroup -> tile order: consecutive workgroups land on different XCDs, so
 // the tile sequence is dealt out in contiguous chunks per XCD, then swept in
-// groups of 8 tile rows.
+// groups of 3 tile rows (down a group, then across).
 #include "common.h"
 #include "lds_dma.h"
 
@@ -166,7 +166,8 @@ template <bool AK, bool BK, int EPI, int NW, int KD, int STAGES>
 __global__ void __launch_bounds__(NW * 64, 1)
 gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
-               int64_t N, int64_t K, float alpha, int64_t k_per_split, float* __restrict__ partial) {
+               int64_t N, int64_t K, float alpha, int64_t k_per_split, float* __restrict__ partial,
+               int first_into_c) {
   static_assert(NW == 4, "the k-step schedule is written for 4 waves of 128x128");
   constexpr int WM = 128, WN = 128;
   constexpr int FI = WM / 32, FJ = WN / 32;
@@ -435,7 +436,10 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   // Direct epilogue (float outputs, and unaligned bf16 outputs): lane owns row
   // m = ... + col and columns n .. n+3 (n = 8*jj + 4*half).
   float* Cf = reinterpret_cast<float*>(C);
-  float* P = partial ? partial + (int64_t)blockIdx.y * M * N : nullptr;
+  // split 0 of an accumulated float product adds straight into C (the other
+  // splits' partials are added by the reduction after this kernel)
+  float* P = partial && !(first_into_c && blockIdx.y == 0)
+                 ? partial + (int64_t)blockIdx.y * M * N : nullptr;
   const int64_t ldo = P ? N : ldc;
   const bool vec = (ldo % 4 == 0) && (reinterpret_cast<uintptr_t>(P ? (void*)P : C) % 16 == 0) &&
                    (EPI != ALODLM_EPI_RESIDUAL ||
@@ -544,46 +548,49 @@ template <bool AK, bool BK, int NW, int KD, int ST>
 static void launch_dl(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                       int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N, int64_t K,
                       float alpha, int epi, float* part, int64_t kps, int64_t nsplit,
-                      hipStream_t st) {
+                      int first_into_c, hipStream_t st) {
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
   dim3 grid((unsigned)tiles, (unsigned)nsplit);
   if (epi == ALODLM_EPI_STORE)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
   else if (epi == ALODLM_EPI_RESIDUAL)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
   else if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE_F32, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
   else
     gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, NW, KD, ST><<<grid, NW * 64, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
 }
 
 template <bool AK, bool BK>
 static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                           int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
-                          int64_t nsplit, hipStream_t st) {
+                          int64_t nsplit, int first_into_c, hipStream_t st) {
   // 4 waves, 32-deep k stages in a ring of 4 (128 KB of LDS)
   launch_dl<AK, BK, 4, 32, 4>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
-                              nsplit, st);
+                              nsplit, first_into_c, st);
 }
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
-// splits > 1 (float-output epilogues only), the caller reduces it.
+// splits > 1 (float-output epilogues only), the caller reduces it.  With
+// `first_into_c` (an accumulated float product) split 0 adds its result into
+// C itself and its partial plane is left unwritten: the caller then adds
+// planes 1.. only.
 void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
-                    int64_t* nsplit_out, hipStream_t st) {
+                    int64_t* nsplit_out, int first_into_c, hipStream_t st) {
   int64_t kps = K;
   if (splits > 1) kps = (((K + splits - 1) / splits) + KMIN - 1) / KMIN * KMIN;
   const int64_t nsplit = (K + kps - 1) / kps;
   *nsplit_out = nsplit;
   float* p = ((epi == ALODLM_EPI_ACCUM || epi == ALODLM_EPI_STORE_F32) && nsplit > 1) ? part : nullptr;
-  if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
-  else launch_layout<false, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, st);
+  if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
+  else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
+  else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
+  else launch_layout<false, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
 }

@@ -218,8 +218,21 @@ rmsnorm_bwd_bf16_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict_
   for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += NORM_WAVES) {
     const bool skip = skip_exits && skip_exits[row] <= skip_depth;
     const float r = rstd[row];
-    uint4 ar[NCH], br[NCH];
+    uint4 ar[NCH], br[NCH], cr[NCH];
     float s = 0.f;
+    // At hidden 4096 (two waves per SIMD either way) the residual gradient is
+    // loaded with dy and x, so that its latency overlaps theirs instead of
+    // following the row's reduction (41.2 -> 39.9 us per 8B call); at 2048 the
+    // extra registers cost a wave per SIMD and the early load lost (107.9 ->
+    // 116.6 us per 1.7B call), so it is loaded in the second pass there.
+    constexpr bool early = NCH >= 8;
+    if (early && dres) {
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        const int64_t c = (int64_t)lane * 8 + 512 * t;
+        if (c < cols) cr[t] = *reinterpret_cast<const uint4*>(dres + row * cols + c);
+      }
+    }
 #pragma unroll
     for (int t = 0; t < NCH; ++t) {
       const int64_t c = (int64_t)lane * 8 + 512 * t;
@@ -249,8 +262,12 @@ rmsnorm_bwd_bf16_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict_
       const int64_t c = (int64_t)lane * 8 + 512 * t;
       if (c >= cols) continue;
       float o[8];
-      if (dres) Vec8<bf16_t>::load(dres + row * cols + c, o);
-      else {
+      if (early && dres) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = bf16_elem(cr[t], i);
+      } else if (dres) {
+        Vec8<bf16_t>::load(dres + row * cols + c, o);
+      } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = 0.f;
       }

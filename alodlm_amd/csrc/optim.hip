@@ -76,12 +76,15 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   float clip = 1.0f;
   if (total_norm) clip = fminf(1.0f, max_norm / (total_norm[0] + 1e-6f));
   const float decay = 1.0f - lr * weight_decay[t];
-  T* p = reinterpret_cast<T*>(params[t]);
-  float* w = master[t];
-  float* m = exp_avg[t];
-  float* v = exp_avg_sq[t];
-  const G* g = reinterpret_cast<const G*>(grads[t]);
-  const bool separate = reinterpret_cast<void*>(w) != reinterpret_cast<void*>(p);
+  // the tables hold generic pointers to device memory: the casts let every
+  // access be a global (not flat) memory instruction
+#define OPT_GLOBAL __attribute__((address_space(1)))
+  OPT_GLOBAL T* p = (OPT_GLOBAL T*)reinterpret_cast<T*>(params[t]);
+  OPT_GLOBAL float* w = (OPT_GLOBAL float*)master[t];
+  OPT_GLOBAL float* m = (OPT_GLOBAL float*)exp_avg[t];
+  OPT_GLOBAL float* v = (OPT_GLOBAL float*)exp_avg_sq[t];
+  const OPT_GLOBAL G* g = (const OPT_GLOBAL G*)reinterpret_cast<const G*>(grads[t]);
+  const bool separate = (const OPT_GLOBAL void*)w != (const OPT_GLOBAL void*)p;
   auto update = [&](float gi, float& wi, float& mi, float& vi) {
     gi *= clip;
     wi *= decay;
@@ -95,52 +98,79 @@ adamw_kernel(void* const* __restrict__ params, float* const* __restrict__ master
   // bytes (float) or 8 bytes (bf16)
   constexpr uintptr_t half = sizeof(T) == 2 ? 2 : 1;
   constexpr uintptr_t ghalf = sizeof(G) == 2 ? 2 : 1;
-  const uintptr_t align = reinterpret_cast<uintptr_t>(w + beg) | reinterpret_cast<uintptr_t>(m + beg) |
-                          reinterpret_cast<uintptr_t>(v + beg) |
-                          reinterpret_cast<uintptr_t>(g + beg) * ghalf |
-                          (separate ? reinterpret_cast<uintptr_t>(p + beg) * half : 0);
+  const uintptr_t align = (uintptr_t)(w + beg) | (uintptr_t)(m + beg) | (uintptr_t)(v + beg) |
+                          (uintptr_t)(g + beg) * ghalf | (separate ? (uintptr_t)(p + beg) * half : 0);
   if ((align & 15) == 0) {
-    // 4 elements per thread and step: 16-byte float32 state, 4 * sizeof(T)
-    // bytes of gradient and parameter (the same arithmetic per element)
+    // 4 elements per thread and group: 16-byte float32 state, 4 * sizeof(T)
+    // bytes of gradient and parameter (the same arithmetic per element).  Two
+    // groups per step, all their loads issued before either is updated (the
+    // stores would otherwise order every load after the previous group's
+    // stores), and every stream non-temporal: each byte is read and written
+    // once.
     const int64_t vec_end = beg + (end - beg) / 4 * 4;
-    for (int64_t j = beg + threadIdx.x * 4; j < vec_end; j += OPT_THREADS * 4) {
-      float4 w4 = *reinterpret_cast<const float4*>(w + j);
-      float4 m4 = *reinterpret_cast<const float4*>(m + j);
-      float4 v4 = *reinterpret_cast<const float4*>(v + j);
-      float gv[4], wv[4] = {w4.x, w4.y, w4.z, w4.w}, mv[4] = {m4.x, m4.y, m4.z, m4.w},
-                   vv[4] = {v4.x, v4.y, v4.z, v4.w};
+    constexpr int64_t STRIDE = OPT_THREADS * 4;
+    typedef float nt_f4 __attribute__((ext_vector_type(4)));
+    typedef unsigned nt_u2 __attribute__((ext_vector_type(2)));
+    auto load4f = [](const OPT_GLOBAL float* a) {
+      const nt_f4 q = __builtin_nontemporal_load((const OPT_GLOBAL nt_f4*)a);
+      return make_float4(q.x, q.y, q.z, q.w);
+    };
+    auto store4f = [](OPT_GLOBAL float* a, float x, float y, float z, float wv) {
+      __builtin_nontemporal_store(nt_f4{x, y, z, wv}, (OPT_GLOBAL nt_f4*)a);
+    };
+    auto load_g = [&](int64_t j, float* gv) {
       if constexpr (sizeof(G) == 2) {
-        const uint2 gr = *reinterpret_cast<const uint2*>(g + j);
+        const nt_u2 gr = __builtin_nontemporal_load((const OPT_GLOBAL nt_u2*)(g + j));
         gv[0] = bf16_to_float((bf16_t)(gr.x & 0xffff)); gv[1] = bf16_to_float((bf16_t)(gr.x >> 16));
         gv[2] = bf16_to_float((bf16_t)(gr.y & 0xffff)); gv[3] = bf16_to_float((bf16_t)(gr.y >> 16));
       } else {
-        const float4 g4 = *reinterpret_cast<const float4*>(g + j);
+        const float4 g4 = load4f((const OPT_GLOBAL float*)g + j);
         gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
       }
+    };
+    auto finish = [&](int64_t j, float* gv, float4 w4, float4 m4, float4 v4) {
+      float wv[4] = {w4.x, w4.y, w4.z, w4.w}, mv[4] = {m4.x, m4.y, m4.z, m4.w},
+            vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) update(gv[e], wv[e], mv[e], vv[e]);
-      *reinterpret_cast<float4*>(m + j) = make_float4(mv[0], mv[1], mv[2], mv[3]);
-      *reinterpret_cast<float4*>(v + j) = make_float4(vv[0], vv[1], vv[2], vv[3]);
-      *reinterpret_cast<float4*>(w + j) = make_float4(wv[0], wv[1], wv[2], wv[3]);
+      store4f(m + j, mv[0], mv[1], mv[2], mv[3]);
+      store4f(v + j, vv[0], vv[1], vv[2], vv[3]);
+      store4f(w + j, wv[0], wv[1], wv[2], wv[3]);
       if (separate) {
         if constexpr (sizeof(T) == 2) {
-          *reinterpret_cast<uint2*>(p + j) =
-              make_uint2(pack_bf16x2(wv[0], wv[1]),
-                         pack_bf16x2(wv[2], wv[3]));
+          __builtin_nontemporal_store(nt_u2{pack_bf16x2(wv[0], wv[1]), pack_bf16x2(wv[2], wv[3])},
+                                      (OPT_GLOBAL nt_u2*)(p + j));
         } else {
-          *reinterpret_cast<float4*>(p + j) = make_float4(wv[0], wv[1], wv[2], wv[3]);
+          store4f((OPT_GLOBAL float*)p + j, wv[0], wv[1], wv[2], wv[3]);
         }
       }
+    };
+    int64_t j = beg + threadIdx.x * 4;
+    for (; j + STRIDE < vec_end; j += 2 * STRIDE) {
+      const int64_t j2 = j + STRIDE;
+      float ga[4], gb[4];
+      const float4 wa = load4f(w + j), ma = load4f(m + j), va = load4f(v + j);
+      const float4 wb = load4f(w + j2), mb = load4f(m + j2), vb = load4f(v + j2);
+      load_g(j, ga);
+      load_g(j2, gb);
+      finish(j, ga, wa, ma, va);
+      finish(j2, gb, wb, mb, vb);
+    }
+    if (j < vec_end) {
+      float ga[4];
+      const float4 wa = load4f(w + j), ma = load4f(m + j), va = load4f(v + j);
+      load_g(j, ga);
+      finish(j, ga, wa, ma, va);
     }
     i = vec_end;
   }
   for (i += threadIdx.x; i < end; i += OPT_THREADS) {
     float wi = w[i], mi = m[i], vi = v[i];
-    update(Elem<G>::load(g, i), wi, mi, vi);
+    update(Elem<G>::load((const G*)g, i), wi, mi, vi);
     m[i] = mi;
     v[i] = vi;
     w[i] = wi;
-    if (separate) Elem<T>::store(p, i, wi);
+    if (separate) Elem<T>::store((T*)p, i, wi);
   }
 }
 

@@ -324,8 +324,11 @@ cross_entropy_row_kernel(bf16_t* __restrict__ logits, const int32_t* __restrict_
     return __builtin_amdgcn_make_buffer_rsrc(logits + r * V, 0, (int)(V * 2), 0x00020000);
   };
   typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  // non-temporal (cache policy 2): a depth's logits are several GB, read
+  // once and written once here
+  constexpr int NT = 2;
   auto load = [&](__amdgpu_buffer_rsrc_t rs, int j) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, j * CHUNK, 0));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, j * CHUNK, NT));
   };
   int64_t row = blockIdx.x;
   if (row >= rows) return;
@@ -413,7 +416,7 @@ cross_entropy_row_kernel(bf16_t* __restrict__ logits, const int32_t* __restrict_
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(cf * g[2 * i], cf * g[2 * i + 1]);
         __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{w[0], w[1], w[2], w[3]}, rs, voff,
-                                               j * CHUNK, 0);
+                                               j * CHUNK, NT);
       }
       // the next row's chunk j into the registers just freed (the last row
       // re-reads its own chunk, which is never used); the chunks are kept in

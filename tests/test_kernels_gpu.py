@@ -115,25 +115,34 @@ def test_gemm_store_splitk_long_k(M, N):
     assert (C1.cpu().double() - C.cpu().double()).abs().max().item() <= 8e-3 * scale
 
 
-def test_gemm_splitk_accumulates_large_k():
-    """dW-shaped product (both operands m/n-contiguous, K = 8192 rows) uses split-K."""
+@pytest.mark.parametrize("epi", [2, 3])
+@pytest.mark.parametrize("M,N,K", [(256, 384, 8192), (512, 512, 16384)])
+def test_gemm_splitk_accumulates_large_k(M, N, K, epi):
+    """dW-shaped products (both operands m/n-contiguous, long K) use split-K:
+    accumulated into a float32 C holding ones (ALODLM_EPI_ACCUM: split 0 adds
+    into C itself, the others' partials are added after), or written over a
+    C holding garbage (ALODLM_EPI_STORE_F32); the same bits on a second run."""
     L = lib()
-    M, N, K = 256, 384, 8192
-    log(f"gemm splitk M={M} N={N} K={K}")
+    log(f"gemm splitk M={M} N={N} K={K} epi={epi}")
     g = torch.Generator().manual_seed(5)
     dY = torch.randn(K, M, generator=g).to(torch.bfloat16)
     X = torch.randn(K, N, generator=g).to(torch.bfloat16)
-    C = torch.ones(M, N, dtype=torch.float32, device=DEV)
-    need = L.query("alodlm_gemm_workspace", M, N, K, 2, 1)
-    assert need > 0
+    need = L.query("alodlm_gemm_workspace", M, N, K, epi, 1)
+    assert need >= 2 * M * N, "the product should be split"
     ws = torch.empty(need, dtype=torch.float32, device=DEV)
     dYd, Xd = dY.to(DEV), X.to(DEV)  # named: the pointers must outlive the call
-    L.call("alodlm_gemm", L.ptr(dYd), M, 0, L.ptr(Xd), N, 0, L.ptr(C), N, None, 0,
-           M, N, K, 1.0, 2, 1, L.ptr(ws), st())
-    torch.cuda.synchronize()
-    ref = 1.0 + dY.double().T @ X.double()
-    err = (C.cpu().double() - ref).abs().max().item() / ref.abs().max().item()
+    outs = []
+    for _ in range(2):
+        C = torch.full((M, N), 1.0 if epi == 2 else float("nan"), dtype=torch.float32,
+                       device=DEV)
+        L.call("alodlm_gemm", L.ptr(dYd), M, 0, L.ptr(Xd), N, 0, L.ptr(C), N, None, 0,
+               M, N, K, 1.0, epi, 1, L.ptr(ws), st())
+        torch.cuda.synchronize()
+        outs.append(C.cpu())
+    ref = (1.0 if epi == 2 else 0.0) + dY.double().T @ X.double()
+    err = (outs[0].double() - ref).abs().max().item() / ref.abs().max().item()
     assert err < 1e-5
+    assert torch.equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
