@@ -653,6 +653,73 @@ def summarize_trace(directory, last_steps, out=sys.stdout):
         print(f"| `{name[:70]}` | {c / n:g} | {t / n / 1e6:.1f} | {t / c / 1e3:.1f} |", file=out)
 
 
+def summarize_counters(directories, out=sys.stdout, top=24):
+    """Summarise ``rocprofv3 --pmc`` runs of this benchmark (one directory per
+    counter pass): per kernel, its dispatches and each counter's mean per
+    dispatch, then the derived columns the counters present allow:
+
+    * MFMA util = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024): busy
+      cycles are summed over the 1024 SIMDs, GRBM_GUI_ACTIVE over the 8 XCDs;
+    * VALU / SALU / LDS instructions per MFMA instruction;
+    * HBM MiB per dispatch = FETCH_SIZE and WRITE_SIZE (KiB), each scaled by
+      what it reads for the 1 GiB device copy of ``--traffic-calibration``
+      (the first dispatch of a kernel named like a copy: the fill that
+      creates the copy's source comes before it and reads nothing)."""
+    import csv
+    import glob
+    per, names = {}, {}
+    for d in directories:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            disp = {}
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    key = (path, int(r["Dispatch_Id"]))
+                    name = r["Kernel_Name"].split("(")[0].strip().removeprefix("void ")
+                    disp.setdefault(key, [name, {}])
+                    c = disp[key][1]
+                    c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            scale = {}
+            copies = [c for _, (n, c) in sorted(disp.items()) if "copy" in n.lower()]
+            for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+                if copies and copies[0].get(counter, 0) > 0:
+                    scale[counter] = 1048576.0 / copies[0][counter]
+            for key, (name, c) in disp.items():
+                for counter, v in c.items():
+                    acc = per.setdefault(name, {}).setdefault(counter, [0.0, 0])
+                    acc[0] += v * scale.get(counter, 1.0)
+                    acc[1] += 1
+                names[name] = max(names.get(name, 0), sum(1 for k in disp if disp[k][0] == name))
+    mean = {n: {k: v[0] / v[1] for k, v in cs.items()} for n, cs in per.items()}
+    order = sorted(mean, key=lambda n: -(mean[n].get("SQ_BUSY_CYCLES", 0) * names[n] or
+                                         (mean[n].get("FETCH_SIZE", 0) + mean[n].get("WRITE_SIZE", 0))
+                                         * names[n]))
+    cols = []
+    have = lambda *ks: all(any(k in mean[n] for n in mean) for k in ks)
+    if have("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"):
+        cols.append(("MFMA util", lambda m: f"{100 * m['SQ_VALU_MFMA_BUSY_CYCLES'] / (m['GRBM_GUI_ACTIVE'] / 8 * 1024):.1f} %"))
+    for k, label in (("SQ_INSTS_VALU", "VALU/MFMA"), ("SQ_INSTS_SALU", "SALU/MFMA"),
+                     ("SQ_INSTS_LDS", "LDS/MFMA")):
+        if have(k, "SQ_INSTS_MFMA"):
+            cols.append((label, lambda m, k=k: f"{m[k] / m['SQ_INSTS_MFMA']:.2f}" if m["SQ_INSTS_MFMA"] else "-"))
+    if have("SQ_LDS_BANK_CONFLICT"):
+        cols.append(("LDS bank conflicts (M cycles/dispatch)", lambda m: f"{m['SQ_LDS_BANK_CONFLICT'] / 1e6:.2f}"))
+    if have("FETCH_SIZE"):
+        cols.append(("fetch MiB", lambda m: f"{m['FETCH_SIZE'] / 1024:.1f}"))
+    if have("WRITE_SIZE"):
+        cols.append(("write MiB", lambda m: f"{m['WRITE_SIZE'] / 1024:.1f}"))
+    print("| kernel | dispatches | " + " | ".join(c for c, _ in cols) + " |", file=out)
+    print("|---|---|" + "---|" * len(cols), file=out)
+    for n in order[:top]:
+        m = mean[n]
+        cells = []
+        for _, f in cols:
+            try:
+                cells.append(f(m))
+            except (KeyError, ZeroDivisionError):
+                cells.append("-")
+        print(f"| `{n[:70]}` | {names[n]} | " + " | ".join(cells) + " |", file=out)
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -675,9 +742,15 @@ def main():
     parser.add_argument("--summarize-trace", metavar="DIR",
                         help="print a summary of the rocprofv3 kernel trace under DIR (the "
                              "last --steps steps) and exit; needs no GPU")
+    parser.add_argument("--summarize-counters", metavar="DIR", nargs="+",
+                        help="print a per-kernel summary of rocprofv3 --pmc runs under the "
+                             "DIRs (one per counter pass) and exit; needs no GPU")
     args = parser.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.steps)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

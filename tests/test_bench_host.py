@@ -77,3 +77,39 @@ def test_trace_summary_counts_busy_and_idle_time(tmp_path):
     lines = [l for l in text.splitlines() if l.startswith("| 0 |") or l.startswith("| 1 |")]
     assert len(lines) == 2
     assert "| `gemm_dl_kernel<1>` | 2 |" in text and "| `adamw_kernel<float>` | 2 |" in text
+
+
+def test_counter_summary_derives_mfma_use_and_scaled_traffic(tmp_path):
+    """bench.py --summarize-counters: per-kernel means over dispatches, MFMA
+    utilisation from the busy cycles of 1024 SIMDs over GRBM_GUI_ACTIVE of 8
+    XCDs, instructions per MFMA, and FETCH_SIZE / WRITE_SIZE scaled by what
+    the 1 GiB calibration copy (the first copy dispatch; the fill that makes
+    its source comes first) reads, each counter from its own pass."""
+    import io
+    import bench
+    head = "Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value"
+    sq = tmp_path / "a"
+    sq.mkdir()
+    rows = [head]
+    for d in (1, 2):  # two dispatches of one kernel, per-XCD rows summed
+        rows += [f"{d},void gemm(x),SQ_VALU_MFMA_BUSY_CYCLES,512000",
+                 f"{d},void gemm(x),GRBM_GUI_ACTIVE,4000", f"{d},void gemm(x),GRBM_GUI_ACTIVE,4000",
+                 f"{d},void gemm(x),SQ_INSTS_MFMA,100", f"{d},void gemm(x),SQ_INSTS_VALU,150"]
+    (sq / "p_counter_collection.csv").write_text("\n".join(rows) + "\n")
+    passes = []
+    for counter, fill, copy, gemm in (("FETCH_SIZE", 0, 524288, 1024),
+                                      ("WRITE_SIZE", 1048576, 1048576, 2048)):
+        tr = tmp_path / counter
+        tr.mkdir()
+        rows = [head, f"1,void fill(z),{counter},{fill}", f"2,__amd_rocclr_copyBuffer,{counter},{copy}",
+                f"3,void gemm(x),{counter},{gemm}"]
+        (tr / "p_counter_collection.csv").write_text("\n".join(rows) + "\n")
+        passes.append(str(tr))
+    out = io.StringIO()
+    bench.summarize_counters([str(sq), *passes], out=out)
+    line = next(l for l in out.getvalue().splitlines() if l.startswith("| `gemm`"))
+    cells = [c.strip() for c in line.strip("|").split("|")]
+    # 512000 busy cycles / (8000 / 8 * 1024) = 50 %; 150 VALU / 100 MFMA;
+    # fetch 1024 KiB x 2 (the copy read 512 MiB of 1 GiB) = 2 MiB, write 2 MiB
+    assert cells[1] == "2" and cells[2] == "50.0 %" and cells[3] == "1.50"
+    assert cells[-2:] == ["2.0", "2.0"]
