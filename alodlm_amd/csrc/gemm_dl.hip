@@ -166,11 +166,15 @@ template <int NW> struct Opnd<false, NW> {
 
 // Epilogue of a 256x256 output tile.  `quad(t, row, col, v)` gives this
 // lane's t-th group of 4 outputs (t < 64): tile row, first of 4 consecutive
-// tile columns and the unscaled sums.  bf16 outputs (STORE / RESIDUAL) go
-// through LDS (`tile`: 128 KB, free once every wave has passed the loop), so
-// that global traffic is whole 512-byte tile rows: the tile is written as
-// bf16 into [256][256] (chunk' = chunk ^ (row & 31)), then each thread moves
+// tile columns and the unscaled sums (row and col are compile-time per t plus
+// a per-lane part).  bf16 outputs (STORE / RESIDUAL) go through LDS (`tile`:
+// TILE_LDS bytes, free once every wave has passed the loop), so that global
+// traffic is whole 512-byte tile rows: the tile is written as bf16 into 256
+// rows of TILE_ROW bytes (512 + 16 of padding, which keeps both the 8-byte
+// writes of 16 rows and the 16-byte reads along a row free of bank conflicts
+// with addresses that are a base plus an immediate), then each thread moves
 // 16-byte chunks, 32 threads per row (and reads the matching 16 bytes of R).
+constexpr int TILE_ROW = 528, TILE_LDS = TB * TILE_ROW;
 template <int EPI, int NTHR, typename Quad>
 __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, int64_t ldc,
                                               const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
@@ -205,9 +209,10 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
         int row, col;
         float v[4];
         quad(t, row, col, v);
-        const int chunk = col >> 3;
-        *reinterpret_cast<uint2*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4) + (col & 4) * 2) =
-            make_uint2(pack_bf16x2(alpha * v[0], alpha * v[1]), pack_bf16x2(alpha * v[2], alpha * v[3]));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= alpha;
+        *reinterpret_cast<uint2*>(tile + row * TILE_ROW + col * 2) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       const int chunk = threadIdx.x & 31;
@@ -216,7 +221,7 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
 #pragma unroll
         for (int it = 0; it < ITER; ++it) {
           const int row = it * (NTHR / 32) + (int)(threadIdx.x >> 5);
-          const uint4 w = *reinterpret_cast<const uint4*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4));
+          const uint4 w = *reinterpret_cast<const uint4*>(tile + row * TILE_ROW + chunk * 16);
           bf16_t* dst = Cb + (m0 + row) * ldc + n;
           if constexpr (EPI == ALODLM_EPI_RESIDUAL) {
             // reference order: x + round_bf16(proj), rounded once more
@@ -241,7 +246,7 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
         const int row = it * (NTHR / 32) + (int)(threadIdx.x >> 5);
         const int64_t m = m0 + row;
         if (m >= M || n >= N) continue;
-        uint4 w = *reinterpret_cast<const uint4*>(tile + row * 512 + ((chunk ^ (row & 31)) << 4));
+        uint4 w = *reinterpret_cast<const uint4*>(tile + row * TILE_ROW + chunk * 16);
         const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
         if (EPI == ALODLM_EPI_RESIDUAL) {
           float r[8], o[8];
@@ -335,9 +340,8 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
 // The kernel.  Each wave's 128x128 tile is 8 x 8 blocks of 16x16; the 64
 // MFMAs of a stage are issued block column by block column (j outer).  Per
 // tile tt (stage s):
-//  * MFMAs 1..23 (odd ones of block column 0, then two per column): the 8
-//    direct loads of tile tt+STAGES-1 into the stage of tile tt-1 (freed by
-//    the previous barrier);
+//  * MFMAs 1, 5, 9, 17, 21, .., 33: the 8 direct loads of tile tt+STAGES-1
+//    into the stage of tile tt-1 (freed by the previous barrier);
 //  * after MFMA 7: wait for tile tt+1's loads, barrier (publishes tile tt+1;
 //    every wave has finished reading tile tt);
 //  * MFMAs 8..63: the fragments of tile tt+1.  B fragment j is reloaded in
@@ -354,7 +358,9 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   constexpr int WAVES_N = TB / WN;
   constexpr int OPB = TB * KD * 2;
   static_assert(STAGES % 2 == 0 && STAGES >= 4, "fragment sets alternate with the stage parity");
-  __shared__ __attribute__((aligned(1024))) char lds[2][STAGES][OPB];
+  // the A stages, then the B stages; the output tile is staged over them
+  constexpr int LDS_BYTES = 2 * STAGES * OPB > TILE_LDS ? 2 * STAGES * OPB : TILE_LDS;
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
 
   const int tiles_m = (int)((M + TB - 1) / TB), tiles_n = (int)((N + TB - 1) / TB);
   const int T = tiles_m * tiles_n;
@@ -391,9 +397,9 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   constexpr int PA = Opnd<AK, NW>::PER, PB = Opnd<BK, NW>::PER, PL = PA + PB;
   static_assert(PL <= 8, "load_slot places 8 direct loads per stage");
   // at the barrier of tile tt (after MFMA 7), tiles tt+2 .. tt+STAGES-2 and
-  // the first loads of tile tt+STAGES-1 (issued after MFMAs 1, 3, 5, 7) may be
+  // the first loads of tile tt+STAGES-1 (issued after MFMAs 1 and 5) may be
   // in flight
-  constexpr int VM_LOOP = (STAGES - 3) * PL + (PL < 4 ? PL : 4);
+  constexpr int VM_LOOP = (STAGES - 3) * PL + (PL < 2 ? PL : 2);
   constexpr int VM_PRO = (STAGES - 2) * PL;
 
   const char* pa = oa.origin(A, m0, kbeg);
@@ -411,14 +417,18 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
     if (d < PA) dma16_m0(pa, oa.off[d], mw + (uint32_t)(sl * OPB + NW * d * 1024));
     else dma16_m0(pb, ob.off[d - PA], mw + (uint32_t)((STAGES + sl) * OPB + NW * (d - PA) * 1024));
   };
-  const char* lds0 = lds[0][0];
+  const char* lds0 = lds;
 
   // with one wave per SIMD a 16x16x32 MFMA leaves room for about three other
-  // instructions, so the memory instructions are spread one group per MFMA
+  // instructions, so the memory instructions are spread one group per MFMA.
+  // The direct loads go out every 4 MFMAs from MFMA 1 (13, where the last B
+  // fragment is read, skipped): their cost is not latency (never waiting for
+  // them takes as long) but the vector-memory path and the LDS writes they
+  // share with the fragment reads, and bunched into MFMAs 1..23 they ran 1-3 %
+  // slower.
   auto load_slot = [](int q) {  // direct load issued after MFMA q, or -1
-    const int r = q & 7, b = q >> 3;
-    if (b == 0 && (r & 1)) return r >> 1;                            // q 1, 3, 5, 7
-    if ((b == 1 || b == 2) && (r == 3 || r == 7)) return 4 + 2 * (b - 1) + (r == 7);  // q 11 .. 23
+    if (q == 1 || q == 5) return q >> 2;                  // before the barrier
+    if (q >= 9 && q <= 33 && (q & 3) == 1 && q != 13) return q < 13 ? 2 : (q - 9) / 4 + 1;
     return -1;
   };
   auto tile_body = [&](const int s) {
@@ -484,7 +494,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
   };
-  tile_epilogue<EPI, NW * 64>(lds[0][0], quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
+  tile_epilogue<EPI, NW * 64>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
                               first_into_c);
 }
 
