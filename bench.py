@@ -664,7 +664,8 @@ def summarize_counters(directories, out=sys.stdout, top=24):
     * HBM MiB per dispatch = FETCH_SIZE and WRITE_SIZE (KiB), each scaled by
       what it reads for the 1 GiB device copy of ``--traffic-calibration``
       (the first dispatch of a kernel named like a copy: the fill that
-      creates the copy's source comes before it and reads nothing)."""
+      creates the copy's source comes before it and reads nothing), and the
+      GEMMs' bytes per launch (`traffic_bytes_per_launch`)."""
     import csv
     import glob
     per, names = {}, {}
@@ -707,6 +708,18 @@ def summarize_counters(directories, out=sys.stdout, top=24):
         cols.append(("fetch MiB", lambda m: f"{m['FETCH_SIZE'] / 1024:.1f}"))
     if have("WRITE_SIZE"):
         cols.append(("write MiB", lambda m: f"{m['WRITE_SIZE'] / 1024:.1f}"))
+    if have("FETCH_SIZE", "WRITE_SIZE"):
+        # HBM bytes per GEMM launch, the reductions of split-K partials included
+        # (the figure the bench line's roofline reports as `traffic`)
+        gemm = [n for n in mean if n.startswith("gemm_")]
+        red = [n for n in mean if n.startswith("splitk_")]
+        calls = sum(names[n] for n in gemm)
+        total = sum((mean[n].get("FETCH_SIZE", 0) + mean[n].get("WRITE_SIZE", 0)) * names[n]
+                    for n in gemm + red) * 1024
+        if calls:
+            print(f"traffic_bytes_per_launch: {int(total / calls)}\n", file=out)
+            print(f"GEMM calls: {calls}; HBM bytes per call (fetch + write, split-K "
+                  f"reduction included): {total / calls / 1048576:.1f} MiB.\n", file=out)
     print("| kernel | dispatches | " + " | ".join(c for c, _ in cols) + " |", file=out)
     print("|---|---|" + "---|" * len(cols), file=out)
     for n in order[:top]:

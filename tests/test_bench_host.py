@@ -92,9 +92,9 @@ def test_counter_summary_derives_mfma_use_and_scaled_traffic(tmp_path):
     sq.mkdir()
     rows = [head]
     for d in (1, 2):  # two dispatches of one kernel, per-XCD rows summed
-        rows += [f"{d},void gemm(x),SQ_VALU_MFMA_BUSY_CYCLES,512000",
-                 f"{d},void gemm(x),GRBM_GUI_ACTIVE,4000", f"{d},void gemm(x),GRBM_GUI_ACTIVE,4000",
-                 f"{d},void gemm(x),SQ_INSTS_MFMA,100", f"{d},void gemm(x),SQ_INSTS_VALU,150"]
+        rows += [f"{d},void gemm_dl(x),SQ_VALU_MFMA_BUSY_CYCLES,512000",
+                 f"{d},void gemm_dl(x),GRBM_GUI_ACTIVE,4000", f"{d},void gemm_dl(x),GRBM_GUI_ACTIVE,4000",
+                 f"{d},void gemm_dl(x),SQ_INSTS_MFMA,100", f"{d},void gemm_dl(x),SQ_INSTS_VALU,150"]
     (sq / "p_counter_collection.csv").write_text("\n".join(rows) + "\n")
     passes = []
     for counter, fill, copy, gemm in (("FETCH_SIZE", 0, 524288, 1024),
@@ -102,14 +102,16 @@ def test_counter_summary_derives_mfma_use_and_scaled_traffic(tmp_path):
         tr = tmp_path / counter
         tr.mkdir()
         rows = [head, f"1,void fill(z),{counter},{fill}", f"2,__amd_rocclr_copyBuffer,{counter},{copy}",
-                f"3,void gemm(x),{counter},{gemm}"]
+                f"3,void gemm_dl(x),{counter},{gemm}"]
         (tr / "p_counter_collection.csv").write_text("\n".join(rows) + "\n")
         passes.append(str(tr))
     out = io.StringIO()
     bench.summarize_counters([str(sq), *passes], out=out)
-    line = next(l for l in out.getvalue().splitlines() if l.startswith("| `gemm`"))
+    line = next(l for l in out.getvalue().splitlines() if l.startswith("| `gemm_dl`"))
     cells = [c.strip() for c in line.strip("|").split("|")]
     # 512000 busy cycles / (8000 / 8 * 1024) = 50 %; 150 VALU / 100 MFMA;
     # fetch 1024 KiB x 2 (the copy read 512 MiB of 1 GiB) = 2 MiB, write 2 MiB
     assert cells[1] == "2" and cells[2] == "50.0 %" and cells[3] == "1.50"
     assert cells[-2:] == ["2.0", "2.0"]
+    # one GEMM launch of 2 + 2 MiB
+    assert "traffic_bytes_per_launch: 4194304" in out.getvalue()
