@@ -11,7 +11,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libalodlm_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -86,7 +86,7 @@ SIGNATURES = {
     "alodlm_scale": [P, P, I64, I32, P],
     "alodlm_scale_add_f32": [P, P, I64, P, I32, P],
     "alodlm_transpose": [P, P, I64, I64, I32, P],
-    "alodlm_transpose_checked": [P, P, I64, I64, I32, P, P],
+    "alodlm_check_finite": [P, I64, I32, P, P],
 }
 _RESTYPE = {
     "alodlm_last_error": ctypes.c_char_p,

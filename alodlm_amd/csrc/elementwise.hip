@@ -82,22 +82,16 @@ __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restric
 // distinct banks).  One workgroup of 256 threads per tile.
 template <typename T>
 __global__ void __launch_bounds__(256)
-transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols,
-                 int32_t* __restrict__ nonfinite) {
+transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols) {
   __shared__ T tile[64][65];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  bool bad = false;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int rr = ty + 4 * i;
     const int64_t r = r0 + rr, c = c0 + tx;
-    if (r < rows && c < cols) {
-      tile[rr][tx] = src[r * cols + c];
-      bad |= !isfinite(Elem<T>::load(src, r * cols + c));
-    }
+    if (r < rows && c < cols) tile[rr][tx] = src[r * cols + c];
   }
-  if (nonfinite != nullptr && bad) *nonfinite = 1;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -112,27 +106,17 @@ transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, i
 // per tile row on the way in, 8 per transposed row on the way out).
 __global__ void __launch_bounds__(256)
 transpose16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t rows,
-                   int64_t cols, int32_t* __restrict__ nonfinite) {
+                   int64_t cols) {
   __shared__ uint16_t tile[64][64 + 8];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int t = threadIdx.x, part = (t & 7) * 8;
-  uint32_t bad = 0;
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     const int rr = (t >> 3) + 32 * pass;
     const int64_t r = r0 + rr, c = c0 + part;
-    if (r < rows && c < cols) {
-      const uint4 v = *reinterpret_cast<const uint4*>(src + r * cols + c);
-      *reinterpret_cast<uint4*>(&tile[rr][part]) = v;
-      // a bf16 element is inf or NaN when its exponent bits are all ones:
-      // 0x7f80 in either half of a 32-bit word
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        bad |= ((w[e] & 0x7f80u) == 0x7f80u) | ((w[e] & 0x7f800000u) == 0x7f800000u);
-    }
+    if (r < rows && c < cols)
+      *reinterpret_cast<uint4*>(&tile[rr][part]) = *reinterpret_cast<const uint4*>(src + r * cols + c);
   }
-  if (nonfinite != nullptr && bad) *nonfinite = 1;
   __syncthreads();
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
@@ -267,11 +251,6 @@ extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, vo
 
 extern "C" int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
                                 void* stream) {
-  return alodlm_transpose_checked(src, dst, rows, cols, dtype, nullptr, stream);
-}
-
-extern "C" int alodlm_transpose_checked(const void* src, void* dst, int64_t rows, int64_t cols,
-                                        int dtype, int32_t* nonfinite, void* stream) {
   ALODLM_CHECK_ARG(rows >= 0 && cols >= 0, "transpose: negative shape");
   ALODLM_CHECK_ARG(rows <= 64 * 65535LL, "transpose: too many rows");
   if (rows == 0 || cols == 0) return ALODLM_OK;
@@ -280,15 +259,51 @@ extern "C" int alodlm_transpose_checked(const void* src, void* dst, int64_t rows
   if (dtype == ALODLM_BF16 && rows % 8 == 0 && cols % 8 == 0 &&
       ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
     transpose16_kernel<<<grid, 256, 0, as_stream(stream)>>>((const uint16_t*)src, (uint16_t*)dst,
-                                                            rows, cols, nonfinite);
+                                                            rows, cols);
     ALODLM_CHECK_LAUNCH("transpose");
     return ALODLM_OK;
   }
   ALODLM_DISPATCH(dtype, T, {
-    transpose_kernel<T><<<grid, 256, 0, as_stream(stream)>>>((const T*)src, (T*)dst, rows, cols,
-                                                             nonfinite);
+    transpose_kernel<T><<<grid, 256, 0, as_stream(stream)>>>((const T*)src, (T*)dst, rows, cols);
   });
   ALODLM_CHECK_LAUNCH("transpose");
+  return ALODLM_OK;
+}
+
+// *flag = 1 when any of the n elements is inf or NaN (read once, 16 bytes per
+// thread and step of a grid-stride sweep; the flag is only ever set, by a
+// vector store of the same value).
+template <typename T>
+__global__ void __launch_bounds__(256)
+check_finite_kernel(const T* __restrict__ x, int64_t n, int32_t* __restrict__ flag) {
+  constexpr int PER = 16 / sizeof(T);
+  const int64_t stride = (int64_t)gridDim.x * 256 * PER;
+  bool bad = false;
+  int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * PER;
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    for (; i + PER <= n; i += stride) {
+      const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(x + i));
+      T e[PER];
+      __builtin_memcpy(e, &v, 16);
+#pragma unroll
+      for (int k = 0; k < PER; ++k) bad |= !isfinite(Elem<T>::load(e, k));
+    }
+  }
+  for (; i < n; i += stride)  // the tail (or an unaligned array) element by element
+    for (int k = 0; k < PER && i + k < n; ++k) bad |= !isfinite(Elem<T>::load(x, i + k));
+  if (bad) *flag = 1;
+}
+
+extern "C" int alodlm_check_finite(const void* x, int64_t n, int dtype, int32_t* flag,
+                                   void* stream) {
+  ALODLM_CHECK_ARG(n >= 0, "check_finite: negative size");
+  ALODLM_CHECK_ARG(flag != nullptr, "check_finite: no flag");
+  if (n == 0) return ALODLM_OK;
+  const unsigned blocks = (unsigned)std::min<int64_t>(4 * (int64_t)device_cus(), ceil_div_u(n, 256 * 8));
+  ALODLM_DISPATCH(dtype, T, {
+    check_finite_kernel<T><<<blocks, 256, 0, as_stream(stream)>>>((const T*)x, n, flag);
+  });
+  ALODLM_CHECK_LAUNCH("check_finite");
   return ALODLM_OK;
 }
 

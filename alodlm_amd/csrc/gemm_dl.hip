@@ -162,6 +162,86 @@ template <int NW> struct Opnd<false, NW> {
   }
 };
 
+
+// 64-deep stages (the two-stage ring of gemm_dl2_kernel).
+template <bool KMAJ, int NW> struct Opnd64;
+
+// P[rows][ld], k contiguous: a stage is 32 blocks of 1 KB, block b holding
+// rows 8 b .. 8 b + 7 as [8 rows x k 0..31][8 rows x k 32..63] (64-byte rows,
+// chunk' = chunk ^ f(row), f(row) = (row / 2) % 4): one direct-load
+// instruction fills one block from 8 whole 128-byte row pieces, and the
+// fragment reads keep 64-byte rows (measured free of bank conflicts).
+template <int NW> struct Opnd64<true, NW> {
+  static constexpr int NINST = TB / 8, PER = NINST / NW, OPB = TB * 64 * 2;
+  uint32_t off[PER];
+  uint32_t fo;
+  int64_t ld, step;
+  static __device__ __forceinline__ int f(int row) { return (row >> 1) & 3; }
+  __device__ __forceinline__ void init(int64_t ld_, int64_t rows_left, int wave, int lane) {
+    ld = ld_;
+    step = 2 * 64;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int r = 8 * (wave + NW * i) + ((lane & 31) >> 2), h = lane >> 5;
+      const int c = (lane & 3) ^ f(r);
+      const int64_t rc = r < rows_left ? r : rows_left - 1;
+      off[i] = (uint32_t)((rc * ld + 32 * h + 8 * c) * 2);
+    }
+  }
+  // fragments of rows r0 + 16 idx + lane % 16, k step ks, chunk lane / 16
+  __device__ __forceinline__ void init_frag(int r0, int lane, int region) {
+    const int row = r0 + (lane & 15);
+    fo = (uint32_t)(region + (row >> 3) * 1024 + (row & 7) * 64 + (((lane >> 4) ^ f(row)) << 4));
+  }
+  __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
+    return reinterpret_cast<const char*>(P + r0 * ld + k0);
+  }
+  __device__ __forceinline__ bf16x8_t frag(const char* lds, int stage, int ks, int idx) const {
+    return *reinterpret_cast<const bf16x8_t*>(lds + fo + (stage * OPB + idx * 2048 + ks * 512));
+  }
+};
+
+// P[k][ld], m/n contiguous: [64 k][256], 512-byte rows, chunk ^ swz(k) as in
+// the 32-deep layout (k step ks reads k rows 32 ks + ..).
+template <int NW> struct Opnd64<false, NW> {
+  static constexpr int NINST = 64 / 2, PER = NINST / NW, OPB = TB * 64 * 2;
+  uint32_t off[PER];
+  uint32_t fo[4][2];
+  int64_t ld, step;
+  static __device__ __forceinline__ int swz(int k) { return 4 * (k & 3) ^ 2 * ((k >> 3) & 1); }
+  __device__ __forceinline__ void init(int64_t ld_, int64_t cols_left, int wave, int lane) {
+    ld = ld_;
+    step = 2 * 64 * ld;
+    const int last_chunk = (int)((cols_left < TB ? cols_left : TB) / 8) - 1;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int j = wave + NW * i;
+      const int row = 2 * j + (lane >> 5);
+      int c = (lane & 31) ^ swz(row);
+      c = c < last_chunk ? c : last_chunk;
+      off[i] = (uint32_t)((row * ld + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ void init_frag(int r0, int lane, int region) {
+    const int s = lane & 15, g = lane >> 4, m = s >> 2, b = (s & 3) >> 1;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        fo[a][c] = (uint32_t)(region + (8 * g + m) * 512 +
+                              ((r0 >> 3) + 4 * (a ^ m) + 2 * (c ^ (g & 1)) + b) * 16 + (s & 1) * 8);
+  }
+  __device__ __forceinline__ const char* origin(const bf16_t* P, int64_t r0, int64_t k0) const {
+    return reinterpret_cast<const char*>(P + k0 * ld + r0);
+  }
+  __device__ __forceinline__ bf16x8_t frag(const char* lds, int stage, int ks, int idx) const {
+    const char* p0 = lds + fo[idx >> 1][idx & 1] + stage * OPB + ks * 32 * 512;
+    const v4s_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4s_t*)p0);
+    const v4s_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS v4s_t*)(p0 + 4 * 512));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
 }  // namespace
 
 // Epilogue of a 256x256 output tile.  `quad(t, row, col, v)` gives this
@@ -498,6 +578,153 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
                               first_into_c);
 }
 
+// Two 64-deep stages (128 KB): one barrier per 128 MFMAs and 128-byte row
+// pieces per direct load.  Per tile tt (stage s = tt % 2), k step 0 reads k
+// step 1's fragments; after MFMA 7 of k step 1 the barrier publishes tile tt+1
+// (all loads in flight are its) and frees stage s; the rest of k step 1 reads
+// tile tt+1's k step 0 fragments and issues tile tt+2's loads into stage s.
+template <bool AK, bool BK, int EPI>
+__global__ void __launch_bounds__(256, 1)
+gemm_dl2_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
+                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
+                int64_t N, int64_t K, float alpha, int64_t k_per_split, float* __restrict__ partial,
+                int first_into_c) {
+  constexpr int NW = 4, WM = 128, WN = 128, STAGES = 2, KD2 = 64;
+  constexpr int FI = WM / 16, FJ = WN / 16;
+  constexpr int WAVES_N = TB / WN;
+  constexpr int OPB = TB * KD2 * 2;
+  constexpr int LDS_BYTES = 2 * STAGES * OPB > TILE_LDS ? 2 * STAGES * OPB : TILE_LDS;
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+
+  const int tiles_m = (int)((M + TB - 1) / TB), tiles_n = (int)((N + TB - 1) / TB);
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if (T % 8 == 0) t = (t % 8) * (T / 8) + t / 8;
+  const int group = 3, per_group = group * tiles_n;
+  const int g = t / per_group, first_m = g * group;
+  const int gsize = (tiles_m - first_m) < group ? (tiles_m - first_m) : group;
+  const int tm = first_m + (t % per_group) % gsize, tn = (t % per_group) / gsize;
+  const int64_t m0 = __builtin_amdgcn_readfirstlane(tm * TB);
+  const int64_t n0 = __builtin_amdgcn_readfirstlane(tn * TB);
+  const int64_t kbeg = (int64_t)blockIdx.y * k_per_split;
+  const int64_t kend = (kbeg + k_per_split) < K ? (kbeg + k_per_split) : K;
+  const int ntiles = (int)((kend - kbeg + KD2 - 1) / KD2);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  Opnd64<AK, NW> oa;
+  Opnd64<BK, NW> ob;
+  oa.init(lda, M - m0, wave, lane);
+  ob.init(ldb, N - n0, wave, lane);
+  oa.init_frag(wm * WM, lane, 0);
+  ob.init_frag(wn * WN, lane, STAGES * OPB);
+
+  f32x4_t acc[FI][FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8_t fa[2][FI], fb[FJ - 1], fbl[2];
+  constexpr int PA = Opnd64<AK, NW>::PER, PB = Opnd64<BK, NW>::PER, PL = PA + PB;
+  static_assert(PL == 16, "load_slot places 16 direct loads per stage");
+
+  const char* pa = oa.origin(A, m0, kbeg);
+  const char* pb = ob.origin(B, n0, kbeg);
+  int tl = 0;
+  auto advance = [&]() {
+    if (tl + 1 < ntiles) {
+      pa += oa.step;
+      pb += ob.step;
+    }
+    ++tl;
+  };
+  const uint32_t mw = lds_addr(lds) + (uint32_t)wave * 1024u;
+  auto dma_one = [&](int sl, int d) {
+    if (d < PA) dma16_m0(pa, oa.off[d], mw + (uint32_t)(sl * OPB + NW * d * 1024));
+    else dma16_m0(pb, ob.off[d - PA], mw + (uint32_t)((STAGES + sl) * OPB + NW * (d - PA) * 1024));
+  };
+  const char* lds0 = lds;
+
+  // direct loads after MFMA q of k step 1 (after the barrier), away from the
+  // fragment-read slots (q % 8 == 0 or 2, 13, 60)
+  auto load_slot = [](int q) {
+    constexpr int slots[16] = {9, 11, 14, 17, 19, 22, 25, 27, 30, 33, 35, 38, 41, 43, 46, 49};
+    for (int d = 0; d < 16; ++d)
+      if (slots[d] == q) return d;
+    return -1;
+  };
+  // one k step: 64 MFMAs on fragment set `cur`; the fragments of the next k
+  // step (stage sr, k step kr) go to set `cur ^ 1`
+  auto kstep = [&](const int cur, const int sr, const int kr, const bool last, const int s) {
+    const int nxt = cur ^ 1;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) {
+      const int i = q & 7, j = q >> 3, r = q & 7;
+      if (j == FJ - 1)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fbl[cur], fa[cur][i], acc[i][j], 0, 0, 0);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[cur][i], acc[i][j], 0, 0, 0);
+      if (last) {
+        if (q == 7) {
+          __builtin_amdgcn_sched_barrier(0);
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        const int d = load_slot(q);
+        if (d >= 0) dma_one(s, d);
+      }
+      if (j >= 1) {
+        if (r == 0) fb[j - 1] = ob.frag(lds0, sr, kr, j - 1);
+        if (r == 2 && j - 1 < FI - 1) fa[nxt][j - 1] = oa.frag(lds0, sr, kr, j - 1);
+        if (q == 13) fbl[nxt] = ob.frag(lds0, sr, kr, FJ - 1);
+        if (q == 60) fa[nxt][FI - 1] = oa.frag(lds0, sr, kr, FI - 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto tile_body = [&](const int s) {
+    kstep(0, s, 1, false, s);          // reads k step 1 of this tile
+    kstep(1, s ^ 1, 0, true, s);       // barrier, reads k step 0 of tile tt+1, loads tile tt+2
+    advance();
+  };
+
+  if (ntiles > 0) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+#pragma unroll
+      for (int d = 0; d < PL; ++d) dma_one(s, d);
+      advance();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(PL) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < FI; ++i) fa[0][i] = oa.frag(lds0, 0, 0, i);
+#pragma unroll
+    for (int j = 0; j < FJ - 1; ++j) fb[j] = ob.frag(lds0, 0, 0, j);
+    fbl[0] = ob.frag(lds0, 0, 0, FJ - 1);
+    for (int tt = 0; tt < ntiles;) {
+#pragma unroll
+      for (int s = 0; s < STAGES; ++s) {
+        if (tt < ntiles) tile_body(s);
+        ++tt;
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  auto quad = [&](int t, int& row, int& col, float* v) {
+    const int i = t >> 3, j = t & 7;
+    row = wm * WM + i * 16 + (lane & 15);
+    col = wn * WN + j * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
+  };
+  tile_epilogue<EPI, NW * 64>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
+                              first_into_c);
+}
+
 // The direct-load kernel needs whole 32-deep k stages, 16-byte-aligned rows and,
 // for m/n-contiguous operands, dimensions in whole 16-byte chunks.
 bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int64_t M, int64_t N,
@@ -550,6 +777,28 @@ static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t
                           int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
                           int64_t nsplit, int first_into_c, hipStream_t st) {
+  // both operands k-contiguous: two 64-deep stages (128-byte row pieces per
+  // direct load; 3-7 % faster than the 32-deep ring on every such product of
+  // the step, and the same results: the k order of every sum is unchanged)
+  if constexpr (AK && BK) {
+    if (K % 64 == 0 && kps % 64 == 0) {
+      const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
+      dim3 grid((unsigned)tiles, (unsigned)nsplit);
+      if (epi == ALODLM_EPI_STORE)
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      else if (epi == ALODLM_EPI_RESIDUAL)
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_RESIDUAL><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      else if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE_F32><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      else
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_ACCUM><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      return;
+    }
+  }
   // 4 waves, 32-deep k stages in a ring of 4 (128 KB of LDS)
   constexpr int ST = 4;
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);

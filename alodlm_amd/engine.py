@@ -157,46 +157,72 @@ def _layer_views(arena, buf, index, grads=False):
     return LayerGrads(*views) if grads else LayerWeights(*views)
 
 
-class _TransposedWeights:
-    """Out-contiguous copies ([in, out]) of every forward product's weight.
+# Forward row count above which the QKV and gate/up products read
+# out-contiguous weight copies: at 32768 rows (the 1.7B pack) the copies' products
+# measured 2-4 % faster in the step than the [out, in] weights through the
+# two-stage 64-deep kernel; at 4096 rows (the 8B pack) the products ran alike
+# and refreshing those copies (read and write the weights each step) cost
+# 3.6 ms of the 600 ms step.
+ROWS_FOR_COPIES = 8192
 
-    The forward products C = X . W^T then read W^T with out-contiguous rows,
-    the operand layout the GEMM kernel streams fastest (whole 512-byte rows per
-    direct load instead of 64-byte pieces of k-contiguous rows).  The copies
-    are refreshed from the arena at the start of every forward, so they always
-    match the parameters; the backward keeps using the arena itself."""
+
+class _TransposedWeights:
+    """Out-contiguous copies ([in, out]) of projection weights, and the
+    LM-head weight's finiteness flag.
+
+    A forward product C = X . W^T through a copy reads W^T with out-contiguous
+    rows (whole 512-byte rows per direct load).  The output and down
+    projections always use their copies (2-7 % faster in the step); the QKV
+    and gate/up projections use theirs in forwards of more than
+    ROWS_FOR_COPIES rows (allocated at the first such forward) and read the
+    arena weights otherwise; the LM head always reads its arena weight (3-6 %
+    faster).  The copies in use are refreshed from the arena at the start of
+    every forward, so they always match the parameters, and a copy not
+    refreshed is unhooked from its layer; the backward uses the arena itself."""
 
     def __init__(self, engine):
-        pairs = []   # (source [rows, cols], attribute owner, name)
-        for layer in engine.layers:
-            pairs += [(layer.wqkv, layer, "wqkv_t"), (layer.wo, layer, "wo_t"),
-                      (layer.wgu, layer, "wgu_t"), (layer.wd, layer, "wd_t")]
-        pairs.append((engine.lm_head, engine, "lm_head_t"))
-        total, spans = 0, []
-        for src, _, _ in pairs:
-            spans.append(total)
-            total += (src.numel() + _ALIGN - 1) // _ALIGN * _ALIGN
-        self.buf = torch.empty(total, dtype=engine.dtype, device=engine.device)
-        self.jobs = []
-        for (src, owner, name), off in zip(pairs, spans):
-            rows, cols = src.shape
-            dst = self.buf[off:off + src.numel()].view(cols, rows)
-            setattr(owner, name, dst)
-            self.jobs.append((src, dst, rows, cols))
+        self.device, self.dtype = engine.device, engine.dtype
+        self.jobs = self._allocate([(layer.wo, layer, "wo_t") for layer in engine.layers] +
+                                   [(layer.wd, layer, "wd_t") for layer in engine.layers])
+        self.optional = ([(layer.wqkv, layer, "wqkv_t") for layer in engine.layers] +
+                         [(layer.wgu, layer, "wgu_t") for layer in engine.layers])
+        self.optional_jobs = None
+        self.lm_head = engine.lm_head
         # set by the refresh when an LM-head weight is inf or NaN: every row's
         # logits then hold a non-finite column, which makes the reference's
         # loss NaN through its 0 * sum(logits) term (alodlm/model.py:186)
         self.nonfinite = torch.zeros(1, dtype=torch.int32, device=engine.device)
 
-    def refresh(self, code, stream):
+    def _allocate(self, pairs):
+        """One buffer for the copies of `pairs` (source [rows, cols], owner,
+        attribute); each copy is hooked to its owner."""
+        total, spans = 0, []
+        for src, _, _ in pairs:
+            spans.append(total)
+            total += (src.numel() + _ALIGN - 1) // _ALIGN * _ALIGN
+        buf = torch.empty(total, dtype=self.dtype, device=self.device)
+        jobs = []
+        for (src, owner, name), off in zip(pairs, spans):
+            rows, cols = src.shape
+            dst = buf[off:off + src.numel()].view(cols, rows)
+            setattr(owner, name, dst)
+            jobs.append((src, dst, rows, cols, owner, name))
+        return jobs
+
+    def refresh(self, code, stream, rows=0):
+        """Refresh the copies a forward of `rows` rows reads (rows = 0: the
+        decoder's windows, which read the QKV and gate/up arena weights)."""
         self.nonfinite.zero_()
-        last = len(self.jobs) - 1
-        for i, (src, dst, rows, cols) in enumerate(self.jobs):
-            if i == last:   # the LM head
-                call("alodlm_transpose_checked", ptr(src), ptr(dst), rows, cols, code,
-                     ptr(self.nonfinite), stream)
-            else:
-                call("alodlm_transpose", ptr(src), ptr(dst), rows, cols, code, stream)
+        call("alodlm_check_finite", ptr(self.lm_head), self.lm_head.numel(), code,
+             ptr(self.nonfinite), stream)
+        use = rows > ROWS_FOR_COPIES
+        if use and self.optional_jobs is None:
+            self.optional_jobs = self._allocate(self.optional)
+        jobs = self.jobs + (self.optional_jobs if use else [])
+        for src, dst, r, c, _, _ in jobs:
+            call("alodlm_transpose", ptr(src), ptr(dst), r, c, code, stream)
+        for src, dst, r, c, owner, name in self.optional_jobs or []:
+            setattr(owner, name, dst if use else None)
 
 
 class StepEngine(Kernels):
@@ -420,7 +446,7 @@ class StepEngine(Kernels):
             xsel[R:].zero_()
         call("alodlm_gather_rows", ptr(readout), ptr(sel_rows), R, ptr(xsel), H, c, st)
         logits = logits_buf[:Rp]
-        self._gemm(xsel, H, 1, self.lm_head_t, V, 0, logits, V, Rp, V, H)
+        self._gemm(xsel, H, 1, self.lm_head, H, 1, logits, V, Rp, V, H)
         ce = torch.empty(2, R, dtype=torch.float32, device=self.device)
         call("alodlm_cross_entropy", ptr(logits), ptr(sel_target), ptr(sel_coef),
              ptr(sel_count), R, V, ptr(ce[0]), ptr(ce[1]), c, st)
@@ -510,7 +536,6 @@ class StepEngine(Kernels):
         cfg, d = self.cfg, self.dims
         K = cfg.max_depth
         st, c = self._stream(), self.code
-        self.transposed.refresh(c, st)
         # host inputs (a pack from the data loader): the labels are read on the
         # host and the copies to the device do not block
         labels_host = labels.numpy() if labels.device.type == "cpu" else None
@@ -521,6 +546,7 @@ class StepEngine(Kernels):
                         generator=generator, draws=draws, labels_host=labels_host)
         self._rope = Rope(positions=b.positions, inv_freq=self.inv_freq)
         N, H, V = b.ids.numel(), d.hidden, d.vocab
+        self.transposed.refresh(c, st, N)
         S = b.boundaries.numel() - 1
         saves = [] if need_grad else None
         # the readout's persistent buffers and this step's LM-head gradient
@@ -636,7 +662,7 @@ class StepEngine(Kernels):
         K, N = cfg.max_depth, x0.shape[0]
         if x0.shape != (batch.ids.numel(), d.hidden) or x0.dtype != self.dtype:
             raise ValueError("x0 must be [rows, hidden] in the parameter dtype")
-        self.transposed.refresh(self.code, self._stream())
+        self.transposed.refresh(self.code, self._stream(), N)
         b = batch
         self._rope = Rope(positions=b.positions, inv_freq=self.inv_freq)
         self._keep_now = (False, False)
@@ -709,7 +735,7 @@ class StepEngine(Kernels):
                                    for f in finals):
             raise ValueError("finals must be max_depth tensors [rows, hidden] in the parameter dtype")
         st = self._stream()
-        self.transposed.refresh(self.code, st)
+        self.transposed.refresh(self.code, st, N)
         b = batch
         g_lm = self._empty(d.vocab, d.hidden, dtype=torch.float32) if need_grad else None
         S = b.boundaries.numel() - 1

@@ -381,7 +381,7 @@ class Decoder:
                 call("alodlm_gather_rows", ptr(features), ptr(state["mask_row"]), count,
                      ptr(picked), H, code, st)
                 logits = e._empty(count, V)
-                e._gemm(picked, H, 1, e.lm_head_t, V, 0, logits, V, count, V, H)
+                e._gemm(picked, H, 1, e.lm_head, H, 1, logits, V, count, V, H)
                 call("alodlm_decode_readout", ptr(logits), count, V, ptr(state["predicted"]),
                      ptr(state["entropy"]), code, st)
                 call("alodlm_decode_commit", state.ref, ptr(gate), count, depth, int(finish), st)

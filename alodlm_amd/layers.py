@@ -227,8 +227,9 @@ class Rope:
 class LayerWeights:
     """One layer's weights as the kernels take them: q|k|v stacked [W, H],
     gate|up stacked [2I, H], o [H, nq*dh], down [H, I], the four norm weights,
-    and optional out-contiguous copies (``*_t``, [in, out]) that the forward
-    products read fastest.  ``from_layer`` takes an HF Qwen3 decoder layer:
+    and optional out-contiguous copies (``*_t``, [in, out]) that a forward
+    product reads instead of its [out, in] weight when given (the step gives
+    them for all four: the products run faster that way).  ``from_layer`` takes an HF Qwen3 decoder layer:
     adjacent projection weights (the step's parameter arena) are used in
     place, separate ones are stacked into a copy."""
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define ALODLM_ABI_VERSION 6
+#define ALODLM_ABI_VERSION 7
 
 enum { ALODLM_OK = 0, ALODLM_EINVAL = 1, ALODLM_EHIP = 2, ALODLM_EUNSUPPORTED = 3 };
 enum { ALODLM_F32 = 0, ALODLM_BF16 = 1 };
@@ -424,7 +424,7 @@ int alodlm_scatter_ce(const float* ce, const int32_t* sel_rows, const int32_t* n
  * total is NaN when a gate is non-finite or when `nonfinite` (nullable) holds
  * a nonzero value: the reference adds 0 * sum(logits + gates) to the loss
  * (model.py:186), and the step sets that flag when an LM-head weight is
- * non-finite (alodlm_transpose_checked), which makes a logits column
+ * non-finite (alodlm_check_finite), which makes a logits column
  * non-finite in every row, computed or not.
  * One workgroup; `workspace` holds alodlm_objective_workspace(rows, S, K) floats.
  * ------------------------------------------------------------------------ */
@@ -522,20 +522,20 @@ int alodlm_scale(void* x, const float* scale, int64_t n, int dtype, void* stream
 int alodlm_scale_add_f32(const float* x, float* y, int64_t n, const float* scale, int accumulate,
                          void* stream);
 /* dst[c][r] = src[r][c] for a row-major rows x cols matrix (dst and src must
- * not overlap).  The step keeps transposed copies of the projection and
- * LM-head weights ([in, out], refreshed at the start of every forward) so
- * that every forward product reads its weight operand in out-contiguous
- * rows; it replaces the weight layout the forward products of
- * alodlm/model.py:52-58,161 read through torch.nn.Linear. */
+ * not overlap).  The step keeps transposed copies of the projection weights
+ * ([in, out], refreshed at the start of every forward): the layers' forward
+ * products run faster with the weight operand in out-contiguous rows (the
+ * LM-head product reads the [out, in] weight itself, faster that way).  It
+ * replaces the weight layout the forward products of alodlm/model.py:52-58
+ * read through torch.nn.Linear. */
 int alodlm_transpose(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
                      void* stream);
-/* The same transpose, storing 1 into *nonfinite (not cleared here) when any
- * element of src is inf or NaN: the step copies the LM-head weight with it,
- * so that the loss can follow the reference's 0 * sum(logits) term
+/* Stores 1 into *flag (never clears it) when any of the n elements of x is inf
+ * or NaN; reads x once.  The step checks the LM-head weight with it, so that
+ * the loss can follow the reference's 0 * sum(logits) term
  * (alodlm/model.py:186) without computing the logits of rows that carry no
  * loss. */
-int alodlm_transpose_checked(const void* src, void* dst, int64_t rows, int64_t cols, int dtype,
-                             int32_t* nonfinite, void* stream);
+int alodlm_check_finite(const void* x, int64_t n, int dtype, int32_t* flag, void* stream);
 
 #ifdef __cplusplus
 }

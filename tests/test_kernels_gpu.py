@@ -161,6 +161,40 @@ def test_transpose(dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,offset", [(1, 0), (1000, 0), (1000, 1), (4096 * 2048 + 5, 0),
+                                      (151936 * 2048, 0)])
+def test_check_finite(dtype, n, offset):
+    """The LM-head finiteness scan: the flag is set by one inf or NaN anywhere
+    (first, last, middle element, the unaligned tail), stays 0 on finite
+    data (the largest finite values included) and is never cleared."""
+    L = lib()
+    log(f"check_finite n={n} offset={offset} {dtype}")
+    code = L.dtype_code(dtype)
+    buf = torch.zeros(n + offset, dtype=dtype, device=DEV)
+    x = buf[offset:]
+    x[::max(1, n // 7)] = torch.finfo(dtype).max
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+
+    def scan():
+        flag.zero_()
+        L.call("alodlm_check_finite", L.ptr(x), n, code, L.ptr(flag), st())
+        torch.cuda.synchronize()
+        return int(flag.item())
+
+    assert scan() == 0
+    for pos in sorted({0, n // 2, n - 1}):
+        for bad in (float("inf"), float("-inf"), float("nan")):
+            x[pos] = bad
+            assert scan() == 1, (pos, bad)
+            x[pos] = 0
+    assert scan() == 0
+    flag.fill_(1)
+    L.call("alodlm_check_finite", L.ptr(x), n, code, L.ptr(flag), st())
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,inter", [(3, 8), (37, 768), (5, 13)])
 def test_swiglu_fwd_bwd(dtype, rows, inter):
     """SwiGLU against torch float64 ([tf] modeling_qwen3.py:81-83 with the
