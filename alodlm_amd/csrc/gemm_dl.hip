@@ -254,8 +254,12 @@ template <int NW> struct Opnd64<false, NW> {
 // writes of 16 rows and the 16-byte reads along a row free of bank conflicts
 // with addresses that are a base plus an immediate), then each thread moves
 // 16-byte chunks, 32 threads per row (and reads the matching 16 bytes of R).
+// SCALE: multiply by alpha; the bf16-output kernels are instantiated with
+// and without it (every product of the step has alpha = 1, and the 256
+// multiplies per wave are a third of the epilogue's VALU work; one kernel
+// holding both epilogues spilled registers).
 constexpr int TILE_ROW = 528, TILE_LDS = TB * TILE_ROW;
-template <int EPI, int NTHR, typename Quad>
+template <int EPI, int NTHR, bool SCALE, typename Quad>
 __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, int64_t ldc,
                                               const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                                               int64_t m0, int64_t n0, float alpha, float* partial,
@@ -289,8 +293,10 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
         int row, col;
         float v[4];
         quad(t, row, col, v);
+        if (SCALE) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] *= alpha;
+          for (int e = 0; e < 4; ++e) v[e] *= alpha;
+        }
         *reinterpret_cast<uint2*>(tile + row * TILE_ROW + col * 2) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
@@ -378,8 +384,10 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
     quad(t, row, col, v);
     const int64_t m = m0 + row, n = n0 + col;
     if (m >= M) continue;
+    if (SCALE) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] *= alpha;
+      for (int e = 0; e < 4; ++e) v[e] *= alpha;
+    }
     if (vec && n + 4 <= N) {
       if (EPI == ALODLM_EPI_STORE) {
         *reinterpret_cast<uint2*>(Cb + m * ldc + n) =
@@ -427,7 +435,7 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
 //  * MFMAs 8..63: the fragments of tile tt+1.  B fragment j is reloaded in
 //    place once its block column is done (at MFMA 8 (j+1)); the last one,
 //    needed until MFMA 63, and the A fragments go to the other register set.
-template <bool AK, bool BK, int EPI, int STAGES>
+template <bool AK, bool BK, int EPI, int STAGES, bool SCALE>
 __global__ void __launch_bounds__(256, 1)
 gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
@@ -574,7 +582,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
   };
-  tile_epilogue<EPI, NW * 64>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
+  tile_epilogue<EPI, NW * 64, SCALE>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
                               first_into_c);
 }
 
@@ -583,7 +591,7 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
 // step 1's fragments; after MFMA 7 of k step 1 the barrier publishes tile tt+1
 // (all loads in flight are its) and frees stage s; the rest of k step 1 reads
 // tile tt+1's k step 0 fragments and issues tile tt+2's loads into stage s.
-template <bool AK, bool BK, int EPI>
+template <bool AK, bool BK, int EPI, bool SCALE>
 __global__ void __launch_bounds__(256, 1)
 gemm_dl2_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                 int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
@@ -721,7 +729,7 @@ gemm_dl2_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restr
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
   };
-  tile_epilogue<EPI, NW * 64>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
+  tile_epilogue<EPI, NW * 64, SCALE>(lds, quad, C, ldc, R, ldr, M, N, m0, n0, alpha, partial,
                               first_into_c);
 }
 
@@ -772,49 +780,66 @@ int64_t gemm_dl_store_splits(int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
-template <bool AK, bool BK>
-static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
+template <bool AK, bool BK, bool SCALE>
+static void launch_scaled(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                           int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
                           int64_t nsplit, int first_into_c, hipStream_t st) {
+  const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
+  dim3 grid((unsigned)tiles, (unsigned)nsplit);
   // both operands k-contiguous: two 64-deep stages (128-byte row pieces per
   // direct load; 3-7 % faster than the 32-deep ring on every such product of
   // the step, and the same results: the k order of every sum is unchanged)
   if constexpr (AK && BK) {
     if (K % 64 == 0 && kps % 64 == 0) {
-      const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
-      dim3 grid((unsigned)tiles, (unsigned)nsplit);
       if (epi == ALODLM_EPI_STORE)
-        gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE><<<grid, 256, 0, st>>>(
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE, SCALE><<<grid, 256, 0, st>>>(
             A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
-      else if (epi == ALODLM_EPI_RESIDUAL)
-        gemm_dl2_kernel<AK, BK, ALODLM_EPI_RESIDUAL><<<grid, 256, 0, st>>>(
+      else if (epi == ALODLM_EPI_RESIDUAL)  // (without the multiply it spills)
+        gemm_dl2_kernel<AK, BK, ALODLM_EPI_RESIDUAL, true><<<grid, 256, 0, st>>>(
             A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
-      else if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
-        gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE_F32><<<grid, 256, 0, st>>>(
-            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
-      else
-        gemm_dl2_kernel<AK, BK, ALODLM_EPI_ACCUM><<<grid, 256, 0, st>>>(
-            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      else if constexpr (SCALE) {
+        if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
+          gemm_dl2_kernel<AK, BK, ALODLM_EPI_STORE_F32, true><<<grid, 256, 0, st>>>(
+              A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+        else
+          gemm_dl2_kernel<AK, BK, ALODLM_EPI_ACCUM, true><<<grid, 256, 0, st>>>(
+              A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+      }
       return;
     }
   }
   // 4 waves, 32-deep k stages in a ring of 4 (128 KB of LDS)
   constexpr int ST = 4;
-  const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
-  dim3 grid((unsigned)tiles, (unsigned)nsplit);
   if (epi == ALODLM_EPI_STORE)
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, ST><<<grid, 256, 0, st>>>(
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, ST, SCALE><<<grid, 256, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
   else if (epi == ALODLM_EPI_RESIDUAL)
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, ST><<<grid, 256, 0, st>>>(
+    gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, ST, SCALE><<<grid, 256, 0, st>>>(
         A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
-  else if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE_F32, ST><<<grid, 256, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+  else if constexpr (SCALE) {
+    if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
+      gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE_F32, ST, true><<<grid, 256, 0, st>>>(
+          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+    else
+      gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, ST, true><<<grid, 256, 0, st>>>(
+          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+  }
+}
+
+template <bool AK, bool BK>
+static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
+                          int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
+                          int64_t K, float alpha, int epi, float* part, int64_t kps,
+                          int64_t nsplit, int first_into_c, hipStream_t st) {
+  // the float-output epilogues keep the multiply: without it the compiler
+  // hoists their loads of C and spills
+  if (alpha == 1.f && (epi == ALODLM_EPI_STORE || epi == ALODLM_EPI_RESIDUAL))
+    launch_scaled<AK, BK, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
+                                 nsplit, first_into_c, st);
   else
-    gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, ST><<<grid, 256, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+    launch_scaled<AK, BK, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
+                                nsplit, first_into_c, st);
 }
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
