@@ -84,6 +84,41 @@ def test_gemm_layouts_and_epilogues(M, N, K, ak, bk, dtype, epi):
     assert err <= tol, f"max rel err {err}"
 
 
+@pytest.mark.parametrize("M,N,K,ak,bk", [
+    (4352, 4160, 64, 0, 1),    # 17 x 17 tiles (more than one per workgroup), ragged edges
+    (4096, 4608, 96, 1, 0),    # 16 x 18 tiles, a multiple of 8 (per-XCD tile chunks)
+    (4160, 4096, 96, 1, 1),
+    (4096, 4352, 64, 1, 1),    # 64-deep kernel
+    (4608, 4096, 32, 0, 0),
+])
+@pytest.mark.parametrize("epi,alpha", [(0, 1.0), (0, 0.5), (1, 1.0), (2, 0.5)])
+def test_gemm_many_tiles(M, N, K, ak, bk, epi, alpha):
+    L = lib()
+    log(f"gemm many tiles M={M} N={N} K={K} ak={ak} bk={bk} epi={epi} alpha={alpha}")
+    g = torch.Generator().manual_seed(M + N + K + epi)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    Ad = (A if ak else A.T.contiguous()).to(DEV)
+    Bd = (B if bk else B.T.contiguous()).to(DEV)
+    ref = (A.float() @ B.float().T).double() * alpha
+    R = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    if epi == 2:
+        C = torch.randn(M, N, generator=g).to(DEV)
+        expected = C.cpu().double() + ref
+        ws = torch.empty(max(L.query("alodlm_gemm_workspace", M, N, K, epi, 1), 1),
+                         dtype=torch.float32, device=DEV)
+    else:
+        C = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+        ws = None
+        expected = ref if epi == 0 else R.double() + ref.to(torch.bfloat16).double()
+    Rd = R.to(DEV)
+    L.call("alodlm_gemm", L.ptr(Ad), K if ak else M, ak, L.ptr(Bd), K if bk else N, bk, L.ptr(C),
+           N, L.ptr(Rd), N, M, N, K, alpha, epi, 1, L.ptr(ws), st())
+    torch.cuda.synchronize()
+    err = (C.cpu().double() - expected).abs().max().item() / (ref.abs().max().item() + 1e-6)
+    assert err <= (1e-5 if epi == 2 else 8e-3), f"max rel err {err}"
+
+
 @pytest.mark.parametrize("M,N", [(512, 512), (300, 260)])
 def test_gemm_store_splitk_long_k(M, N):
     """A bf16-output product with few output tiles and a long K (the LM head's
