@@ -187,10 +187,17 @@ qknorm_rope_bwd_kernel(const T* __restrict__ dq, const T* __restrict__ dk, const
 }
 
 // ---------------------------------------------------------------------------
-// head_dim 128, bf16: four heads per wavefront pass, 16 lanes per head, lane j
-// owning rotary elements i = 4j..4j+3 and i + 64 (8-byte accesses); sums over
-// a head are 16-lane reductions.  Same arithmetic and rounding points as the
-// kernels above.
+// head_dim 128, bf16.  Same arithmetic and rounding points as the kernels
+// above.  The 64 rotation angles of a row are computed once per row, one per
+// lane (lane l: frequency l), and handed to the lanes that use them by
+// shuffles.
+//  * forward: eight heads per wavefront pass, 8 lanes per head, lane j owning
+//    rotary elements i = 8j..8j+7 and i + 64 (16-byte accesses; 71.6 against
+//    85.6 us per 1.7B call with 16 lanes per head and 8-byte accesses);
+//  * backward: four heads per pass, 16 lanes per head, lane j owning
+//    i = 4j..4j+3 and i + 64 (8-byte accesses: the 8-lane form needs 149
+//    VGPRs, 3 wavefronts per SIMD, and ran 139 against 121 us).
+// Sums over a head are 8- or 16-lane reductions.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float sum16(float v) {
 #pragma unroll
@@ -209,41 +216,54 @@ __device__ __forceinline__ void store4(bf16_t* p, const float* v) {
                  pack_bf16x2(v[2], v[3]));
 }
 
+__device__ __forceinline__ float sum8(float v) {
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __global__ void __launch_bounds__(64 * ROPE_WAVES)
 qknorm_rope128_fwd_kernel(const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ wq,
                           const bf16_t* __restrict__ wk, const int64_t* __restrict__ positions,
                           const float* __restrict__ inv_freq, bf16_t* __restrict__ q_out,
                           bf16_t* __restrict__ k_out, int64_t rows, int nq, int nkv, float eps) {
-  const int lane = threadIdx.x & 63, slot = lane >> 4, j = lane & 15;
+  const int lane = threadIdx.x & 63, slot = lane >> 3, j = lane & 7;
   const int64_t row = (int64_t)blockIdx.x * ROPE_WAVES + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int i0 = 4 * j;
+  const int i0 = 8 * j;
   const float pos = (float)positions[row];
-  float cs[4], sn[4], wqa[4], wqb[4], wka[4], wkb[4];
+  // lane l computes the rotation of frequency l; lane j of a head takes
+  // frequencies 8j..8j+7 from lanes 8j..8j+7
+  float cs[8], sn[8], wqa[8], wqb[8], wka[8], wkb[8];
+  {
+    const float ang = pos * inv_freq[lane];
+    const float c1 = round_bf16(cosf(ang)), s1 = round_bf16(sinf(ang));
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float ang = pos * inv_freq[i0 + e];
-    cs[e] = round_bf16(cosf(ang));
-    sn[e] = round_bf16(sinf(ang));
+    for (int e = 0; e < 8; ++e) {
+      cs[e] = __shfl(c1, i0 + e, 64);
+      sn[e] = __shfl(s1, i0 + e, 64);
+    }
   }
-  load4(wq + i0, wqa); load4(wq + i0 + 64, wqb);
-  load4(wk + i0, wka); load4(wk + i0 + 64, wkb);
+  Vec8<bf16_t>::load(wq + i0, wqa); Vec8<bf16_t>::load(wq + i0 + 64, wqb);
+  Vec8<bf16_t>::load(wk + i0, wka); Vec8<bf16_t>::load(wk + i0 + 64, wkb);
   const int heads = nq + nkv;
   const bf16_t* src = qkv + row * (int64_t)(nq + 2 * nkv) * 128;
-  for (int h0 = 0; h0 < heads; h0 += 4) {
+  for (int h0 = 0; h0 < heads; h0 += 8) {
     const int head = h0 + slot;
     const bool live = head < heads;
     const bool is_q = head < nq;
-    float xa[4] = {0.f, 0.f, 0.f, 0.f}, xb[4] = {0.f, 0.f, 0.f, 0.f};
-    if (live) { load4(src + head * 128 + i0, xa); load4(src + head * 128 + i0 + 64, xb); }
+    float xa[8], xb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xa[e] = xb[e] = 0.f;
+    if (live) { Vec8<bf16_t>::load(src + head * 128 + i0, xa); Vec8<bf16_t>::load(src + head * 128 + i0 + 64, xb); }
     float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ss += xa[e] * xa[e] + xb[e] * xb[e];
-    ss = sum16(ss);
+    for (int e = 0; e < 8; ++e) ss += xa[e] * xa[e] + xb[e] * xb[e];
+    ss = sum8(ss);
     const float r = 1.0f / sqrtf(ss / 128.f + eps);
-    float oa[4], ob[4];
+    float oa[8], ob[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 8; ++e) {
       const float a = round_bf16((is_q ? wqa[e] : wka[e]) * round_bf16(xa[e] * r));
       const float b = round_bf16((is_q ? wqb[e] : wkb[e]) * round_bf16(xb[e] * r));
       oa[e] = round_bf16(a * cs[e]) + round_bf16(-b * sn[e]);
@@ -251,8 +271,8 @@ qknorm_rope128_fwd_kernel(const bf16_t* __restrict__ qkv, const bf16_t* __restri
     }
     if (live) {
       bf16_t* dst = is_q ? q_out + (row * nq + head) * 128 : k_out + (row * nkv + head - nq) * 128;
-      store4(dst + i0, oa);
-      store4(dst + i0 + 64, ob);
+      Vec8<bf16_t>::store(dst + i0, oa);
+      Vec8<bf16_t>::store(dst + i0 + 64, ob);
     }
   }
 }
@@ -267,68 +287,74 @@ qknorm_rope128_bwd_kernel(const bf16_t* __restrict__ dq, const bf16_t* __restric
   __shared__ float lds[ROPE_WAVES * 4][2 * 128];  // [wave*4 + slot][dwq | dwk]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane >> 4, j = lane & 15;
   const int i0 = 4 * j;
-  const int heads = nq + nkv;
   const int64_t width = (int64_t)(nq + 2 * nkv) * 128;
-  float wqa[4], wqb[4], wka[4], wkb[4];
-  float gqa[4] = {0.f, 0.f, 0.f, 0.f}, gqb[4] = {0.f, 0.f, 0.f, 0.f};
-  float gka[4] = {0.f, 0.f, 0.f, 0.f}, gkb[4] = {0.f, 0.f, 0.f, 0.f};
-  load4(wq + i0, wqa); load4(wq + i0 + 64, wqb);
-  load4(wk + i0, wka); load4(wk + i0 + 64, wkb);
+  const float freq = inv_freq[lane];
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-  for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += ROPE_WAVES) {
-    const float pos = (float)positions[row];
-    float cs[4], sn[4];
+  float* L = lds[wave * 4 + slot];
+  // the q heads of the block's rows, then the k heads: one weight-gradient
+  // accumulator set per lane at a time
+#pragma unroll 1
+  for (int kind = 0; kind < 2; ++kind) {
+    const int h_beg = kind ? nq : 0, h_end = kind ? nq + nkv : nq;
+    const bf16_t* w = kind ? wk : wq;
+    float wa[4], wb[4], ga[4] = {0.f, 0.f, 0.f, 0.f}, gb[4] = {0.f, 0.f, 0.f, 0.f};
+    load4(w + i0, wa); load4(w + i0 + 64, wb);
+    for (int64_t row = r0 + wave; row < r0 + rows_per_block && row < rows; row += ROPE_WAVES) {
+      // lane l computes the rotation of frequency l; lane j of a head takes
+      // frequencies 4j..4j+3 from lanes 4j..4j+3
+      float cs[4], sn[4];
+      {
+        const float ang = (float)positions[row] * freq;
+        const float c1 = round_bf16(cosf(ang)), s1 = round_bf16(sinf(ang));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cs[e] = __shfl(c1, i0 + e, 64);
+          sn[e] = __shfl(s1, i0 + e, 64);
+        }
+      }
+      for (int h0 = h_beg; h0 < h_end; h0 += 4) {
+        const int head = h0 + slot;
+        const bool live = head < h_end;
+        float xa[4] = {0.f, 0.f, 0.f, 0.f}, xb[4] = {0.f, 0.f, 0.f, 0.f};
+        float go[4] = {0.f, 0.f, 0.f, 0.f}, gh[4] = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+          const bf16_t* x = qkv + row * width + head * 128;
+          const bf16_t* g = kind ? dk + (row * nkv + head - nq) * 128 : dq + (row * nq + head) * 128;
+          load4(x + i0, xa); load4(x + i0 + 64, xb);
+          load4(g + i0, go); load4(g + i0 + 64, gh);
+        }
+        float ta[4], tb[4], ss = 0.f, s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ta[e] = go[e] * cs[e] + gh[e] * sn[e];   // d/d t[i]
+          tb[e] = gh[e] * cs[e] - go[e] * sn[e];   // d/d t[i + half]
+          ss += xa[e] * xa[e] + xb[e] * xb[e];
+          s += ta[e] * wa[e] * xa[e] + tb[e] * wb[e] * xb[e];
+        }
+        ss = sum16(ss);
+        s = sum16(s);
+        const float r = 1.0f / sqrtf(ss / 128.f + eps);
+        const float k = s * r * r * r / 128.f;
+        float oa[4], ob[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ga[e] += ta[e] * round_bf16(xa[e] * r);
+          gb[e] += tb[e] * round_bf16(xb[e] * r);
+          oa[e] = r * ta[e] * wa[e] - xa[e] * k;
+          ob[e] = r * tb[e] * wb[e] - xb[e] * k;
+        }
+        if (live) {
+          bf16_t* out = dqkv + row * width + head * 128;
+          store4(out + i0, oa);
+          store4(out + i0 + 64, ob);
+        }
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float ang = pos * inv_freq[i0 + e];
-      cs[e] = round_bf16(cosf(ang));
-      sn[e] = round_bf16(sinf(ang));
+      L[kind * 128 + i0 + e] = ga[e];
+      L[kind * 128 + i0 + 64 + e] = gb[e];
     }
-    for (int h0 = 0; h0 < heads; h0 += 4) {
-      const int head = h0 + slot;
-      const bool live = head < heads;
-      const bool is_q = head < nq;
-      float xa[4] = {0.f, 0.f, 0.f, 0.f}, xb[4] = {0.f, 0.f, 0.f, 0.f};
-      float go[4] = {0.f, 0.f, 0.f, 0.f}, gh[4] = {0.f, 0.f, 0.f, 0.f};
-      if (live) {
-        const bf16_t* x = qkv + row * width + head * 128;
-        const bf16_t* g = is_q ? dq + (row * nq + head) * 128 : dk + (row * nkv + head - nq) * 128;
-        load4(x + i0, xa); load4(x + i0 + 64, xb);
-        load4(g + i0, go); load4(g + i0 + 64, gh);
-      }
-      float ta[4], tb[4], ss = 0.f, s = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ta[e] = go[e] * cs[e] + gh[e] * sn[e];   // d/d t[i]
-        tb[e] = gh[e] * cs[e] - go[e] * sn[e];   // d/d t[i + half]
-        ss += xa[e] * xa[e] + xb[e] * xb[e];
-        s += ta[e] * (is_q ? wqa[e] : wka[e]) * xa[e] + tb[e] * (is_q ? wqb[e] : wkb[e]) * xb[e];
-      }
-      ss = sum16(ss);
-      s = sum16(s);
-      const float r = 1.0f / sqrtf(ss / 128.f + eps);
-      const float k = s * r * r * r / 128.f;
-      float oa[4], ob[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float na = round_bf16(xa[e] * r), nb = round_bf16(xb[e] * r);
-        if (is_q) { gqa[e] += ta[e] * na; gqb[e] += tb[e] * nb; }
-        else { gka[e] += ta[e] * na; gkb[e] += tb[e] * nb; }
-        oa[e] = r * ta[e] * (is_q ? wqa[e] : wka[e]) - xa[e] * k;
-        ob[e] = r * tb[e] * (is_q ? wqb[e] : wkb[e]) - xb[e] * k;
-      }
-      if (live) {
-        bf16_t* out = dqkv + row * width + head * 128;
-        store4(out + i0, oa);
-        store4(out + i0 + 64, ob);
-      }
-    }
-  }
-  float* L = lds[wave * 4 + slot];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    L[i0 + e] = gqa[e]; L[i0 + 64 + e] = gqb[e];
-    L[128 + i0 + e] = gka[e]; L[128 + i0 + 64 + e] = gkb[e];
   }
   __syncthreads();
   {
@@ -340,10 +366,15 @@ qknorm_rope128_bwd_kernel(const bf16_t* __restrict__ dq, const bf16_t* __restric
   }
 }
 
-// The head_dim-128 kernels make 8-byte accesses.
+// The head_dim-128 backward makes 8-byte accesses, the forward 16-byte ones.
 static bool rope128_aligned(const void* a, const void* b, const void* c) {
   return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
            reinterpret_cast<uintptr_t>(c)) & 7) == 0;
+}
+
+static bool rope128_aligned16(const void* a, const void* b, const void* c) {
+  return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+           reinterpret_cast<uintptr_t>(c)) & 15) == 0;
 }
 
 static int check_rope(int64_t rows, int64_t nq, int64_t nkv, int64_t dh) {
@@ -361,7 +392,8 @@ extern "C" int alodlm_qknorm_rope_fwd(const void* qkv, const void* wq, const voi
   if (rc) return rc;
   if (rows == 0) return ALODLM_OK;
   ALODLM_DISPATCH(dtype, T, {
-    if (std::is_same<T, bf16_t>::value && dh == 128 && rope128_aligned(qkv, q_out, k_out)) {
+    if (std::is_same<T, bf16_t>::value && dh == 128 && rope128_aligned16(qkv, q_out, k_out) &&
+        rope128_aligned16(wq, wk, wk)) {
       qknorm_rope128_fwd_kernel<<<ceil_div_u(rows, ROPE_WAVES), 64 * ROPE_WAVES, 0,
                                   as_stream(stream)>>>(
           (const bf16_t*)qkv, (const bf16_t*)wq, (const bf16_t*)wk, positions, inv_freq,
