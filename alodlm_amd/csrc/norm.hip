@@ -75,8 +75,67 @@ rmsnorm_fwd_vec_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __re
     if (c < cols) Vec8<T>::load(w + c, wv[t]);
   }
   const int64_t stride = (int64_t)gridDim.x * NORM_WAVES;
-  for (int64_t row = (int64_t)blockIdx.x * NORM_WAVES + (threadIdx.x >> 6); row < rows;
-       row += stride) {
+  int64_t row = (int64_t)blockIdx.x * NORM_WAVES + (threadIdx.x >> 6);
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    // bf16 rows: the next row's loads are issued before this row is reduced
+    // (kept packed until used), so each wavefront has two rows in flight
+    // (49.6 -> 46.8 us per 1.7B call, 20.2 -> 19.7 us at 8B)
+    uint4 nx[NCH], wr[NCH];  // the weight stays packed as well
+#pragma unroll
+    for (int t = 0; t < NCH; ++t) {
+      const int64_t c = (int64_t)lane * 8 + 512 * t;
+      if (c < cols) wr[t] = *reinterpret_cast<const uint4*>(w + c);
+    }
+    auto fetch = [&](int64_t rr) {
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        const int64_t c = (int64_t)lane * 8 + 512 * t;
+        if (c < cols) nx[t] = *reinterpret_cast<const uint4*>(x + rr * cols + c);
+      }
+    };
+    if (row < rows) fetch(row);
+    for (; row < rows; row += stride) {
+      uint4 cur[NCH];
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        cur[t] = nx[t];
+        // unpacked per row (the empty asm hides the weight's origin, so the
+        // floats are not kept alive across the loop)
+        asm volatile("" : "+v"(wr[t].x), "+v"(wr[t].y), "+v"(wr[t].z), "+v"(wr[t].w));
+      }
+      if (row + stride < rows) fetch(row + stride);
+      float v[NCH][8];
+      float ss = 0.f;
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        const int64_t c = (int64_t)lane * 8 + 512 * t;
+        if (c < cols) {
+          const uint32_t wd[4] = {cur[t].x, cur[t].y, cur[t].z, cur[t].w};
+          Vec8<bf16_t>::unpack(wd, v[t]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss += v[t][i] * v[t][i];
+        }
+      }
+      ss = wave_sum(ss);
+      const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+      if (lane == 0 && rstd) rstd[row] = r;
+      T* yr = y + row * cols;
+#pragma unroll
+      for (int t = 0; t < NCH; ++t) {
+        const int64_t c = (int64_t)lane * 8 + 512 * t;
+        if (c < cols) {
+          float wf[8];
+          const uint32_t ww[4] = {wr[t].x, wr[t].y, wr[t].z, wr[t].w};
+          Vec8<bf16_t>::unpack(ww, wf);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[t][i] = wf[i] * Elem<T>::round(v[t][i] * r);
+          Vec8<T>::store(yr + c, v[t]);
+        }
+      }
+    }
+    return;
+  }
+  for (; row < rows; row += stride) {
     const T* xr = x + row * cols;
     float v[NCH][8];
     float ss = 0.f;
