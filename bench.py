@@ -23,7 +23,7 @@ the same line (``sub_records``; --no-sub-records skips them):
                 (masks Bernoulli(t), t ~ U(0, 1) per 2048-row sequence);
                 forward + backward
 
-Prints one JSON line (metric of BASELINE: train tokens/s) with:
+Prints one JSON line (metric: train tokens/s of the headline step) with:
   roofline      the dominant kernel class (by time, from HIP events around its
                 launches on the launch stream, over a few steps after the
                 timed ones so that those carry no per-launch events):

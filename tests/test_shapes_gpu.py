@@ -417,8 +417,8 @@ def test_1p7b_layer_shapes_match_reference_bf16_run():
     score the same rows.  Against the reference's bf16 run: every live
     masked cross-entropy within two bf16 steps; the denoising and
     autoregressive terms within 1e-3; halting probabilities within 5e-2
-    (mean 5e-3).  The loss and the gradients are held to north_star's bounds
-    (loss 1e-2, gradient-sample cosine 0.999, norms 3 %) or, where the
+    (mean 5e-3).  The loss and the gradients are held to the step's parity
+    bounds (loss 1e-2, gradient-sample cosine 0.999, norms 3 %) or, where the
     reference's own bf16 run misses them against its float32 run (the actor
     term: bf16 cross-entropies times sums of log q), to twice that gap:
     measured on the fixture, the reference's loss moves 1.3e-2 and its gate
