@@ -20,9 +20,22 @@ __global__ void embed_gather_kernel(const T* __restrict__ table, const int64_t* 
 template <typename T, int W>
 __global__ void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ act, int64_t rows,
                                   int64_t I) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
-  if (i >= rows * I) return;
-  const int64_t r = i / I, c = i % I;
+  // W == 8: 8-column groups along grid x, one row per grid y (blocks are
+  // dispatched x first, so the streams stay sequential; the flat grid's
+  // 64-bit division for the row and column was 170 of 466 instructions:
+  // 206.7 -> 187.8 us per 1.7B call); W == 1: a flat grid
+  int64_t r, c;
+  if (W == 8) {
+    r = blockIdx.y;
+    c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (c >= I) return;
+  } else {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * I) return;
+    r = i / I;
+    c = i % I;
+  }
+  const int64_t i = r * I + c;
   float g[8], u[8], a[8];
   // the streams are far larger than the caches and used once here: non-temporal
   if (W == 8) {
@@ -46,9 +59,18 @@ template <typename T, int W>
 __global__ void swiglu_bwd_kernel(const T* __restrict__ dact, const T* __restrict__ gu,
                                   T* __restrict__ dgu, T* __restrict__ act, int64_t rows,
                                   int64_t I) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * W;
-  if (i >= rows * I) return;
-  const int64_t r = i / I, c = i % I;
+  int64_t r, c;  // the grid of swiglu_fwd_kernel
+  if (W == 8) {
+    r = blockIdx.y;
+    c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (c >= I) return;
+  } else {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * I) return;
+    r = i / I;
+    c = i % I;
+  }
+  const int64_t i = r * I + c;
   float g[8], u[8], da[8], dg[8], du[8], a[8];
   if (W == 8) {
     Vec8<T>::load_nt(gu + r * 2 * I + c, g);
@@ -222,8 +244,13 @@ extern "C" int alodlm_swiglu_fwd(const void* gu, void* act, int64_t rows, int64_
   const bool v8 = inter % 8 == 0 && aligned8(gu, dtype) && aligned8(act, dtype);
   ALODLM_DISPATCH(dtype, T, {
     if (v8)
-      swiglu_fwd_kernel<T, 8><<<ceil_div_u(rows * inter / 8, 256), 256, 0, as_stream(stream)>>>(
-          (const T*)gu, (T*)act, rows, inter);
+      // one row per grid y: launches of at most 65535 rows
+      for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const int64_t n = rows - r0 < 65535 ? rows - r0 : 65535;
+        swiglu_fwd_kernel<T, 8><<<dim3(ceil_div_u(inter / 8, 256), (unsigned)n), 256, 0,
+                                  as_stream(stream)>>>((const T*)gu + r0 * 2 * inter,
+                                                       (T*)act + r0 * inter, n, inter);
+      }
     else
       swiglu_fwd_kernel<T, 1><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
           (const T*)gu, (T*)act, rows, inter);
@@ -239,8 +266,13 @@ extern "C" int alodlm_swiglu_bwd(const void* dact, const void* gu, void* dgu, vo
                   aligned8(dgu, dtype) && (act == nullptr || aligned8(act, dtype));
   ALODLM_DISPATCH(dtype, T, {
     if (v8)
-      swiglu_bwd_kernel<T, 8><<<ceil_div_u(rows * inter / 8, 256), 256, 0, as_stream(stream)>>>(
-          (const T*)dact, (const T*)gu, (T*)dgu, (T*)act, rows, inter);
+      for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const int64_t n = rows - r0 < 65535 ? rows - r0 : 65535;
+        swiglu_bwd_kernel<T, 8><<<dim3(ceil_div_u(inter / 8, 256), (unsigned)n), 256, 0,
+                                  as_stream(stream)>>>(
+            (const T*)dact + r0 * inter, (const T*)gu + r0 * 2 * inter,
+            (T*)dgu + r0 * 2 * inter, act ? (T*)act + r0 * inter : nullptr, n, inter);
+      }
     else
       swiglu_bwd_kernel<T, 1><<<ceil_div_u(rows * inter, 256), 256, 0, as_stream(stream)>>>(
           (const T*)dact, (const T*)gu, (T*)dgu, (T*)act, rows, inter);

@@ -230,7 +230,10 @@ def test_check_finite(dtype, n, offset):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,inter", [(3, 8), (37, 768), (5, 13)])
+@pytest.mark.parametrize("rows,inter", [(3, 8), (37, 768), (5, 13),
+                                        # two column blocks per row, the second ragged;
+                                        # more rows than one launch takes (65535)
+                                        (300, 2056), (70001, 16)])
 def test_swiglu_fwd_bwd(dtype, rows, inter):
     """SwiGLU against torch float64 ([tf] modeling_qwen3.py:81-83 with the
     reference's roundings); the product written by the backward is
