@@ -901,16 +901,18 @@ fa128_dkdv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 }
 
 // dK / dV of every key from the group's float32 partials, summed in head
-// order (deterministic).  8 consecutive head_dim values per thread.
+// order (deterministic).  8 consecutive head_dim values per thread; grid x:
+// column blocks of a row, y: rows r0 + y, z: dK / dV (no 64-bit division).
 __global__ void __launch_bounds__(256)
 fa128_dkdv_reduce_kernel(const float* __restrict__ partial, int group, int64_t N, int nkv,
-                         bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv) {
+                         bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int64_t lddv,
+                         int64_t r0) {
   const int64_t width = (int64_t)nkv * HD;
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  if (i >= 2 * N * width) return;
-  const int which = i >= N * width;  // 0: dK, 1: dV
-  const int64_t e = which ? i - N * width : i;
-  const int64_t row = e / width, c = e % width;
+  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (c >= width) return;
+  const int which = blockIdx.z;  // 0: dK, 1: dV
+  const int64_t row = r0 + blockIdx.y;
+  const int64_t e = row * width + c;
   const float* src = partial + (int64_t)which * group * N * width + e;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int g = 0; g < group; ++g) {
@@ -929,19 +931,19 @@ fa128_dkdv_reduce_kernel(const float* __restrict__ partial, int group, int64_t N
 
 // delta[h, r] = sum_e dO[r, h, e] O[r, h, e] and lse2[h, r] = lse[h, r] log2(e)
 // (what the dK/dV pass reads when it runs first), and the dK/dV work counter
-// zeroed.  16 lanes per (head, row), 8 head_dim values each; items are
-// row-major so that a workgroup reads whole rows of dO and O.
+// zeroed.  16 lanes per (head, row), 8 head_dim values each; a workgroup
+// takes 16 heads of one row (grid x: head groups, grid y: rows r0 + y), so it
+// reads contiguous pieces of the rows of dO and O, and the row and head need
+// no 64-bit division (which took 150 of the flat grid's 275 instructions).
 __global__ void __launch_bounds__(256)
 fa128_bwd_prep_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ dout,
                       const float* __restrict__ lse, float* __restrict__ delta, int64_t N, int nq,
-                      int* __restrict__ counter) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0;
-  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (item >= N * nq) return;
+                      int* __restrict__ counter, int64_t r0) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *counter = 0;
+  const int h = (int)blockIdx.x * 16 + (int)(threadIdx.x >> 4);
+  if (h >= nq) return;
   const int sub = threadIdx.x & 15;
-  // row-major items: a workgroup reads whole rows (all heads), contiguous
-  const int64_t r = item / nq;
-  const int h = (int)(item - r * nq);
+  const int64_t r = r0 + blockIdx.y;
   const int64_t off = r * nq * HD + (int64_t)h * HD + sub * 8;
   float a[8], b[8];
   Vec8<bf16_t>::load(o + off, a);
@@ -1233,8 +1235,11 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
   if (stored) {
     // delta, lse * log2(e) and the zeroed work counter for the dK/dV pass,
     // which stores dS for the dQ pass (stream order)
-    fa128_bwd_prep_kernel<<<ceil_div_u(N * nq, 16), 256, 0, st>>>(o, dout, lse, delta, N, nq,
-                                                                   counter);
+    for (int64_t r0 = 0; r0 < N; r0 += 65535) {  // at most 65535 rows per launch
+      const int64_t n = N - r0 < 65535 ? N - r0 : 65535;
+      fa128_bwd_prep_kernel<<<dim3(ceil_div_u(nq, 16), (unsigned)n), 256, 0, st>>>(
+          o, dout, lse, delta, N, nq, counter, r0);
+    }
   } else {
     // the dQ pass writes delta and lse * log2(e), which the dK/dV pass reads
     // (stream order), and zeroes the dK/dV work counter
@@ -1249,9 +1254,16 @@ int fa128_bwd_launch(const bf16_t* q, const bf16_t* k, const bf16_t* v, int64_t 
   fa128_dkdv_kernel<<<grid, 256, 0, st>>>(q, k, v, ldv, lse2, delta, dout, bounds, tiles,
                                           (int)n_tiles, dk, dv, lddv, partial, N, nq, nkv, B,
                                           scale, counter, ds, ds_base, (int)ds_blocks);
-  if (split)
-    fa128_dkdv_reduce_kernel<<<ceil_div_u(2 * N * nkv * HD / 8, 256), 256, 0, st>>>(
-        partial, nq / nkv, N, nkv, dk, dv, lddv);
+  if (split) {
+    // a block covers one row's nkv * 16 column groups (at most 256 threads)
+    const int64_t per_row = (int64_t)nkv * HD / 8;
+    const unsigned threads = (unsigned)(per_row < 256 ? per_row : 256);
+    for (int64_t r0 = 0; r0 < N; r0 += 65535) {  // at most 65535 rows per launch
+      const int64_t n = N - r0 < 65535 ? N - r0 : 65535;
+      fa128_dkdv_reduce_kernel<<<dim3(ceil_div_u(per_row, threads), (unsigned)n, 2), threads, 0,
+                                 st>>>(partial, nq / nkv, N, nkv, dk, dv, lddv, r0);
+    }
+  }
   if (stored)
     fa128_dq_ds_kernel<<<dim3((unsigned)nq, (unsigned)n_tiles), 256, 0, st>>>(
         k, ds, ds_base, ds_blocks, bounds, tiles, dq, N, nq, nkv, scale);
