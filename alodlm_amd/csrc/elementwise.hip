@@ -124,33 +124,45 @@ transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, i
 }
 
 // The same transpose for 2-byte elements with rows and cols multiples of 8
-// and 16-byte aligned rows: 64x64 tiles moved in 16-byte pieces (8 threads
-// per tile row on the way in, 8 per transposed row on the way out).
+// and 16-byte aligned rows: 64x64 tiles moved in 16-byte pieces.  On the
+// way in, 8 threads per tile row; on the way out each thread reads 8 tile
+// rows x 2 columns as 32-bit words and writes two transposed 16-byte pieces
+// (half the LDS reads of one column per thread).  Word w of tile row r sits
+// at w ^ 8 * ((r / 16) % 4): the 64 lanes of a read (8 row groups x 8 word
+// columns) then fall in 64 distinct banks, and the 16-byte pieces written on
+// the way in stay contiguous.
 __global__ void __launch_bounds__(256)
 transpose16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int64_t rows,
                    int64_t cols) {
-  __shared__ uint16_t tile[64][64 + 8];
+  __shared__ uint32_t tile[64][32];  // [row][word] (2 elements per word)
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int t = threadIdx.x, part = (t & 7) * 8;
+  const int t = threadIdx.x;
+  auto sw = [](int r) { return 8 * ((r >> 4) & 3); };
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
-    const int rr = (t >> 3) + 32 * pass;
+    const int rr = (t >> 3) + 32 * pass, part = (t & 7) * 8;
     const int64_t r = r0 + rr, c = c0 + part;
     if (r < rows && c < cols)
-      *reinterpret_cast<uint4*>(&tile[rr][part]) = *reinterpret_cast<const uint4*>(src + r * cols + c);
+      *reinterpret_cast<uint4*>(&tile[rr][(part / 2) ^ sw(rr)]) =
+          *reinterpret_cast<const uint4*>(src + r * cols + c);
   }
   __syncthreads();
+  const int part = (t & 7) * 8;  // 8 tile rows part .. part + 7
+  const int cc = (t >> 3) * 2;   // tile columns cc, cc + 1
+  const int64_t r = r0 + part, c = c0 + cc;
+  if (r < rows && c < cols) {
+    uint32_t v[8];
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const int cc = (t >> 3) + 32 * pass;
-    const int64_t c = c0 + cc, r = r0 + part;
-    if (r < rows && c < cols) {
-      uint32_t w[4];
+    for (int k = 0; k < 8; ++k) v[k] = tile[part + k][(cc / 2) ^ sw(part + k)];
+    uint32_t lo[4], hi[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = (uint32_t)tile[part + 2 * e][cc] | ((uint32_t)tile[part + 2 * e + 1][cc] << 16);
-      *reinterpret_cast<uint4*>(dst + c * rows + r) = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = (v[2 * e] & 0xffffu) | (v[2 * e + 1] << 16);          // column cc
+      hi[e] = (v[2 * e] >> 16) | (v[2 * e + 1] & 0xffff0000u);      // column cc + 1
     }
+    *reinterpret_cast<uint4*>(dst + c * rows + r) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    if (c + 1 < cols)
+      *reinterpret_cast<uint4*>(dst + (c + 1) * rows + r) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
   }
 }
 
