@@ -204,7 +204,21 @@ template <typename T>
 __global__ void scale_any_kernel(T* __restrict__ x, const float* __restrict__ s, int64_t n) {
   const float k = s[0];
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+  int64_t head = 0;
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0 && 16 % sizeof(T) == 0) {
+    // 16 bytes per thread and step (8 or 4 elements); the tail below
+    constexpr int PER = 16 / sizeof(T);
+    head = n / PER * PER;
+    for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * PER; i < head;
+         i += stride * PER) {
+      T e[PER];
+      *reinterpret_cast<uint4*>(e) = *reinterpret_cast<const uint4*>(x + i);
+#pragma unroll
+      for (int q = 0; q < PER; ++q) Elem<T>::store(e, q, Elem<T>::load(e, q) * k);
+      *reinterpret_cast<uint4*>(x + i) = *reinterpret_cast<const uint4*>(e);
+    }
+  }
+  for (int64_t i = head + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     Elem<T>::store(x, i, Elem<T>::load(x, i) * k);
 }
 

@@ -176,6 +176,44 @@ __global__ void scatter_rows_kernel(const T* __restrict__ src, const int32_t* __
   dst[(int64_t)sel[j] * H + c] = src[i];
 }
 
+// The same row moves in 16-byte units (rows of a whole number of units,
+// 16-byte aligned buffers): grid x covers a row's U units, grid y rows
+// j0 + y; SCATTER: dst row sel[j] <- src row j, else dst row j <- src row
+// sel[j].
+template <bool SCATTER>
+__global__ void move_rows16_kernel(const uint4* __restrict__ src, const int32_t* __restrict__ sel,
+                                   int64_t j0, uint4* __restrict__ dst, int64_t U) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= U) return;
+  const int64_t j = j0 + blockIdx.y;
+  const int64_t other = sel[j];
+  if (SCATTER) dst[other * U + u] = src[j * U + u];
+  else dst[j * U + u] = src[other * U + u];
+}
+
+__global__ void zero16_kernel(uint4* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// rows of 16-byte units: launches of at most 65535 rows
+template <bool SCATTER>
+static void move_rows16(const void* src, const int32_t* sel, int64_t n, void* dst, int64_t U,
+                        hipStream_t st) {
+  const unsigned threads = (unsigned)(U < 256 ? (U + 63) / 64 * 64 : 256);
+  for (int64_t j0 = 0; j0 < n; j0 += 65535) {
+    const int64_t m = n - j0 < 65535 ? n - j0 : 65535;
+    move_rows16_kernel<SCATTER><<<dim3(ceil_div_u(U, threads), (unsigned)m), threads, 0, st>>>(
+        (const uint4*)src, sel, j0, (uint4*)dst, U);
+  }
+}
+
+static bool rows16(const void* a, const void* b, int64_t row_bytes) {
+  return row_bytes % 16 == 0 &&
+         ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+}
+
 #define CE_LOG2E 1.4426950408889634f
 
 // ce = lse - logit[target] (rounded like the reference's CE output),
@@ -552,8 +590,12 @@ extern "C" int alodlm_gather_rows(const void* src, const int32_t* sel_rows, int6
                                   void* dst, int64_t hidden, int dtype, void* stream) {
   if (n_sel == 0) return ALODLM_OK;
   ALODLM_DISPATCH(dtype, T, {
-    gather_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
-        (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
+    const int64_t row_bytes = hidden * (int64_t)sizeof(T);
+    if (rows16(src, dst, row_bytes))
+      move_rows16<false>(src, sel_rows, n_sel, dst, row_bytes / 16, as_stream(stream));
+    else
+      gather_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
+          (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
   });
   ALODLM_CHECK_LAUNCH("gather_rows");
   return ALODLM_OK;
@@ -563,11 +605,20 @@ extern "C" int alodlm_scatter_rows(const void* src, const int32_t* sel_rows, int
                                    void* dst, int64_t rows, int64_t hidden, int dtype,
                                    void* stream) {
   ALODLM_DISPATCH(dtype, T, {
-    zero_kernel<T><<<ceil_div_u(rows * hidden, 256), 256, 0, as_stream(stream)>>>((T*)dst,
-                                                                                  rows * hidden);
-    if (n_sel > 0)
-      scatter_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
-          (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
+    const int64_t row_bytes = hidden * (int64_t)sizeof(T);
+    if (rows16(src, dst, row_bytes)) {
+      const int64_t units = rows * row_bytes / 16;
+      const int64_t blocks = (units + 255) / 256;
+      zero16_kernel<<<(unsigned)(blocks < 8192 ? blocks : 8192), 256, 0, as_stream(stream)>>>(
+          (uint4*)dst, units);
+      if (n_sel > 0) move_rows16<true>(src, sel_rows, n_sel, dst, row_bytes / 16, as_stream(stream));
+    } else {
+      zero_kernel<T><<<ceil_div_u(rows * hidden, 256), 256, 0, as_stream(stream)>>>(
+          (T*)dst, rows * hidden);
+      if (n_sel > 0)
+        scatter_rows_kernel<T><<<ceil_div_u(n_sel * hidden, 256), 256, 0, as_stream(stream)>>>(
+            (const T*)src, sel_rows, n_sel, (T*)dst, hidden);
+    }
   });
   ALODLM_CHECK_LAUNCH("scatter_rows");
   return ALODLM_OK;

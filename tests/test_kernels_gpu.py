@@ -230,6 +230,52 @@ def test_check_finite(dtype, n, offset):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,offset", [(1, 0), (13, 0), (1000, 1), (4096 * 2048 + 5, 0),
+                                      (4096 * 2048 + 5, 3)])
+def test_scale_in_place(dtype, n, offset):
+    """x *= s[0] in place, rounded to the storage type once, on 16-byte pieces
+    and the element tail (and a start that is not 16-byte aligned)."""
+    L = lib()
+    log(f"scale n={n} offset={offset} {dtype}")
+    g = torch.Generator().manual_seed(n + offset)
+    x = torch.randn(n + offset, generator=g).to(dtype)
+    k = torch.tensor([0.37], dtype=torch.float32)
+    xd, kd = x.to(DEV), k.to(DEV)
+    L.call("alodlm_scale", L.ptr(xd[offset:]), L.ptr(kd), n, L.dtype_code(dtype), st())
+    torch.cuda.synchronize()
+    expected = x.clone()
+    expected[offset:] = (x[offset:].float() * k[0]).to(dtype)
+    assert torch.equal(xd.cpu(), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,H,n_sel", [(300, 2048, 123), (50, 13, 20), (70000, 8, 66000),
+                                          (40, 151936, 7)])
+def test_gather_scatter_rows(dtype, rows, H, n_sel):
+    """Row gather (dst[j] = src[sel[j]]) and scatter (dst zeroed, then
+    dst[sel[j]] = src[j]) against torch indexing: 16-byte row moves, the
+    element path (rows of 13), more selected rows than one launch takes."""
+    L = lib()
+    log(f"gather/scatter rows={rows} H={H} n_sel={n_sel} {dtype}")
+    g = torch.Generator().manual_seed(rows + H)
+    src = torch.randn(rows, H, generator=g).to(dtype)
+    sel = torch.randperm(rows, generator=g)[:n_sel].sort().values.to(torch.int32)
+    src_d, sel_d = src.to(DEV), sel.to(DEV)
+    code = L.dtype_code(dtype)
+    out = torch.empty(n_sel, H, dtype=dtype, device=DEV)
+    L.call("alodlm_gather_rows", L.ptr(src_d), L.ptr(sel_d), n_sel, L.ptr(out), H, code, st())
+    back = torch.full((rows, H), 7.0, dtype=dtype, device=DEV)
+    L.call("alodlm_scatter_rows", L.ptr(out), L.ptr(sel_d), n_sel, L.ptr(back), rows, H, code,
+           st())
+    torch.cuda.synchronize()
+    idx = sel.long()
+    assert torch.equal(out.cpu(), src[idx])
+    expected = torch.zeros(rows, H, dtype=dtype)
+    expected[idx] = src[idx]
+    assert torch.equal(back.cpu(), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,inter", [(3, 8), (37, 768), (5, 13),
                                         # two column blocks per row, the second ragged;
                                         # more rows than one launch takes (65535)
