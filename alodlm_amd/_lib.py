@@ -49,6 +49,7 @@ SIGNATURES = {
     "alodlm_rotary_bwd": [P, P, P, P, I64, I64, I64, I32, P],
     "alodlm_gemm_workspace": [I64, I64, I64, I32, I32],
     "alodlm_gemm": [P, I64, I32, P, I64, I32, P, I64, P, I64, I64, I64, I64, F32, I32, I32, P, P],
+    "alodlm_gemm_segk": [P, P, I32, I64, I64, I64, P, I64, I64, I64, F32, I32, P, P],
     "alodlm_attention_fwd": [P, P, P, I64, P, P, P, I64, P, P, I64, I64, I64, I64, I64, I32, P],
     "alodlm_attention_ds_blocks": [P, I64, I64, P],
     "alodlm_attention_bwd_workspace": [I64, I64, I64, I64, I64, I64],

@@ -12,6 +12,7 @@
 //
 // float path and unaligned shapes: a plain LDS-tiled FMA kernel.
 #include "common.h"
+#include "gemm_dl.h"
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
@@ -373,14 +374,6 @@ void gemm_big_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B
                      int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
                      int64_t* nsplit_out, hipStream_t st);
 
-bool gemm_dl_eligible(int64_t lda, int a_kmajor, int64_t ldb, int b_kmajor, int64_t M, int64_t N,
-                      int64_t K);
-int64_t gemm_dl_splits(int64_t M, int64_t N, int64_t K);
-int64_t gemm_dl_store_splits(int64_t M, int64_t N, int64_t K);
-void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
-                    int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
-                    int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
-                    int64_t* nsplit_out, int first_into_c, hipStream_t st);
 
 // The 256x256 kernel takes the products whose output fills at least one tile.
 // The 256x256 kernel needs whole 64-deep k tiles for k-contiguous operands.
@@ -523,5 +516,48 @@ extern "C" int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void*
           (const T*)A, sam, sak, (const T*)B, sbn, sbk, C, ldc, (const T*)R, ldr, M, N, K, alpha);
   });
   ALODLM_CHECK_LAUNCH("gemm_simple");
+  return ALODLM_OK;
+}
+
+extern "C" int alodlm_gemm_segk(const void* const* a_segs, const void* const* b_segs, int nseg,
+                                int64_t seg_k, int64_t lda, int64_t ldb, void* C, int64_t ldc,
+                                int64_t M, int64_t N, float alpha, int epilogue, float* workspace,
+                                void* stream) {
+  ALODLM_CHECK_ARG(nseg >= 1 && nseg <= KSEGS_MAX, "gemm_segk: 1 to 8 segments");
+  ALODLM_CHECK_ARG(epilogue == ALODLM_EPI_ACCUM || epilogue == ALODLM_EPI_STORE_F32,
+                   "gemm_segk: float32 output epilogues only");
+  ALODLM_CHECK_ARG(M >= 0 && N >= 0 && seg_k > 0 && seg_k % 32 == 0,
+                   "gemm_segk: segments must hold a positive multiple of 32 k rows");
+  if (M == 0 || N == 0) return ALODLM_OK;
+  const int64_t K = seg_k * nseg;
+  ALODLM_CHECK_ARG(gemm_dl_eligible(lda, 0, ldb, 0, M, N, K),
+                   "gemm_segk: M and N must be >= 256 and multiples of 8, lda/ldb multiples of 8");
+  KSegs segs{};
+  for (int i = 0; i < KSEGS_MAX; ++i) {
+    const int s = i < nseg ? i : nseg - 1;
+    ALODLM_CHECK_ARG(a_segs[s] != nullptr && b_segs[s] != nullptr, "gemm_segk: null segment");
+    ALODLM_CHECK_ARG(mfma_eligible(a_segs[s], lda, 0, b_segs[s], ldb, 0, M, N, seg_k),
+                     "gemm_segk: segment bases must be 16-byte aligned");
+    segs.a[i] = (const bf16_t*)a_segs[s];
+    segs.b[i] = (const bf16_t*)b_segs[s];
+  }
+  segs.k = seg_k;
+  hipStream_t st = as_stream(stream);
+  int64_t splits = gemm_dl_splits(M, N, K);
+  if (splits > 1 && workspace == nullptr) splits = 1;
+  if (splits > 1) {
+    const int64_t kps = (((K + splits - 1) / splits) + 31) / 32 * 32;
+    if ((K + kps - 1) / kps < 2) splits = 1;
+  }
+  const int first_into_c = epilogue == ALODLM_EPI_ACCUM;
+  int64_t nsplit = 1;
+  gemm_dl_launch(segs.a[0], lda, 0, segs.b[0], ldb, 0, C, ldc, nullptr, 0, M, N, K, alpha,
+                 epilogue, workspace, splits, &nsplit, first_into_c, st, &segs);
+  ALODLM_CHECK_LAUNCH("gemm_bf16_dl_segk");
+  if (nsplit > 1) {
+    if (first_into_c) splitk_reduce(workspace + M * N, nsplit - 1, M, N, (float*)C, ldc, st);
+    else splitk_reduce(workspace, nsplit, M, N, (float*)C, ldc, st, true);
+    ALODLM_CHECK_LAUNCH("gemm_splitk_reduce");
+  }
   return ALODLM_OK;
 }

@@ -44,6 +44,7 @@
 // the tile sequence is dealt out in contiguous chunks per XCD, then swept in
 // groups of 3 tile rows (down a group, then across).
 #include "common.h"
+#include "gemm_dl.h"
 #include "lds_dma.h"
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
@@ -435,12 +436,20 @@ __device__ __forceinline__ void tile_epilogue(char* tile, Quad quad, void* C, in
 //  * MFMAs 8..63: the fragments of tile tt+1.  B fragment j is reloaded in
 //    place once its block column is done (at MFMA 8 (j+1)); the last one,
 //    needed until MFMA 63, and the A fragments go to the other register set.
-template <bool AK, bool BK, int EPI, int STAGES, bool SCALE>
+// Base of segment i (a select chain: no dynamic indexing of the argument).
+__device__ __forceinline__ const bf16_t* seg_base(const bf16_t* const (&p)[KSEGS_MAX], int i) {
+  const bf16_t* r = p[0];
+#pragma unroll
+  for (int j = 1; j < KSEGS_MAX; ++j) r = i == j ? p[j] : r;
+  return r;
+}
+
+template <bool AK, bool BK, int EPI, int STAGES, bool SCALE, bool SEGK = false>
 __global__ void __launch_bounds__(256, 1)
 gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restrict__ B,
                int64_t ldb, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                int64_t N, int64_t K, float alpha, int64_t k_per_split, float* __restrict__ partial,
-               int first_into_c) {
+               int first_into_c, KSegs segs) {
   constexpr int NW = 4, WM = 128, WN = 128;
   constexpr int FI = WM / 16, FJ = WN / 16;
   constexpr int WAVES_N = TB / WN;
@@ -490,13 +499,36 @@ gemm_dl_kernel(const bf16_t* __restrict__ A, int64_t lda, const bf16_t* __restri
   constexpr int VM_LOOP = (STAGES - 3) * PL + (PL < 2 ? PL : 2);
   constexpr int VM_PRO = (STAGES - 2) * PL;
 
-  const char* pa = oa.origin(A, m0, kbeg);
-  const char* pb = ob.origin(B, n0, kbeg);
+  const bf16_t* A0 = A;
+  const bf16_t* B0 = B;
+  int64_t k0 = kbeg;
+  int seg = 0, left = 0;  // segment of the next load and its tiles left (SEGK)
+  if constexpr (SEGK) {
+    seg = (int)(kbeg / segs.k);
+    k0 = kbeg - (int64_t)seg * segs.k;
+    A0 = seg_base(segs.a, seg);
+    B0 = seg_base(segs.b, seg);
+    left = (int)((segs.k - k0) / KD);
+  }
+  const char* pa = oa.origin(A0, m0, k0);
+  const char* pb = ob.origin(B0, n0, k0);
   int tl = 0;
   auto advance = [&]() {
     if (tl + 1 < ntiles) {
-      pa += oa.step;
-      pb += ob.step;
+      if constexpr (SEGK) {
+        if (--left == 0) {  // the next tile opens the next segment
+          ++seg;
+          pa = oa.origin(seg_base(segs.a, seg), m0, 0);
+          pb = ob.origin(seg_base(segs.b, seg), n0, 0);
+          left = (int)(segs.k / KD);
+        } else {
+          pa += oa.step;
+          pb += ob.step;
+        }
+      } else {
+        pa += oa.step;
+        pb += ob.step;
+      }
     }
     ++tl;
   };
@@ -784,9 +816,21 @@ template <bool AK, bool BK, bool SCALE>
 static void launch_scaled(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                           int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
-                          int64_t nsplit, int first_into_c, hipStream_t st) {
+                          int64_t nsplit, int first_into_c, const KSegs* segs, hipStream_t st) {
   const int64_t tiles = ((M + TB - 1) / TB) * ((N + TB - 1) / TB);
   dim3 grid((unsigned)tiles, (unsigned)nsplit);
+  // K over separate segments: the dW layout with float outputs only
+  if constexpr (!AK && !BK && SCALE) {
+    if (segs != nullptr) {
+      if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
+        gemm_dl_kernel<false, false, ALODLM_EPI_STORE_F32, 4, true, true><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, *segs);
+      else
+        gemm_dl_kernel<false, false, ALODLM_EPI_ACCUM, 4, true, true><<<grid, 256, 0, st>>>(
+            A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, *segs);
+      return;
+    }
+  }
   // both operands k-contiguous: two 64-deep stages (128-byte row pieces per
   // direct load; 3-7 % faster than the 32-deep ring on every such product of
   // the step, and the same results: the k order of every sum is unchanged)
@@ -813,17 +857,17 @@ static void launch_scaled(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t
   constexpr int ST = 4;
   if (epi == ALODLM_EPI_STORE)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE, ST, SCALE><<<grid, 256, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, KSegs{});
   else if (epi == ALODLM_EPI_RESIDUAL)
     gemm_dl_kernel<AK, BK, ALODLM_EPI_RESIDUAL, ST, SCALE><<<grid, 256, 0, st>>>(
-        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+        A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, KSegs{});
   else if constexpr (SCALE) {
     if (epi == ALODLM_EPI_STORE_F32 && part == nullptr)
       gemm_dl_kernel<AK, BK, ALODLM_EPI_STORE_F32, ST, true><<<grid, 256, 0, st>>>(
-          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, KSegs{});
     else
       gemm_dl_kernel<AK, BK, ALODLM_EPI_ACCUM, ST, true><<<grid, 256, 0, st>>>(
-          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c);
+          A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, kps, part, first_into_c, KSegs{});
   }
 }
 
@@ -831,15 +875,15 @@ template <bool AK, bool BK>
 static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, void* C,
                           int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M, int64_t N,
                           int64_t K, float alpha, int epi, float* part, int64_t kps,
-                          int64_t nsplit, int first_into_c, hipStream_t st) {
+                          int64_t nsplit, int first_into_c, const KSegs* segs, hipStream_t st) {
   // the float-output epilogues keep the multiply: without it the compiler
   // hoists their loads of C and spills
   if (alpha == 1.f && (epi == ALODLM_EPI_STORE || epi == ALODLM_EPI_RESIDUAL))
     launch_scaled<AK, BK, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
-                                 nsplit, first_into_c, st);
+                                 nsplit, first_into_c, segs, st);
   else
     launch_scaled<AK, BK, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, part, kps,
-                                nsplit, first_into_c, st);
+                                nsplit, first_into_c, segs, st);
 }
 
 // Launch the direct-load kernel; `part` (splits*M*N floats) is used when
@@ -850,14 +894,14 @@ static void launch_layout(const bf16_t* A, int64_t lda, const bf16_t* B, int64_t
 void gemm_dl_launch(const bf16_t* A, int64_t lda, int a_kmajor, const bf16_t* B, int64_t ldb,
                     int b_kmajor, void* C, int64_t ldc, const bf16_t* R, int64_t ldr, int64_t M,
                     int64_t N, int64_t K, float alpha, int epi, float* part, int64_t splits,
-                    int64_t* nsplit_out, int first_into_c, hipStream_t st) {
+                    int64_t* nsplit_out, int first_into_c, hipStream_t st, const KSegs* segs) {
   int64_t kps = K;
   if (splits > 1) kps = (((K + splits - 1) / splits) + KMIN - 1) / KMIN * KMIN;
   const int64_t nsplit = (K + kps - 1) / kps;
   *nsplit_out = nsplit;
   float* p = ((epi == ALODLM_EPI_ACCUM || epi == ALODLM_EPI_STORE_F32) && nsplit > 1) ? part : nullptr;
-  if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
-  else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
-  else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
-  else launch_layout<false, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, st);
+  if (a_kmajor && b_kmajor) launch_layout<true, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, segs, st);
+  else if (a_kmajor) launch_layout<true, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, segs, st);
+  else if (b_kmajor) launch_layout<false, true>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, segs, st);
+  else launch_layout<false, false>(A, lda, B, ldb, C, ldc, R, ldr, M, N, K, alpha, epi, p, kps, nsplit, first_into_c, segs, st);
 }

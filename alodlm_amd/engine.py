@@ -34,6 +34,7 @@ the same pack shape and the caching allocator reuses its blocks.
 """
 
 from dataclasses import dataclass
+import ctypes
 import math
 
 import torch
@@ -268,6 +269,11 @@ class StepEngine(Kernels):
         self.fused_optimizer = None
         self.grads_pending = False
         self._written = None
+        # weight-gradient products of the looped layers held until each
+        # layer's last backward application (_flush_dw); group_dw forces the
+        # choice (None: decided per backward by memory, _decide_group_dw)
+        self.group_dw = None
+        self._dw_pending = None
         # the readout's persistent buffers (_readout_buffers)
         self._readout = None
 
@@ -333,15 +339,77 @@ class StepEngine(Kernels):
         return self.layer_fwd(self.layers[li], x, b.kernel_mask, self._rope, save,
                               keep=self._keep_now if save is not None else (False, False), tag=li)
 
-    def _layer_bwd(self, dy, saved, b, g):
+    def _layer_bwd(self, dy, saved, b, g, last=True):
         li = saved[0]
         # a layer's first backward application writes its matrices' gradients
         # (the arena is not zeroed there); later ones accumulate
         first = self._written is not None and li not in self._written
         if first:
             self._written.add(li)
-        return self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li], b.kernel_mask,
-                              self._rope, first=first)
+        if self._dw_pending is None:
+            return self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li],
+                                  b.kernel_mask, self._rope, first=first)
+        entries = []
+        dx = self.layer_bwd(dy, saved, self.layers[li], self.grad_layers[li], b.kernel_mask,
+                            self._rope, first=first, defer=entries)
+        self._dw_pending.setdefault(li, []).append(entries)
+        if last:
+            self._flush_dw(li)
+        return dx
+
+    def _flush_dw(self, li):
+        """The projection weight gradients of layer ``li`` over all its
+        backward applications so far (alodlm/model.py:152: autograd sums the
+        passes' gradients): per matrix one product whose k runs through the
+        applications' rows in the order they were taken
+        (alodlm_gemm_segk), written when the arena holds no earlier
+        contribution of this backward, else added."""
+        passes = self._dw_pending.pop(li)
+        epi = EPI_ACCUM if self._written is None else EPI_STORE_F32
+        for j in range(len(passes[0])):
+            segs = [p[j] for p in passes]
+            A, lda, B, ldb, C, ldc, M, Nc = segs[0]
+            rows = A.shape[0]
+            if len(segs) == 1 or not self._segk_eligible(segs, rows):
+                for n, (A, lda, B, ldb, C, ldc, M, Nc) in enumerate(segs):
+                    self._gemm(A, lda, 0, B, ldb, 0, C, ldc, M, Nc, A.shape[0],
+                               epi=epi if n == 0 else EPI_ACCUM)
+                continue
+            a_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[0]) for e in segs])
+            b_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[2]) for e in segs])
+            K = rows * len(segs)
+            need = query("alodlm_gemm_workspace", M, Nc, K, epi, self.code)
+            ws = self._workspace(need) if need else None
+            call("alodlm_gemm_segk", ctypes.addressof(a_ptrs), ctypes.addressof(b_ptrs),
+                 len(segs), rows, lda, ldb, ptr(C), ldc, M, Nc, 1.0, epi, ptr(ws),
+                 self._stream())
+
+    def _segk_eligible(self, segs, rows):
+        A, lda, B, ldb, C, ldc, M, Nc = segs[0]
+        return (len(segs) <= 8 and self.dtype == torch.bfloat16 and rows % 32 == 0
+                and M >= 256 and Nc >= 256 and M % 8 == 0 and Nc % 8 == 0
+                and lda % 8 == 0 and ldb % 8 == 0
+                and all(e[0].shape[0] == rows and e[2].shape[0] == rows
+                        and ptr(e[0]) % 16 == 0 and ptr(e[2]) % 16 == 0 for e in segs))
+
+    def _decide_group_dw(self, N, looped):
+        """Whether this backward holds the looped layers' weight-gradient
+        operands until their last application (one product per matrix over
+        all passes instead of one per pass): only if those operands of
+        max_depth - 1 passes fit in half of what this process can still
+        allocate."""
+        if self.group_dw is not None:
+            return bool(self.group_dw)
+        K, d = self.cfg.max_depth, self.dims
+        if K < 2 or K > 8 or self.dtype != torch.bfloat16 or N % 32 or not looped:
+            return False
+        QD = d.heads * d.head_dim
+        per_pass = N * (4 * d.hidden + 3 * d.intermediate + QD + d.qkv_width) * 2
+        need = (K - 1) * looped * per_pass
+        dev = self.device
+        free, _ = torch.cuda.mem_get_info(dev)
+        cached = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+        return need < 0.5 * (free + cached)
 
     # ------------------------------------------------------------------ shared pieces
     def _carry(self, core_out, b, exits, depth):
@@ -618,23 +686,31 @@ class StepEngine(Kernels):
         scale = self._upstream(grad_scale, state["dgate"])
         self._lm_grad_store(state, scale, grads, accumulate)
         plan_original = self.embed_plan(b.original) if K > 1 else None
+        # the looped layers' weight gradients: one product per matrix over the
+        # passes, at each layer's last application (depth 0), when it fits
+        looped = len(state["depths"][0]["coda_saves"]) + len(state["depths"][0]["core_saves"])
+        self._dw_pending = {} if self._decide_group_dw(N, looped) else None
         dnext = None  # gradient at the core input of depth+1
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
             dr = self._readout_bwd(rec, depth, state["dgate"][depth], scale, g_norm, g_gw, g_gb,
                                    g_db)
             for saved in reversed(rec["coda_saves"]):
-                dr = self._layer_bwd(dr, saved, b, grads)
+                dr = self._layer_bwd(dr, saved, b, grads, last=depth == 0)
             if dnext is not None:
                 # x_in(depth+1) = exits <= depth+1 ? E[original] : norm(core_out(depth))
                 dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], plan_original,
                                      exits, depth + 1, dr, g_norm, g_embed)
             for saved in reversed(rec["core_saves"]):
-                dr = self._layer_bwd(dr, saved, b, grads)
+                dr = self._layer_bwd(dr, saved, b, grads, last=depth == 0)
             dnext = dr
         dx = dnext
         for saved in reversed(state["prelude"]):
             dx = self._layer_bwd(dx, saved, b, grads)
+        if self._dw_pending is not None:
+            for li in list(self._dw_pending):
+                self._flush_dw(li)
+            self._dw_pending = None
         self.embed_scatter(dx, self.embed_plan(b.ids), g_embed)
         self._written = None
         return grads

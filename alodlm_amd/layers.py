@@ -433,14 +433,23 @@ class Kernels:
             save.append((tag, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2))
         return y
 
-    def layer_bwd(self, dy, saved, w, gw, mask, rope, first=False):
+    def layer_bwd(self, dy, saved, w, gw, mask, rope, first=False, defer=None):
         """Backward of ``layer_fwd`` from its saved tuple: returns dx and adds
         the weight gradients into the float32 views ``gw`` (``first``: the four
         projection matrices' gradients are written instead of added; the norm
-        weights' are always added)."""
+        weights' are always added).  With a list ``defer`` the four projection
+        products are not run: their operands (A, lda, B, ldb, C, ldc, M, N;
+        k = the rows) are appended to it in the order down, gate/up, O, QKV,
+        and the tensors stay alive through the list."""
         _, x, rstd1, qkv, o, lse, x1, rstd2, gu, q, k, h1, h2 = saved
         d, N, st, c = self.dims, x.shape[0], self._stream(), self.code
         wepi = EPI_STORE_F32 if first else EPI_ACCUM
+
+        def dw(A, lda, B, ldb, C, ldc, M, Nc):  # C (+)= A^T B over the N rows
+            if defer is None:
+                self._gemm(A, lda, 0, B, ldb, 0, C, ldc, M, Nc, N, epi=wepi)
+            else:
+                defer.append((A, lda, B, ldb, C, ldc, M, Nc))
         H, W, I = d.hidden, d.qkv_width, d.intermediate
         QD = d.heads * d.head_dim
         # ---- MLP: y = x1 + act . Wd^T  (the SwiGLU backward also rewrites act)
@@ -450,14 +459,14 @@ class Kernels:
         dgu = self._empty(N, 2 * I)
         call("alodlm_swiglu_bwd", ptr(dact), ptr(gu), ptr(dgu), ptr(act), N, I, c, st)
         del dact
-        self._gemm(dy, H, 0, act, I, 0, gw.wd, I, H, I, N, epi=wepi)
+        dw(dy, H, act, I, gw.wd, I, H, I)
         del act
         if h2 is None:
             h2 = self._empty(N, H)
             call("alodlm_rmsnorm_fwd", ptr(x1), ptr(w.ln2), ptr(h2), None, N, H, d.eps, c, st)
         dh2 = self._empty(N, H)
         self._gemm(dgu, 2 * I, 1, w.wgu, H, 0, dh2, H, N, H, 2 * I)
-        self._gemm(dgu, 2 * I, 0, h2, H, 0, gw.wgu, H, 2 * I, H, N, epi=wepi)
+        dw(dgu, 2 * I, h2, H, gw.wgu, H, 2 * I, H)
         del dgu, h2
         dx1 = self._empty(N, H)
         ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))
@@ -467,7 +476,7 @@ class Kernels:
         # ---- attention: x1 = x + o . Wo^T
         do = self._empty(N, QD)
         self._gemm(dx1, H, 1, w.wo, QD, 0, do, QD, N, QD, H)
-        self._gemm(dx1, H, 0, o, QD, 0, gw.wo, QD, H, QD, N, epi=wepi)
+        dw(dx1, H, o, QD, gw.wo, QD, H, QD)
         if q is None:
             q = self._empty(N, QD)
             k = self._empty(N, d.kv_heads * d.head_dim)
@@ -486,7 +495,7 @@ class Kernels:
             call("alodlm_rmsnorm_fwd", ptr(x), ptr(w.ln1), ptr(h1), None, N, H, d.eps, c, st)
         dh1 = self._empty(N, H)
         self._gemm(dqkv, W, 1, w.wqkv, H, 0, dh1, H, N, H, W)
-        self._gemm(dqkv, W, 0, h1, H, 0, gw.wqkv, H, W, H, N, epi=wepi)
+        dw(dqkv, W, h1, H, gw.wqkv, H, W, H)
         del dqkv, h1
         dx = self._empty(N, H)
         ws = self._workspace(query("alodlm_rmsnorm_bwd_workspace", N, H))

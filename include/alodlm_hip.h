@@ -204,6 +204,19 @@ int alodlm_gemm(const void* A, int64_t lda, int a_kmajor, const void* B, int64_t
                 int b_kmajor, void* C, int64_t ldc, const void* R, int64_t ldr, int64_t M,
                 int64_t N, int64_t K, float alpha, int epilogue, int dtype, float* workspace,
                 void* stream);
+/* The weight gradient of a layer applied once per recurrent pass
+ * (alodlm/model.py:152, the loop over depths, whose autograd sums the passes'
+ * nn.Linear weight gradients) as one product:
+ *   C[m, n] (=|+=) alpha * sum_i sum_k A_i[k*lda + m] * B_i[k*ldb + n]
+ * over nseg (1..8) segments of seg_k k rows each (a multiple of 32), A_i =
+ * a_segs[i], B_i = b_segs[i] (bf16, m/n-contiguous like alodlm_gemm with
+ * a_kmajor = b_kmajor = 0, 16-byte aligned), C float32; epilogue
+ * ALODLM_EPI_STORE_F32 or ALODLM_EPI_ACCUM.  M, N >= 256 and multiples of 8.
+ * workspace: alodlm_gemm_workspace(M, N, nseg * seg_k, epilogue, bf16)
+ * floats, or NULL.  One float32 sum runs through the segments in order. */
+int alodlm_gemm_segk(const void* const* a_segs, const void* const* b_segs, int nseg,
+                     int64_t seg_k, int64_t lda, int64_t ldb, void* C, int64_t ldc, int64_t M,
+                     int64_t N, float alpha, int epilogue, float* workspace, void* stream);
 
 /* ---------------------------------------------------------------------------
  * GQA attention under the dual-stream training mask (alodlm/model.py:62-73
