@@ -375,14 +375,18 @@ class StepEngine(Kernels):
                     self._gemm(A, lda, 0, B, ldb, 0, C, ldc, M, Nc, A.shape[0],
                                epi=epi if n == 0 else EPI_ACCUM)
                 continue
-            a_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[0]) for e in segs])
-            b_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[2]) for e in segs])
-            K = rows * len(segs)
-            need = query("alodlm_gemm_workspace", M, Nc, K, epi, self.code)
-            ws = self._workspace(need) if need else None
-            call("alodlm_gemm_segk", ctypes.addressof(a_ptrs), ctypes.addressof(b_ptrs),
-                 len(segs), rows, lda, ldb, ptr(C), ldc, M, Nc, 1.0, epi, ptr(ws),
-                 self._stream())
+            self._gemm_segk(segs, rows, epi)
+
+    def _gemm_segk(self, segs, rows, epi):
+        """C (+)= sum_i A_i^T B_i over the segments' ``rows`` rows each
+        (alodlm_gemm_segk); ``segs`` holds _layer_bwd's deferred operands."""
+        A, lda, B, ldb, C, ldc, M, Nc = segs[0]
+        a_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[0]) for e in segs])
+        b_ptrs = (ctypes.c_void_p * len(segs))(*[ptr(e[2]) for e in segs])
+        need = query("alodlm_gemm_workspace", M, Nc, rows * len(segs), epi, self.code)
+        ws = self._workspace(need) if need else None
+        call("alodlm_gemm_segk", ctypes.addressof(a_ptrs), ctypes.addressof(b_ptrs), len(segs),
+             rows, lda, ldb, ptr(C), ldc, M, Nc, 1.0, epi, ptr(ws), self._stream())
 
     def _segk_eligible(self, segs, rows):
         A, lda, B, ldb, C, ldc, M, Nc = segs[0]
@@ -773,6 +777,9 @@ class StepEngine(Kernels):
         g_embed, g_norm, _, g_gw, g_gb, g_db = self._grad_views(grads)
         exits = state["exits"]
         plan_original = self.embed_plan(b.original) if K > 1 else None
+        first = state["depths"][0]
+        self._dw_pending = ({} if self._decide_group_dw(first["core_out"].shape[0],
+                                                        len(first["core_saves"])) else None)
         dnext = None
         for depth in reversed(range(K)):
             rec = state["depths"][depth]
@@ -787,8 +794,12 @@ class StepEngine(Kernels):
                 dr = self._carry_bwd(dnext, rec["core_out"], rec["carry_rstd"], plan_original,
                                      exits, depth + 1, dr, g_norm, g_embed)
             for saved in reversed(rec["core_saves"]):
-                dr = self._layer_bwd(dr, saved, b, grads)
+                dr = self._layer_bwd(dr, saved, b, grads, last=depth == 0)
             dnext = dr
+        if self._dw_pending is not None:
+            for li in list(self._dw_pending):
+                self._flush_dw(li)
+            self._dw_pending = None
         return dnext, grads
 
     def readout_forward(self, finals, batch, need_grad=True, exit_uniforms=None, generator=None):

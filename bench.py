@@ -126,7 +126,7 @@ class KernelTimer:
         timer = self
         gemm, fwd, bwd = engine._gemm, engine._attention_fwd, engine._attention_bwd
 
-        def timed(kind, fn, flops_fn):
+        def timed(kind, fn, flops_fn, bytes_fn=None):
             def run(*args, **kwargs):
                 start = torch.cuda.Event(enable_timing=True)
                 end = torch.cuda.Event(enable_timing=True)
@@ -134,12 +134,21 @@ class KernelTimer:
                 out = fn(*args, **kwargs)
                 end.record()
                 timer.records.setdefault(kind, []).append((start, end, flops_fn(*args, **kwargs)))
-                if kind == "gemm_bf16":
-                    timer.gemm_bytes += gemm_bytes(*args, **kwargs)
+                if bytes_fn is not None:
+                    timer.gemm_bytes += bytes_fn(*args, **kwargs)
                 return out
             return run
 
-        engine._gemm = timed("gemm_bf16", gemm, lambda *a, **k: 2.0 * a[8] * a[9] * a[10])
+        def segk_flops(segs, rows, epi):  # a looped layer's grouped weight gradient
+            return 2.0 * segs[0][6] * segs[0][7] * rows * len(segs)
+
+        def segk_bytes(segs, rows, epi):
+            A, lda, B, ldb, C, ldc, M, N = segs[0]
+            return gemm_bytes(A, lda, 0, B, ldb, 0, C, ldc, M, N, rows * len(segs), epi=epi)
+
+        engine._gemm = timed("gemm_bf16", gemm, lambda *a, **k: 2.0 * a[8] * a[9] * a[10],
+                             gemm_bytes)
+        engine._gemm_segk = timed("gemm_bf16", engine._gemm_segk, segk_flops, segk_bytes)
         engine._attention_fwd = timed("attention_fwd", fwd, engine._attention_fwd_flops)
         engine._attention_bwd = timed("attention_bwd", bwd, engine._attention_bwd_flops)
 
